@@ -1,0 +1,357 @@
+"""Bench for the MI355X backend of manifesto's data-parallel hot path.
+
+Headline (BASELINE.json metric, configs[1]): FP8 e4m3 -> bf16 dequantisation of
+a [4096, 14336] byte tensor with a per-tensor f32 scale of 0.0125, reported as
+achieved HBM GB/s (algorithmic bytes / kernel time) and as a fraction of the
+MI355X's 8 TB/s.  One step = one kernel launch over one resident batch.  Buffer
+sets are rotated so the footprint exceeds the 256 MB Infinity Cache, and the
+timed steps are replayed from a captured HIP graph so the clock sees kernel
+time, not Python launch overhead.  The other BASELINE configs (axpy, SwiGLU,
+the f16 gelu chain, Int4) are measured the same way and listed under
+"configs".  The CPU baseline is the oracle (a C restatement of the Go loops,
+-O2 -ffp-contract=off) timed on this host, single-threaded.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only N]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBS = 8000.0
+METRIC = "achieved HBM GB/s (% of MI355X peak) for fused elementwise + FP8/Int4 dequant"
+MALL_BYTES = 256 << 20
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Workload:
+    cfg = 0
+    name = ""
+    dtype = "f32"
+
+    def __init__(self, torch, M, O):
+        self.torch, self.M, self.O = torch, M, O
+        self.sets = []
+
+    @property
+    def stream(self):
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def rotations(self):
+        return max(2, -(-2 * MALL_BYTES // self.bytes_per_step))
+
+    def setup(self):
+        for _ in range(self.rotations()):
+            self.sets.append(self.make_set())
+
+    def step(self, i):
+        self.launch(self.sets[i % len(self.sets)])
+
+
+def _rand_u8(torch, n, gen):
+    return torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=gen)
+
+
+class Axpy(Workload):
+    cfg, name, dtype = 1, "axpy f32 y=0.75*x+y, N=2^24, x,y~U[-1,1]", "f32"
+    n = 1 << 24
+    bytes_per_step = 12 * n
+    kernel = "k_axpy_f32"
+
+    def make_set(self):
+        t = self.torch
+        g = t.Generator(device="cuda").manual_seed(1 + len(self.sets))
+        x = t.rand(self.n, device="cuda", generator=g) * 2 - 1
+        y = t.rand(self.n, device="cuda", generator=g) * 2 - 1
+        return x, y
+
+    def launch(self, s):
+        x, y = s
+        self.M.axpy(y.data_ptr(), x.data_ptr(), self.n, 0.75, self.M.FLOAT32, self.stream)
+
+    def cpu_sample(self):
+        rng = np.random.default_rng(1)
+        x = rng.uniform(-1, 1, self.n).astype(np.float32)
+        y = rng.uniform(-1, 1, self.n).astype(np.float32)
+        O = self.O
+        return self.n, lambda: O.lib().orc_axpy_f32(y.ctypes.data, x.ctypes.data, self.n, 0.75), \
+            "the full N=2^24 f32 axpy (runtime/axpy.go:115-117 loop)"
+
+
+class Fp8(Workload):
+    cfg, name, dtype = 2, "fp8_e4m3 -> bf16 dequant [4096,14336], per-tensor scale 0.0125", "f32"
+    n = 4096 * 14336
+    bytes_per_step = 3 * n + 4
+    kernel = "k_dequant_fp8<bf16>"
+
+    def make_set(self):
+        t = self.torch
+        g = t.Generator(device="cuda").manual_seed(2 + len(self.sets))
+        return _rand_u8(t, self.n, g), t.empty(self.n, dtype=t.int16, device="cuda")
+
+    def launch(self, s):
+        src, out = s
+        M = self.M
+        M.dequant_fp8(out.data_ptr(), M.BFLOAT16, src.data_ptr(), M.F8E4M3, self.n, 0.0125, self.stream)
+
+    def cpu_sample(self):
+        rng = np.random.default_rng(2)
+        codes = rng.integers(0, 256, self.n, dtype=np.uint8)
+        out = np.empty(self.n, dtype=np.uint16)
+        O = self.O
+        return self.n, lambda: O.lib().orc_dequant_fp8(codes.ctypes.data, self.n, O.F8E4M3, 0.0125,
+                                                       O.BFLOAT16, out.ctypes.data), \
+            "the full [4096,14336] tensor: BytesToFloat32 pass + scale + RNE narrowing pass"
+
+
+class SwiGLU(Workload):
+    cfg, name, dtype = 3, "fused silu(gate)*up, bf16 [8192,14336] ~N(0,1) -> bf16", "f32"
+    n = 8192 * 14336
+    bytes_per_step = 6 * n
+    kernel = "fused_swiglu"
+
+    def setup(self):
+        O = self.O
+        self.nodes = O.flatten((O.N_MUL, (O.N_SILU, ("in", 0)), ("in", 1)))
+        self.k = self.M.FusedKernel(self.nodes, [(self.M.BFLOAT16, 0, 0)] * 2, self.M.BFLOAT16, "swiglu")
+        super().setup()
+
+    def make_set(self):
+        t = self.torch
+        g = t.Generator(device="cuda").manual_seed(3 + len(self.sets))
+        gate = t.randn(self.n, device="cuda", generator=g).to(t.bfloat16)
+        up = t.randn(self.n, device="cuda", generator=g).to(t.bfloat16)
+        return gate, up, t.empty(self.n, dtype=t.bfloat16, device="cuda")
+
+    def launch(self, s):
+        gate, up, out = s
+        self.k.launch([gate.data_ptr(), up.data_ptr()], out.data_ptr(), self.n, self.stream)
+
+    def cpu_sample(self):
+        O = self.O
+        m = 1 << 22
+        rng = np.random.default_rng(3)
+        g = O.f32_to_bf16(rng.standard_normal(m, dtype=np.float32))
+        u = O.f32_to_bf16(rng.standard_normal(m, dtype=np.float32))
+        nodes = self.nodes
+
+        def run():  # shape.cast to f32, CPUKernel.Run, narrow to bf16
+            out = O.run(nodes, [O.decode(g, O.BFLOAT16), O.decode(u, O.BFLOAT16)], m)
+            O.f32_to_bf16(out)
+        return m, run, "2^22 elements of the same chain: bf16->f32 casts, CPUKernel.Run, f32->bf16"
+
+
+class GeluChain(Workload):
+    cfg, name, dtype = 4, "fused gelu_tanh((x+bias)*s)+residual, f16 [4,4096,4096], bias[4096], s=1.1", "f32"
+    n = 4 * 4096 * 4096
+    bytes_per_step = 6 * n + 4096 * 2
+    kernel = "fused_gelu_chain"
+
+    def setup(self):
+        O, M = self.O, self.M
+        self.nodes = O.flatten((O.N_ADD, (O.N_GELU, (O.N_MUL, (O.N_ADD, ("in", 0), ("in", 1)), ("in", 2))),
+                                ("in", 3)))
+        ops = [(M.FLOAT16, M.OPERAND_FULL, 0), (M.FLOAT16, M.OPERAND_PERIODIC, 4096),
+               (M.FLOAT32, M.OPERAND_SCALAR, 0), (M.FLOAT16, M.OPERAND_FULL, 0)]
+        self.k = M.FusedKernel(self.nodes, ops, M.FLOAT16, "gelu_chain")
+        super().setup()
+
+    def make_set(self):
+        t = self.torch
+        g = t.Generator(device="cuda").manual_seed(4 + len(self.sets))
+        x = t.randn(self.n, device="cuda", generator=g).to(t.float16)
+        res = t.randn(self.n, device="cuda", generator=g).to(t.float16)
+        bias = (t.randn(4096, device="cuda", generator=g) * 0.02).to(t.float16)
+        s = t.tensor([1.1], dtype=t.float32, device="cuda")
+        return x, bias, s, res, t.empty(self.n, dtype=t.float16, device="cuda")
+
+    def launch(self, st):
+        x, bias, s, res, out = st
+        self.k.launch([x.data_ptr(), bias.data_ptr(), s.data_ptr(), res.data_ptr()], out.data_ptr(),
+                      self.n, self.stream)
+
+    def cpu_sample(self):
+        O = self.O
+        m = 1 << 22
+        rng = np.random.default_rng(4)
+        x = O.f32_to_f16(rng.standard_normal(m, dtype=np.float32))
+        r = O.f32_to_f16(rng.standard_normal(m, dtype=np.float32))
+        b = O.decode(O.f32_to_f16(rng.normal(0, 0.02, 4096).astype(np.float32)), O.FLOAT16)
+        s = np.array([1.1], np.float32)
+        nodes = self.nodes
+
+        def run():
+            out = O.run(nodes, [O.decode(x, O.FLOAT16), b, s, O.decode(r, O.FLOAT16)], m, [0, 4096, 1, 0])
+            O.f32_to_f16(out)
+        return m, run, "2^22 elements of the same chain: f16->f32 casts, CPUKernel.Run, f32->f16"
+
+
+class Int4(Workload):
+    cfg, name, dtype = 5, "int4 -> bf16 dequant [14336,4096], f16 scale per 128", "f32"
+    n = 14336 * 4096
+    bytes_per_step = n // 2 + (n // 128) * 2 + 2 * n
+    kernel = "k_dequant_int4<bf16,f16>"
+
+    def make_set(self):
+        t = self.torch
+        g = t.Generator(device="cuda").manual_seed(5 + len(self.sets))
+        packed = _rand_u8(t, self.n // 2, g)
+        scales = (t.rand(self.n // 128, device="cuda", generator=g) * 0.015 + 0.005).to(t.float16)
+        return packed, scales, t.empty(self.n, dtype=t.int16, device="cuda")
+
+    def launch(self, s):
+        packed, scales, out = s
+        M = self.M
+        M.dequant_int4(out.data_ptr(), M.BFLOAT16, packed.data_ptr(), self.n, scales.data_ptr(), M.FLOAT16,
+                       128, self.stream)
+
+    def cpu_sample(self):
+        O = self.O
+        rng = np.random.default_rng(5)
+        packed = rng.integers(0, 256, self.n // 2, dtype=np.uint8)
+        scales = O.f32_to_f16(rng.uniform(0.005, 0.02, self.n // 128).astype(np.float32))
+        out = np.empty(self.n, dtype=np.uint16)
+        return self.n, lambda: O.lib().orc_dequant_int4(packed.ctypes.data, self.n, scales.ctypes.data,
+                                                        O.FLOAT16, 128, O.BFLOAT16, out.ctypes.data), \
+            "the full [14336,4096] tensor: f64 nibble decode pass + scale + RNE narrowing pass"
+
+
+WORKLOADS = [Axpy, Fp8, SwiGLU, GeluChain, Int4]
+
+
+def time_gpu(w, steps, warmup, use_graph=True):
+    torch = w.torch
+    for i in range(max(warmup, len(w.sets))):
+        w.step(i)
+    torch.cuda.synchronize()
+    reps = len(w.sets)
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        with torch.cuda.stream(cap):
+            with torch.cuda.graph(graph, stream=cap):
+                for i in range(reps):
+                    w.step(i)
+        torch.cuda.synchronize()
+        replays = max(1, -(-steps // reps))
+        graph.replay()  # warm
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s = torch.cuda.current_stream()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record(s)
+        for _ in range(replays):
+            graph.replay()
+        end.record(s)
+        end.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        n = replays * reps
+    else:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s = torch.cuda.current_stream()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record(s)
+        for i in range(steps):
+            w.step(i)
+        end.record(s)
+        end.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        n = steps
+    ms = start.elapsed_time(end) / n
+    return ms, n, wall
+
+
+def time_cpu(w, budget_s=3.0):
+    m, fn, what = w.cpu_sample()
+    fn()  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    sec = el / reps
+    per_elem = w.bytes_per_step / w.n
+    return {"value": round(m * per_elem / sec / 1e9, 3), "unit": "GB/s",
+            "elements_per_s": round(m / sec, 1), "cores": 1, "kind": "port",
+            "sample": f"{what}; {reps} repetition(s), {el:.1f} s; GOMAXPROCS-equivalent 1 (serial loops)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--only", type=int, default=0, help="measure only this BASELINE config")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards with no exchange step; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import manifesto_amd as M
+    import oracle as O
+    M.init(0)
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {props.name} ({props.multi_processor_count} CUs)")
+
+    results = {}
+    for cls in WORKLOADS:
+        if args.only and cls.cfg != args.only and cls.cfg != 2:
+            continue
+        w = cls(torch, M, O)
+        w.setup()
+        ms, n, wall = time_gpu(w, args.steps, args.warmup, use_graph=not args.no_graph)
+        gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
+        r = {"config": cls.cfg, "workload": w.name, "kernel": w.kernel, "ms_per_step": round(ms, 5),
+             "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+             "elements_per_s": round(w.n / (ms * 1e-3), 1), "bytes_per_step": w.bytes_per_step,
+             "steps_timed": n, "rotated_sets": len(w.sets), "wall_s": round(wall, 4)}
+        if not args.no_cpu:
+            r["cpu_baseline"] = time_cpu(w)
+            r["speedup_vs_cpu"] = round(gbs / r["cpu_baseline"]["value"], 1)
+        log(json.dumps(r))
+        results[cls.cfg] = r
+        del w
+        torch.cuda.empty_cache()
+
+    head = results[2]
+    line = {
+        "metric": METRIC, "value": head["GB_s"], "unit": "GB/s", "n_gpus": 1,
+        "steps": head["steps_timed"], "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded torch RNG on device; uniform bytes over all 256 codes)",
+        "config": {"workload": "BASELINE config 2: fp8_e4m3 -> bf16 dequant [4096,14336], scale 0.0125",
+                   "elements": Fp8.n, "algorithmic_bytes_per_step": Fp8.bytes_per_step,
+                   "timing": "HIP events on the launch stream around graph replays of rotated buffer sets"},
+        "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": head["frac_of_peak"], "traffic": None, "kernel": head["kernel"]},
+        "cpu_baseline": head.get("cpu_baseline"),
+        "elements_per_s": head["elements_per_s"],
+        "configs": [results[k] for k in sorted(results)],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,194 @@
+/*
+ * mfh.h — C ABI of the MI355X (gfx950) backend for manifesto's data-parallel
+ * hot path: fused elementwise chains, runtime host math (axpy, scalar
+ * broadcast, linspace) and FP8 / Int4 / BF16 / F16 dequantisation.
+ *
+ * Plain pointers and sizes only.  Device pointers come from mfh_alloc (or any
+ * hipMalloc'd memory); `stream` is a hipStream_t, NULL for the null stream.
+ * Every launch is asynchronous on `stream`; mfh_stream_sync waits.
+ *
+ * dtype arguments are manifesto's wire codes (dtype/dtype.go:29-49):
+ *   1 Float64, 2 Float32, 3 Float16, 4 BFloat16, 5 Float8E4M3, 6 Float8E5M2,
+ *   7 Int64, 8 Int32, 9 Int16, 10 Int8, 11 Int4 (two per byte, low nibble
+ *   first), 12 Uint64, 13 Uint32, 14 Uint16, 15 Uint8.
+ *
+ * Return codes: MFH_OK (0) or a negative MFH_ERR_*; mfh_last_error() gives the
+ * calling thread's message.  Entry points that the reference declares without
+ * an error channel (mfh_axpy mirrors axpyDevice.Axpy) record failures in a
+ * sticky per-process error that mfh_stream_sync and mfh_take_sticky_error
+ * report, as the reference's zero-host-sync rule requires
+ * (scripts/check_banned.sh:34-55).
+ */
+#ifndef MFH_H
+#define MFH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MFH_OK 0
+#define MFH_ERR_INVALID_ARGUMENT (-1)
+#define MFH_ERR_DTYPE_UNSUPPORTED (-2) /* tensor.ErrDTypeUnsupported, tensor/errors.go:16-19 */
+#define MFH_ERR_SHAPE_MISMATCH (-3)    /* tensor.ErrShapeMismatch, tensor/errors.go:26-29 */
+#define MFH_ERR_DEVICE (-4)            /* a HIP runtime call failed */
+#define MFH_ERR_COMPILE (-5)           /* hiprtc rejected a generated kernel */
+#define MFH_ERR_NOT_INITIALIZED (-6)   /* mfh_init was not called */
+#define MFH_ERR_CLOSED (-7)            /* tensor.ErrBackendClosed, tensor/errors.go:50-52 */
+
+/* ---- runtime: device, memory, streams ---------------------------------- */
+
+/* Library version, major*10000 + minor*100 + patch. */
+int mfh_version(void);
+
+/* Binds the library to HIP device `device` and reads its properties.
+ * Replaces the device-side construction behind tensor.Backend
+ * (tensor/backend.go:18-68).  Idempotent for the same device. */
+int mfh_init(int device);
+
+/* Releases the JIT kernel cache; outstanding mfh_kernel handles become
+ * invalid.  tensor.Backend.Close (tensor/backend.go:64-66). */
+int mfh_shutdown(void);
+
+/* Thread-local message of the last failing call on this thread. */
+const char* mfh_last_error(void);
+
+/* Returns and clears the sticky error left by entry points without an error
+ * channel (mfh_axpy); MFH_OK when there is none. */
+int mfh_take_sticky_error(void);
+
+/* Capabilities (tensor/backend.go:82-110): total device bytes, native
+ * alignment in bytes, number of compute units. */
+int mfh_capabilities(int64_t* max_bytes, int32_t* native_alignment, int32_t* compute_units);
+
+/* Device storage for one tensor (tensor.Backend.Upload allocates, Tensor.Close
+ * releases: tensor/backend.go:40, tensor/tensor.go:75). */
+int mfh_alloc(void** ptr, size_t bytes);
+int mfh_free(void* ptr);
+
+/* Host<->device copies behind Upload / Download / Tensor.RawBytes
+ * (tensor/backend.go:40,59; tensor/tensor.go:109). */
+int mfh_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int mfh_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+
+/* Waits for `stream`; reports a pending sticky error.  Tensor.Sync
+ * (tensor/tensor.go:114). */
+int mfh_stream_sync(void* stream);
+
+/* ---- runtime host math -------------------------------------------------- */
+
+/* y <- y + alpha*x in place over `count` elements of storage dtype `dtype`
+ * (Float32, Float16 or BFloat16), the product rounded to f32 before the add
+ * and the sum re-encoded with round-to-nearest-even.  Same signature and
+ * contract as axpyDevice.Axpy (runtime/axpy.go:13-15), called where
+ * axpyOntoResident dispatches (runtime/axpy.go:84-90); the host loop it
+ * replaces is runtime/axpy.go:115-117 and :145-147.  No return value: errors
+ * are sticky. */
+void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype, void* stream);
+
+/* out[i] = in[i] op scalar, op 0 add, 1 sub, 2 mul, 3 div, computed in f32
+ * after decoding `in_dtype`, stored as `out_dtype` (Float32/Float16/BFloat16).
+ * Division by zero and unknown ops are rejected like applyScalarBroadcast
+ * (runtime/executor_math.go:195-234). */
+int mfh_scalar_broadcast(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype,
+                         int64_t count, float scalar, int32_t op, void* stream);
+
+/* out[i] = start + i*step, step = (stop-start)/intervals in f32, endpoints
+ * pinned when endpoint != 0.  runLinspace (runtime/executor_math.go:57-108). */
+int mfh_linspace(void* out, uint8_t out_dtype, int64_t count, float start, float stop,
+                 int32_t endpoint, void* stream);
+
+/* ---- dtype conversion and dequantisation -------------------------------- */
+
+/* Element-wise conversion of `count` logical elements from `in_dtype` to
+ * `out_dtype` (Float32, Float16 or BFloat16) with the reference's exact bit
+ * rules: BytesToFloat32 (dtype/convert/convert.go:85-146) followed, for 16-bit
+ * outputs, by BytesToBFloat16 / BytesToFloat16 narrowing (:155-188).
+ * in_dtype may be any numeric code including Int4 (count nibbles). */
+int mfh_convert(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype,
+                int64_t count, void* stream);
+
+/* FP8 (Float8E4M3 or Float8E5M2) -> out_dtype with a per-tensor f32 scale:
+ * out = encode(fl32(decode(q) * scale)).  decode is F8E4M3.Float32 /
+ * F8E5M2.Float32 (dtype/fp8.go:39-70,149-183); the scale has no counterpart
+ * in the reference (BytesToBFloat16, dtype/convert/convert.go:155, is the
+ * scale == 1 case).  A NaN code stays the reference's NaN; a NaN scale
+ * propagates quieted; Inf*0 gives 0xffc00000 before narrowing. */
+int mfh_dequant_fp8(void* out, uint8_t out_dtype, const void* in, uint8_t fp8_dtype,
+                    int64_t count, float scale, void* stream);
+
+/* Packed signed Int4 (decodeInt4ToFloat64, dtype/convert/decoders.go:262-289)
+ * -> out_dtype with one scale per `group` consecutive elements:
+ * out[i] = encode(fl32(q[i]) * scales[i / group]); scale_dtype is Float32,
+ * Float16 or BFloat16.  The group scale has no counterpart in the reference
+ * (OperationDequant4, ir/operation.go:158, names the device op). */
+int mfh_dequant_int4(void* out, uint8_t out_dtype, const void* packed, int64_t count,
+                     const void* scales, uint8_t scale_dtype, int64_t group, void* stream);
+
+/* ---- fused elementwise chains ------------------------------------------- */
+
+/* One FusionAST node (optimizer/fusion_ast.go:70-76).  A FusionAST crosses the
+ * ABI as the pre-order list of its nodes; each node's children follow it, their
+ * number fixed by NodeType.Arity (optimizer/fusion_ast.go:168-180).  `type` is
+ * the optimizer.NodeType value: 1 Input, 2 Constant, 3 Add, 4 Sub, 5 Mul,
+ * 6 Div, 7 Max, 8 Min, 9 Neg, 10 Abs, 11 Sqrt, 12 Exp, 13 Log, 14 ReLU,
+ * 15 Sigmoid, 16 Tanh, 17 Silu, 18 Gelu, 19 LeakyReLU. */
+typedef struct {
+    int32_t type;
+    int32_t input_index; /* Input: index into the input list */
+    double value;        /* Constant: the literal, rounded to f32 when used */
+} mfh_ast_node;
+
+/* How a kernel input is read.  MFH_OPERAND_FULL: one value per element, as
+ * CPUKernel.Run requires (codegen/cpu.go:78-85).  MFH_OPERAND_PERIODIC:
+ * `period` values, element i reads index i % period (a row-broadcast bias).
+ * MFH_OPERAND_SCALAR: one value read by every element.  The last two are new;
+ * they give the same results as a pre-expanded FULL input. */
+#define MFH_OPERAND_FULL 0
+#define MFH_OPERAND_PERIODIC 1
+#define MFH_OPERAND_SCALAR 2
+
+typedef struct {
+    uint8_t dtype; /* Float32, Float16 or BFloat16 storage */
+    uint8_t mode;  /* MFH_OPERAND_* */
+    uint8_t reserved[6];
+    int64_t period; /* MFH_OPERAND_PERIODIC only */
+} mfh_operand;
+
+/* Transcendental nodes evaluated in f64 exactly as codegen/cpu.go:172-200
+ * writes them (bit-identical to the reference but for f64 rounding ties);
+ * without it Sigmoid/Silu/Gelu use f32 algorithms within 2 ulp. */
+#define MFH_FUSION_PRECISE 1u
+
+typedef struct mfh_kernel mfh_kernel;
+
+/* EmitHIP: validates the tree, generates one HIP kernel for it (single pass
+ * over HBM, inputs decoded and output encoded in registers) and compiles it
+ * for gfx950 with hiprtc, cached by source.  The codegen target beside
+ * EmitCPU / EmitMetal (codegen/cpu.go:97, codegen/metal.go:79) selected
+ * through EmitFusion (codegen/codegen.go:68-99).  `output_port` names the
+ * kernel like metalKernelName (codegen/metal.go:281-290); may be NULL. */
+int mfh_fusion_compile(const mfh_ast_node* nodes, int32_t n_nodes, const mfh_operand* inputs,
+                       int32_t n_inputs, uint8_t out_dtype, const char* output_port,
+                       uint32_t flags, mfh_kernel** kernel);
+
+/* HIPKernel.Source / KernelName / Identifier, like MetalKernel
+ * (codegen/metal.go:38-56).  The strings live until mfh_fusion_release. */
+const char* mfh_fusion_source(const mfh_kernel* kernel);
+const char* mfh_fusion_kernel_name(const mfh_kernel* kernel);
+int32_t mfh_fusion_num_inputs(const mfh_kernel* kernel);
+
+/* Runs the kernel over `count` elements: CPUKernel.Run (codegen/cpu.go:59-90)
+ * with device buffers.  `inputs` holds one device pointer per declared input;
+ * a wrong count fails like the reference ("expects N inputs, got M"). */
+int mfh_fusion_launch(const mfh_kernel* kernel, const void* const* inputs, int32_t n_inputs,
+                      void* out, int64_t count, void* stream);
+
+int mfh_fusion_release(mfh_kernel* kernel);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MFH_H */

@@ -1,0 +1,143 @@
+// codec.hpp — bit-exact dtype codecs for gfx950 device code.
+//
+// Shared by the ahead-of-time kernels and, as text, by the prelude of every
+// JIT-compiled fused kernel, so it uses no includes and no std types.
+//
+// Each function reproduces the bit rules of manifesto's Go codecs:
+//   F8E4M3.Float32   dtype/fp8.go:39-70
+//   F8E5M2.Float32   dtype/fp8.go:149-183
+//   NewBfloat16FromFloat32  dtype/bfloat16.go:41-55
+//   f16bitsToF32bits / f32bitsToF16bits  dtype/float16.go:222-315
+//   int4 nibbles     dtype/convert/decoders.go:262-289
+// The narrowing encoders use the gfx950 conversion instructions
+// (v_cvt_pk_bf16_f32, v_cvt_f16_f32: IEEE round-to-nearest-even with
+// denormals kept) and patch NaN results to the Go payload rule explicitly.
+#ifndef MFH_CODEC_HPP
+#define MFH_CODEC_HPP
+
+typedef unsigned char mfh_u8;
+typedef unsigned short mfh_u16;
+typedef unsigned int mfh_u32;
+typedef int mfh_i32;
+typedef long long mfh_i64;
+typedef unsigned long long mfh_u64;
+typedef float mfh_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 mfh_bf16x2 __attribute__((ext_vector_type(2)));
+
+#define MFH_DEV __device__ inline __attribute__((always_inline))
+
+MFH_DEV float mfh_f32(mfh_u32 u) { return __builtin_bit_cast(float, u); }
+MFH_DEV mfh_u32 mfh_bits(float f) { return __builtin_bit_cast(mfh_u32, f); }
+MFH_DEV bool mfh_isnan(float f) { return (mfh_bits(f) & 0x7fffffffu) > 0x7f800000u; }
+
+// ---- FP8 -> f32 bits ------------------------------------------------------
+
+// E4M3: S.1111.111 is NaN (sign kept, canonical quiet payload), no Inf;
+// subnormal m*2^-9 is renormalised (the Go loop shifts until bit 3 is set).
+MFH_DEV mfh_u32 mfh_e4m3_bits(mfh_u32 code)
+{
+    mfh_u32 sign = (code & 0x80u) << 24;
+    mfh_u32 mag = code & 0x7fu;
+    mfh_u32 e = mag >> 3, m = mag & 7u;
+    if (e == 0u) {
+        mfh_u32 shift = (mfh_u32)__builtin_clz(m | 1u) - 28u;  // 1->3, 2..3->2, 4..7->1
+        m = (m << shift) & 7u;
+        e = 1u - shift;                                         // wraps like the Go uint32
+    }
+    mfh_u32 normal = sign | ((e + 120u) << 23) | (m << 20);
+    mfh_u32 out = mag == 0u ? sign : normal;
+    return mag == 0x7fu ? (sign | 0x7fc00000u) : out;
+}
+
+// E5M2: exponent 31 is Inf (m == 0) or a quiet NaN carrying m at bit 21.
+MFH_DEV mfh_u32 mfh_e5m2_bits(mfh_u32 code)
+{
+    mfh_u32 sign = (code & 0x80u) << 24;
+    mfh_u32 e = (code >> 2) & 0x1fu, m = code & 3u;
+    if (e == 0x1fu) return sign | (m == 0u ? 0x7f800000u : (0x7fc00000u | (m << 21)));
+    if (e == 0u) {
+        if (m == 0u) return sign;
+        mfh_u32 shift = (mfh_u32)__builtin_clz(m) - 29u;  // 1->2, 2..3->1
+        m = (m << shift) & 3u;
+        e = 1u - shift;
+    }
+    return sign | ((e + 112u) << 23) | (m << 21);
+}
+
+// ---- BF16 -------------------------------------------------------------------
+
+MFH_DEV float mfh_bf16_to_f32(mfh_u32 h) { return mfh_f32(h << 16); }
+
+// Software statement of the Go rule (used where a NaN can appear and for
+// checking the hardware path): NaN -> top half | 0x0040, else RNE via
+// + 0x7fff + kept LSB.
+MFH_DEV mfh_u32 mfh_bf16_rne_sw(float v)
+{
+    mfh_u32 b = mfh_bits(v);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 16) | 0x0040u;
+    return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+}
+
+// Two values -> packed bf16x2 (lo in bits 0..15).  v_cvt_pk_bf16_f32 rounds to
+// nearest even; a NaN lane is rewritten to the Go payload rule.
+MFH_DEV mfh_u32 mfh_bf16x2_rne(float lo, float hi)
+{
+    mfh_f32x2 v = {lo, hi};
+    mfh_u32 r = __builtin_bit_cast(mfh_u32, __builtin_convertvector(v, mfh_bf16x2));
+    if (mfh_isnan(lo) || mfh_isnan(hi)) {
+        mfh_u32 a = mfh_isnan(lo) ? ((mfh_bits(lo) >> 16) | 0x40u) : (r & 0xffffu);
+        mfh_u32 b = mfh_isnan(hi) ? ((mfh_bits(hi) >> 16) | 0x40u) : (r >> 16);
+        r = a | (b << 16);
+    }
+    return r;
+}
+
+MFH_DEV mfh_u32 mfh_bf16_rne(float v) { return mfh_bf16x2_rne(v, 0.0f) & 0xffffu; }
+
+// ---- F16 --------------------------------------------------------------------
+
+// Exact widening; a NaN becomes sign | 0x7fc00000 | payload << 13 as in Go.
+MFH_DEV float mfh_f16_to_f32(mfh_u32 h)
+{
+    float f = (float)__builtin_bit_cast(_Float16, (mfh_u16)h);
+    if ((h & 0x7c00u) == 0x7c00u && (h & 0x3ffu) != 0u)
+        f = mfh_f32(((h & 0x8000u) << 16) | 0x7fc00000u | ((h & 0x3ffu) << 13));
+    return f;
+}
+
+// RNE narrowing with overflow to Inf; NaN -> sign | 0x7e00 | payload >> 13.
+MFH_DEV mfh_u32 mfh_f16_rne(float v)
+{
+    mfh_u32 r = (mfh_u32)__builtin_bit_cast(mfh_u16, (_Float16)v);
+    if (mfh_isnan(v)) {
+        mfh_u32 b = mfh_bits(v);
+        r = ((b >> 16) & 0x8000u) | 0x7e00u | ((b & 0x7fffffu) >> 13);
+    }
+    return r;
+}
+
+// ---- Int4 -------------------------------------------------------------------
+
+// Nibble k (0..7) of a 32-bit word, sign-extended: element 2j is the low
+// nibble of byte j.
+MFH_DEV mfh_i32 mfh_int4_at(mfh_u32 word, mfh_u32 k)
+{
+    return __builtin_amdgcn_sbfe((mfh_i32)word, k * 4u, 4u);
+}
+
+// ---- scale multiply -----------------------------------------------------------
+
+// One IEEE multiply with the NaN rules of an x86 mulss(decoded, scale) made
+// explicit, so the result never depends on which NaN the hardware forwards.
+MFH_DEV float mfh_scale_mul(float decoded, float scale)
+{
+    mfh_u32 d = mfh_bits(decoded), s = mfh_bits(scale);
+    if ((d & 0x7fffffffu) > 0x7f800000u) return mfh_f32(d | 0x00400000u);
+    if ((s & 0x7fffffffu) > 0x7f800000u) return mfh_f32(s | 0x00400000u);
+    bool d_inf = (d & 0x7fffffffu) == 0x7f800000u, s_inf = (s & 0x7fffffffu) == 0x7f800000u;
+    bool d_zero = (d & 0x7fffffffu) == 0u, s_zero = (s & 0x7fffffffu) == 0u;
+    if ((d_inf && s_zero) || (d_zero && s_inf)) return mfh_f32(0xffc00000u);
+    return decoded * scale;
+}
+
+#endif  // MFH_CODEC_HPP

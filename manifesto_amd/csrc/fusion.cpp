@@ -1,0 +1,417 @@
+// fusion.cpp — the HIP codegen target for FusionAST (EmitHIP) and its
+// execution (HIPKernel.Run).
+//
+// EmitHIP is the gfx950 counterpart of EmitCPU / EmitMetal (codegen/cpu.go:97,
+// codegen/metal.go:79): one kernel per FusionAST whose body is the fused
+// expression, evaluated per element with the reference's f32 semantics
+// (codegen/cpu.go:126-214).  Unlike the Metal template (f32 buffers, one
+// element per thread) the generated kernel
+//   * reads each operand in its storage dtype (f32 / bf16 / f16) and decodes in
+//     registers, so a bf16 or f16 tensor needs no separate cast pass,
+//   * encodes the result to the output dtype with the reference's rounding,
+//   * moves 8 elements per thread per step with 16-byte loads and stores in a
+//     grid-stride loop, and reads broadcast operands (a [period] bias, a
+//     scalar) in place of pre-expanded copies.
+// The source is compiled for gfx950 by hiprtc with -ffp-contract=off, so
+// every Add/Sub/Mul/Div rounds on its own as in Go, and cached by its text.
+#include <hip/hiprtc.h>
+
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "common.hpp"
+#include "fusion.hpp"
+
+namespace mfh {
+
+#include "mfh_prelude.inc"  // kPrelude: codec.hpp + devmath.hpp + fusion_io.hpp
+
+int blocks_per_cu();  // dequant.hip
+
+namespace {
+
+constexpr int kVec = 8;
+constexpr int kBlockThreads = 256;
+
+const char* io_suffix(int dtype)
+{
+    switch (dtype) {
+    case kFloat32: return "f32";
+    case kBFloat16: return "bf16";
+    case kFloat16: return "f16";
+    default: return nullptr;
+    }
+}
+
+std::string hex32(float f)
+{
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    char buf[32];
+    snprintf(buf, sizeof buf, "mfh_fromfbits(0x%08xu)", u);
+    return buf;
+}
+
+// Pre-order list -> child links; -1 if malformed.
+int link(const std::vector<mfh_ast_node>& nodes, int idx, std::vector<int>& c0, std::vector<int>& c1)
+{
+    if (idx >= (int)nodes.size()) return -1;
+    int arity = node_arity(nodes[idx].type);
+    if (arity < 0) return -1;
+    int next = idx + 1;
+    for (int k = 0; k < arity; k++) {
+        (k == 0 ? c0 : c1)[idx] = next;
+        next = link(nodes, next, c0, c1);
+        if (next < 0) return -1;
+    }
+    return next;
+}
+
+struct Emitter {
+    const std::vector<mfh_ast_node>& nodes;
+    const std::vector<int>& c0;
+    const std::vector<int>& c1;
+    bool precise;
+    std::string body;
+    int tmp = 0;
+
+    std::string fresh() { return "t" + std::to_string(tmp++); }
+
+    std::string let(const std::string& expr)
+    {
+        std::string name = fresh();
+        body += "        const float " + name + " = " + expr + ";\n";
+        return name;
+    }
+
+    // Returns the name holding node idx's value for the current element.
+    std::string emit(int idx)
+    {
+        const mfh_ast_node& n = nodes[idx];
+        switch (n.type) {
+        case kNodeInput: return "x" + std::to_string(n.input_index);
+        case kNodeConstant: return let(hex32((float)n.value));  // float32(node.Value)
+        default: break;
+        }
+        std::string a = emit(c0[idx]);
+        if (node_arity(n.type) == 2) {
+            std::string b = emit(c1[idx]);
+            switch (n.type) {
+            case kNodeAdd: return let(a + " + " + b);
+            case kNodeSub: return let(a + " - " + b);
+            case kNodeMul: return let(a + " * " + b);
+            case kNodeDiv: return let(a + " / " + b);
+            case kNodeMax: return let("(" + a + " > " + b + ") ? " + a + " : " + b);
+            case kNodeMin: return let("(" + a + " < " + b + ") ? " + a + " : " + b);
+            }
+        }
+        switch (n.type) {
+        case kNodeNeg: return let("-" + a);
+        case kNodeAbs: return let("(" + a + " < 0.0f) ? -" + a + " : " + a);
+        case kNodeSqrt: return let("mfh_sqrtf(" + a + ")");
+        case kNodeExp: return let("mfh_exp_ref(" + a + ")");
+        case kNodeLog: return let("mfh_log_ref(" + a + ")");
+        case kNodeReLU: return let("(" + a + " < 0.0f) ? 0.0f : " + a);
+        case kNodeSigmoid: return let((precise ? "mfh_sigmoid_ref(" : "mfh_sigmoid(") + a + ")");
+        case kNodeTanh: return let("mfh_tanh_ref(" + a + ")");
+        case kNodeSilu: return let((precise ? "mfh_silu_ref(" : "mfh_silu(") + a + ")");
+        case kNodeGelu: return let((precise ? "mfh_gelu_ref(" : "mfh_gelu(") + a + ")");
+        case kNodeLeakyReLU: {
+            std::string scaled = let("0.01f * " + a);
+            return let("(" + a + " >= 0.0f) ? " + a + " : " + scaled);
+        }
+        }
+        return let("0.0f");  // unreachable: validated
+    }
+};
+
+std::string sanitize(const std::string& port)
+{
+    std::string s;
+    for (char ch : port) s += ((ch >= 'a' && ch <= 'z') || (ch >= 'A' && ch <= 'Z') || (ch >= '0' && ch <= '9')) ? ch : '_';
+    return s.empty() ? "anon" : s;
+}
+
+std::string operand_index(const mfh_operand& op, const char* elem)
+{
+    if (op.mode == MFH_OPERAND_PERIODIC) return std::string("(") + elem + " % " + std::to_string(op.period) + "LL)";
+    return elem;
+}
+
+// ---- compiled-code cache -----------------------------------------------------
+
+struct CodeObject {
+    std::vector<char> code;
+    std::string kernel_name;
+    std::mutex mu;
+    int device = -1;
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;
+};
+
+std::mutex g_cache_mu;
+std::unordered_map<std::string, std::shared_ptr<CodeObject>> g_cache;
+
+int compile_source(const std::string& source, const std::string& kernel_name, std::shared_ptr<CodeObject>* out)
+{
+    {
+        std::lock_guard<std::mutex> lock(g_cache_mu);
+        auto it = g_cache.find(source);
+        if (it != g_cache.end()) {
+            *out = it->second;
+            return MFH_OK;
+        }
+    }
+    hiprtcProgram prog;
+    if (hiprtcCreateProgram(&prog, source.c_str(), (kernel_name + ".hip").c_str(), 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+        return fail(MFH_ERR_COMPILE, "codegen hip: hiprtcCreateProgram failed");
+    const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                          "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature",
+                          "-Xclang", "-packed-fp32-ops"};
+    hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
+    if (rc != HIPRTC_SUCCESS) {
+        size_t log_size = 0;
+        hiprtcGetProgramLogSize(prog, &log_size);
+        std::string log(log_size + 1, '\0');
+        hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        return fail(MFH_ERR_COMPILE, "codegen hip: compiling %s failed: %s", kernel_name.c_str(), log.c_str());
+    }
+    auto obj = std::make_shared<CodeObject>();
+    size_t size = 0;
+    hiprtcGetCodeSize(prog, &size);
+    obj->code.resize(size);
+    hiprtcGetCode(prog, obj->code.data());
+    hiprtcDestroyProgram(&prog);
+    obj->kernel_name = kernel_name;
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    auto it = g_cache.emplace(source, obj).first;
+    *out = it->second;
+    return MFH_OK;
+}
+
+int load_function(CodeObject& obj, int device, hipFunction_t* fn)
+{
+    std::lock_guard<std::mutex> lock(obj.mu);
+    if (obj.function && obj.device == device) {
+        *fn = obj.function;
+        return MFH_OK;
+    }
+    if (obj.module) {
+        (void)hipModuleUnload(obj.module);
+        obj.module = nullptr;
+        obj.function = nullptr;
+    }
+    MFH_TRY(check_hip(hipModuleLoadData(&obj.module, obj.code.data()), "hipModuleLoadData"));
+    MFH_TRY(check_hip(hipModuleGetFunction(&obj.function, obj.module, obj.kernel_name.c_str()), "hipModuleGetFunction"));
+    obj.device = device;
+    *fn = obj.function;
+    return MFH_OK;
+}
+
+}  // namespace
+
+int node_arity(int type)
+{
+    switch (type) {
+    case kNodeInput: case kNodeConstant: return 0;
+    case kNodeNeg: case kNodeAbs: case kNodeSqrt: case kNodeExp: case kNodeLog: case kNodeReLU:
+    case kNodeSigmoid: case kNodeTanh: case kNodeSilu: case kNodeGelu: case kNodeLeakyReLU: return 1;
+    case kNodeAdd: case kNodeSub: case kNodeMul: case kNodeDiv: case kNodeMax: case kNodeMin: return 2;
+    default: return -1;
+    }
+}
+
+}  // namespace mfh
+
+// The opaque handle of the C ABI: one compiled FusionAST (HIPKernel).
+struct mfh_kernel {
+    std::string identifier;
+    std::string kernel_name;
+    std::string source;
+    std::vector<mfh_operand> inputs;
+    uint8_t out_dtype = mfh::kFloat32;
+    bool periods_vectorizable = true;
+    std::shared_ptr<mfh::CodeObject> code;
+};
+
+namespace mfh {
+
+int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, int n_inputs,
+             uint8_t out_dtype, const char* output_port, uint32_t flags, mfh_kernel** out)
+{
+    if (!out) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: kernel out-pointer is NULL");
+    *out = nullptr;
+    if (!nodes || n_nodes <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: fusion root is required");
+    if (n_inputs < 0 || (n_inputs > 0 && !inputs))
+        return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: bad input list");
+    if (!io_suffix(out_dtype))
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "codegen hip: output dtype %s is not f32/bf16/f16", dtype_name(out_dtype));
+    std::vector<mfh_ast_node> list(nodes, nodes + n_nodes);
+    for (int i = 0; i < n_nodes; i++) {
+        if (node_arity(list[i].type) < 0)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: unsupported node type %d", list[i].type);
+        if (list[i].type == kNodeInput && (list[i].input_index < 0 || list[i].input_index >= n_inputs))
+            return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: input index %d out of range [0, %d)",
+                        list[i].input_index, n_inputs);
+    }
+    std::vector<int> c0(n_nodes, -1), c1(n_nodes, -1);
+    if (link(list, 0, c0, c1) != n_nodes)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: the node list is not one pre-order tree");
+
+    bool periods_vectorizable = true;
+    for (int k = 0; k < n_inputs; k++) {
+        const mfh_operand& op = inputs[k];
+        if (!io_suffix(op.dtype))
+            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "codegen hip: input %d dtype %s is not f32/bf16/f16", k, dtype_name(op.dtype));
+        if (op.mode > MFH_OPERAND_SCALAR)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: input %d has unknown mode %d", k, op.mode);
+        if (op.mode == MFH_OPERAND_PERIODIC && op.period <= 0)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: input %d period must be positive", k);
+        if (op.mode == MFH_OPERAND_PERIODIC && op.period % kVec != 0) periods_vectorizable = false;
+    }
+
+    const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
+    Emitter em{list, c0, c1, precise, "", 0};
+    std::string result = em.emit(0);
+
+    std::string identifier = output_port && *output_port ? output_port : "anon";
+    std::string kernel_name = "fused_" + sanitize(output_port ? output_port : "");
+    const char* osfx = io_suffix(out_dtype);
+
+    std::string src;
+    src.reserve(sizeof(kPrelude) + 4096);
+    src += kPrelude;
+    src += "\n// EmitHIP: fusion '" + identifier + "'" + (precise ? " (precise transcendentals)" : "") + "\n";
+    src += "extern \"C\" __global__ __launch_bounds__(256) void " + kernel_name + "(\n";
+    for (int k = 0; k < n_inputs; k++) src += "    const void* __restrict__ p" + std::to_string(k) + ",\n";
+    src += "    void* __restrict__ pout, mfh_i64 n, mfh_i64 nvec)\n{\n";
+    src += "    const mfh_i64 stride = (mfh_i64)gridDim.x * 256;\n";
+    src += "    const mfh_i64 tid = (mfh_i64)blockIdx.x * 256 + threadIdx.x;\n";
+    for (int k = 0; k < n_inputs; k++)
+        if (inputs[k].mode == MFH_OPERAND_SCALAR)
+            src += "    const float s" + std::to_string(k) + " = mfh_ld1_" + io_suffix(inputs[k].dtype) + "(p" +
+                   std::to_string(k) + ", 0);\n";
+    // vector loop
+    src += "    for (mfh_i64 v = tid; v < nvec; v += stride) {\n";
+    src += "        const mfh_i64 e0 = v * 8;\n";
+    for (int k = 0; k < n_inputs; k++) {
+        if (inputs[k].mode == MFH_OPERAND_SCALAR) continue;
+        std::string ks = std::to_string(k);
+        src += "        float a" + ks + "[8];\n";
+        src += "        mfh_ld8_" + std::string(io_suffix(inputs[k].dtype)) + "(p" + ks + ", " +
+               operand_index(inputs[k], "e0") + ", a" + ks + ");\n";
+    }
+    src += "        float r[8];\n#pragma unroll\n        for (int j = 0; j < 8; j++) {\n";
+    for (int k = 0; k < n_inputs; k++) {
+        std::string ks = std::to_string(k);
+        src += "        const float x" + ks + " = " + (inputs[k].mode == MFH_OPERAND_SCALAR ? "s" + ks : "a" + ks + "[j]") + ";\n";
+    }
+    src += em.body;
+    src += "        r[j] = " + result + ";\n        }\n";
+    src += std::string("        mfh_st8_") + osfx + "(pout, e0, r);\n    }\n";
+    // scalar tail (and the whole range when the vector path is off)
+    src += "    for (mfh_i64 i = nvec * 8 + tid; i < n; i += stride) {\n";
+    for (int k = 0; k < n_inputs; k++) {
+        std::string ks = std::to_string(k);
+        if (inputs[k].mode == MFH_OPERAND_SCALAR)
+            src += "        const float x" + ks + " = s" + ks + ";\n";
+        else
+            src += "        const float x" + ks + " = mfh_ld1_" + io_suffix(inputs[k].dtype) + "(p" + ks + ", " +
+                   operand_index(inputs[k], "i") + ");\n";
+    }
+    src += em.body;
+    src += std::string("        mfh_st1_") + osfx + "(pout, i, " + result + ");\n    }\n}\n";
+
+    auto kernel = std::make_unique<mfh_kernel>();
+    kernel->identifier = identifier;
+    kernel->kernel_name = kernel_name;
+    kernel->source = std::move(src);
+    kernel->inputs.assign(inputs, inputs + n_inputs);
+    kernel->out_dtype = out_dtype;
+    kernel->periods_vectorizable = periods_vectorizable;
+    MFH_TRY(compile_source(kernel->source, kernel_name, &kernel->code));
+    *out = kernel.release();
+    return MFH_OK;
+}
+
+int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
+            hipStream_t stream)
+{
+    if (!kernel) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: kernel is empty");
+    if (n_inputs != (int)kernel->inputs.size())
+        return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: kernel \"%s\" expects %d inputs, got %d",
+                    kernel->identifier.c_str(), (int)kernel->inputs.size(), n_inputs);
+    if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: negative count %lld", (long long)count);
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    if (count == 0) return MFH_OK;
+    if (!out) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: output buffer is NULL");
+    bool vec_ok = kernel->periods_vectorizable && aligned16(out);
+    for (int k = 0; k < n_inputs; k++) {
+        if (!inputs[k])
+            return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: input %d is NULL", k);
+        if (kernel->inputs[k].mode != MFH_OPERAND_SCALAR && !aligned16(inputs[k])) vec_ok = false;
+    }
+    hipFunction_t fn;
+    MFH_TRY(load_function(*kernel->code, dev->ordinal, &fn));
+    int64_t nvec = vec_ok ? count / kVec : 0;
+    int64_t items = nvec > 0 ? nvec : count;
+    int64_t need = (items + kBlockThreads - 1) / kBlockThreads;
+    int64_t cap = (int64_t)dev->compute_units * blocks_per_cu();
+    unsigned grid = (unsigned)std::max<int64_t>(1, std::min(need, cap));
+    std::vector<const void*> ptrs(inputs, inputs + n_inputs);
+    std::vector<void*> args;
+    args.reserve(n_inputs + 3);
+    for (int k = 0; k < n_inputs; k++) args.push_back(&ptrs[k]);
+    args.push_back(&out);
+    args.push_back(&count);
+    args.push_back(&nvec);
+    return check_hip(hipModuleLaunchKernel(fn, grid, 1, 1, kBlockThreads, 1, 1, 0, stream, args.data(), nullptr),
+                     "hipModuleLaunchKernel");
+}
+
+void release_kernel_cache()
+{
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    for (auto& kv : g_cache) {
+        std::lock_guard<std::mutex> obj_lock(kv.second->mu);
+        if (kv.second->module) (void)hipModuleUnload(kv.second->module);
+        kv.second->module = nullptr;
+        kv.second->function = nullptr;
+    }
+    g_cache.clear();
+}
+
+}  // namespace mfh
+
+using namespace mfh;
+
+extern "C" {
+
+int mfh_fusion_compile(const mfh_ast_node* nodes, int32_t n_nodes, const mfh_operand* inputs, int32_t n_inputs,
+                       uint8_t out_dtype, const char* output_port, uint32_t flags, mfh_kernel** kernel)
+{
+    return emit_hip(nodes, n_nodes, inputs, n_inputs, out_dtype, output_port, flags, kernel);
+}
+
+const char* mfh_fusion_source(const mfh_kernel* kernel) { return kernel ? kernel->source.c_str() : nullptr; }
+const char* mfh_fusion_kernel_name(const mfh_kernel* kernel) { return kernel ? kernel->kernel_name.c_str() : nullptr; }
+int32_t mfh_fusion_num_inputs(const mfh_kernel* kernel) { return kernel ? (int32_t)kernel->inputs.size() : -1; }
+
+int mfh_fusion_launch(const mfh_kernel* kernel, const void* const* inputs, int32_t n_inputs, void* out,
+                      int64_t count, void* stream)
+{
+    return run_hip(kernel, inputs, n_inputs, out, count, (hipStream_t)stream);
+}
+
+int mfh_fusion_release(mfh_kernel* kernel)
+{
+    delete kernel;
+    return MFH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,25 @@
+// fusion.hpp — FusionAST node types (optimizer/fusion_ast.go:30-65) and the
+// HIP codegen target's entry points.
+#ifndef MFH_FUSION_HPP
+#define MFH_FUSION_HPP
+
+#include <cstdint>
+
+#include "common.hpp"
+
+namespace mfh {
+
+// optimizer.NodeType values, in the Go iota order.
+enum NodeType : int32_t {
+    kNodeInvalid = 0, kNodeInput, kNodeConstant,
+    kNodeAdd, kNodeSub, kNodeMul, kNodeDiv, kNodeMax, kNodeMin,
+    kNodeNeg, kNodeAbs, kNodeSqrt, kNodeExp, kNodeLog,
+    kNodeReLU, kNodeSigmoid, kNodeTanh, kNodeSilu, kNodeGelu, kNodeLeakyReLU,
+};
+
+// NodeType.Arity (optimizer/fusion_ast.go:168-180); -1 for unknown types.
+int node_arity(int type);
+
+}  // namespace mfh
+
+#endif  // MFH_FUSION_HPP

@@ -1,0 +1,238 @@
+// hostmath.hip — the runtime's vector math on gfx950: axpy (runtime/axpy.go),
+// scalar broadcast and linspace (runtime/executor_math.go).
+//
+// axpy moves 12 bytes per f32 element (read x, read y, write y) and does two
+// flops, so it is an HBM stream: 16-byte vectors in a grid-stride loop.  The
+// product is rounded before the add (the library is built with
+// -ffp-contract=off), as the Go loop at runtime/axpy.go:115-117 computes it.
+#include "launch.hpp"
+
+namespace mfh {
+namespace {
+
+template <int DT>
+MFH_DEV float dec16(mfh_u32 h)
+{
+    return DT == kBFloat16 ? mfh_bf16_to_f32(h) : mfh_f16_to_f32(h);
+}
+
+template <int DT>
+MFH_DEV mfh_u32 enc16x2(float lo, float hi)
+{
+    if constexpr (DT == kBFloat16) return mfh_bf16x2_rne(lo, hi);
+    else return mfh_f16_rne(lo) | (mfh_f16_rne(hi) << 16);
+}
+
+MFH_DEV float axpy_step(float y, float x, float alpha)
+{
+    float product = alpha * x;
+    return y + product;
+}
+
+__global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, const float* __restrict__ x,
+                                                     mfh_i64 n, float alpha, int vec_ok)
+{
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 nvec = vec_ok ? (n >> 2) : 0;
+    u32x4* yv = reinterpret_cast<u32x4*>(y);
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
+        u32x4 a = xv[v], b = yv[v];
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; k++) o[k] = mfh_bits(axpy_step(mfh_f32(b[k]), mfh_f32(a[k]), alpha));
+        yv[v] = o;
+    }
+    for (mfh_i64 i = nvec * 4 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        y[i] = axpy_step(y[i], x[i], alpha);
+}
+
+// 16-bit storage: decode, the same f32 step, re-encode (axpyOntoHost tensor
+// path, runtime/axpy.go:120-161, in one pass instead of five).
+template <int DT>
+__global__ __launch_bounds__(kBlock) void k_axpy16(mfh_u16* __restrict__ y, const mfh_u16* __restrict__ x,
+                                                   mfh_i64 n, float alpha, int vec_ok)
+{
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 nvec = vec_ok ? (n >> 3) : 0;
+    u32x4* yv = reinterpret_cast<u32x4*>(y);
+    const u32x4* xv = reinterpret_cast<const u32x4*>(x);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
+        u32x4 a = xv[v], b = yv[v];
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float lo = axpy_step(dec16<DT>(b[k] & 0xffffu), dec16<DT>(a[k] & 0xffffu), alpha);
+            float hi = axpy_step(dec16<DT>(b[k] >> 16), dec16<DT>(a[k] >> 16), alpha);
+            o[k] = enc16x2<DT>(lo, hi);
+        }
+        yv[v] = o;
+    }
+    for (mfh_i64 i = nvec * 8 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float r = axpy_step(dec16<DT>(y[i]), dec16<DT>(x[i]), alpha);
+        y[i] = (mfh_u16)(enc16x2<DT>(r, 0.0f) & 0xffffu);
+    }
+}
+
+template <int DT>
+MFH_DEV float load_f(const void* p, mfh_i64 i)
+{
+    if constexpr (DT == kFloat32) return static_cast<const float*>(p)[i];
+    else return dec16<DT>(static_cast<const mfh_u16*>(p)[i]);
+}
+
+template <int DT>
+MFH_DEV void store_f(void* p, mfh_i64 i, float v)
+{
+    if constexpr (DT == kFloat32) static_cast<float*>(p)[i] = v;
+    else static_cast<mfh_u16*>(p)[i] = (mfh_u16)(enc16x2<DT>(v, 0.0f) & 0xffffu);
+}
+
+MFH_DEV float apply_op(float v, float s, int op)
+{
+    switch (op) {
+    case 0: return v + s;
+    case 1: return v - s;
+    case 2: return v * s;
+    default: return v / s;
+    }
+}
+
+template <int IN, int OUT>
+__global__ __launch_bounds__(kBlock) void k_scalar_broadcast(void* __restrict__ out, const void* __restrict__ in,
+                                                             mfh_i64 n, float s, int op)
+{
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    for (mfh_i64 i = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        store_f<OUT>(out, i, apply_op(load_f<IN>(in, i), s, op));
+}
+
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void k_linspace(void* __restrict__ out, mfh_i64 n, float start,
+                                                     float stop, float step, int pin_first, int pin_last)
+{
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    for (mfh_i64 i = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float scaled = (float)i * step;
+        float v = start + scaled;
+        if (pin_first && i == 0) v = start;
+        if (pin_last && i == n - 1) v = stop;
+        store_f<OUT>(out, i, v);
+    }
+}
+
+int check_float_dtype(int dt, const char* what)
+{
+    if (dt == kFloat32 || dt == kBFloat16 || dt == kFloat16) return MFH_OK;
+    return fail(MFH_ERR_DTYPE_UNSUPPORTED, "%s: dtype %s is not f32/bf16/f16", what, dtype_name(dt));
+}
+
+template <int IN>
+int launch_broadcast(int out_dt, unsigned grid, hipStream_t s, void* out, const void* in, int64_t n,
+                     float scalar, int op)
+{
+    switch (out_dt) {
+    case kFloat32: k_scalar_broadcast<IN, kFloat32><<<grid, kBlock, 0, s>>>(out, in, n, scalar, op); break;
+    case kBFloat16: k_scalar_broadcast<IN, kBFloat16><<<grid, kBlock, 0, s>>>(out, in, n, scalar, op); break;
+    default: k_scalar_broadcast<IN, kFloat16><<<grid, kBlock, 0, s>>>(out, in, n, scalar, op); break;
+    }
+    return launch_status("k_scalar_broadcast");
+}
+
+}  // namespace
+}  // namespace mfh
+
+using namespace mfh;
+
+extern "C" {
+
+void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype, void* stream)
+{
+    const Device* dev;
+    if (bind_device(&dev) != MFH_OK) {
+        fail_sticky(MFH_ERR_NOT_INITIALIZED, "mfh_axpy: mfh_init has not been called");
+        return;
+    }
+    if (count < 0) {
+        fail_sticky(MFH_ERR_INVALID_ARGUMENT, "mfh_axpy: negative count %lld", (long long)count);
+        return;
+    }
+    if (count == 0) return;
+    if (!y || !x) {
+        fail_sticky(MFH_ERR_INVALID_ARGUMENT, "mfh_axpy: NULL buffer");
+        return;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    int vec_ok = aligned16(y) && aligned16(x);
+    switch (dtype) {
+    case kFloat32: {
+        int64_t items = vec_ok ? std::max<int64_t>(count >> 2, 1) : count;
+        k_axpy_f32<<<grid_for(items, dev), kBlock, 0, s>>>(static_cast<float*>(y), static_cast<const float*>(x),
+                                                           count, alpha, vec_ok);
+        break;
+    }
+    case kBFloat16:
+    case kFloat16: {
+        int64_t items = vec_ok ? std::max<int64_t>(count >> 3, 1) : count;
+        unsigned grid = grid_for(items, dev);
+        auto* yy = static_cast<mfh_u16*>(y);
+        auto* xx = static_cast<const mfh_u16*>(x);
+        if (dtype == kBFloat16) k_axpy16<kBFloat16><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
+        else k_axpy16<kFloat16><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
+        break;
+    }
+    default:
+        fail_sticky(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_axpy: dtype %s is not f32/bf16/f16", dtype_name(dtype));
+        return;
+    }
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) fail_sticky(MFH_ERR_DEVICE, "mfh_axpy: launch failed: %s", hipGetErrorString(err));
+}
+
+int mfh_scalar_broadcast(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype, int64_t count,
+                         float scalar, int32_t op, void* stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    MFH_TRY(check_float_dtype(out_dtype, "mfh_scalar_broadcast"));
+    MFH_TRY(check_float_dtype(in_dtype, "mfh_scalar_broadcast"));
+    if (op < 0 || op > 3) return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: unsupported op %d", op);
+    if (op == 3 && scalar == 0.0f)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: scalar divisor must be nonzero");
+    if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: negative count");
+    if (count == 0) return MFH_OK;
+    if (!out || !in) return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: NULL buffer");
+    unsigned grid = grid_for(count, dev);
+    hipStream_t s = (hipStream_t)stream;
+    switch (in_dtype) {
+    case kFloat32: return launch_broadcast<kFloat32>(out_dtype, grid, s, out, in, count, scalar, op);
+    case kBFloat16: return launch_broadcast<kBFloat16>(out_dtype, grid, s, out, in, count, scalar, op);
+    default: return launch_broadcast<kFloat16>(out_dtype, grid, s, out, in, count, scalar, op);
+    }
+}
+
+int mfh_linspace(void* out, uint8_t out_dtype, int64_t count, float start, float stop, int32_t endpoint,
+                 void* stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    MFH_TRY(check_float_dtype(out_dtype, "math.linspace"));
+    if (count <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "math.linspace: count must be positive");
+    if (!out) return fail(MFH_ERR_INVALID_ARGUMENT, "math.linspace: NULL buffer");
+    int64_t intervals = count == 1 ? 1 : (endpoint ? count - 1 : count);
+    float diff = stop - start;
+    float step = diff / (float)intervals;
+    // count == 1 returns start itself; with the endpoint both ends are pinned.
+    int pin_first = (count == 1 || endpoint) ? 1 : 0;
+    int pin_last = (count > 1 && endpoint) ? 1 : 0;
+    unsigned grid = grid_for(count, dev);
+    hipStream_t s = (hipStream_t)stream;
+    switch (out_dtype) {
+    case kFloat32: k_linspace<kFloat32><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;
+    case kBFloat16: k_linspace<kBFloat16><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;
+    default: k_linspace<kFloat16><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;
+    }
+    return launch_status("k_linspace");
+}
+
+}  // extern "C"

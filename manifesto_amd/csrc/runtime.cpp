@@ -1,0 +1,203 @@
+// runtime.cpp — device binding, memory, copies, streams and error state.
+#include <atomic>
+#include <cstdio>
+#include <mutex>
+
+#include "common.hpp"
+
+namespace mfh {
+
+namespace {
+thread_local std::string t_last_error;
+std::atomic<int> g_sticky_code{MFH_OK};
+std::mutex g_sticky_mu;
+std::string g_sticky_msg;
+std::mutex g_init_mu;
+Device g_device;
+std::atomic<bool> g_ready{false};
+
+std::string vformat(const char* fmt, va_list ap)
+{
+    char buf[1024];
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    return buf;
+}
+}  // namespace
+
+int fail(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    t_last_error = vformat(fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+void fail_sticky(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    std::string msg = vformat(fmt, ap);
+    va_end(ap);
+    std::lock_guard<std::mutex> lock(g_sticky_mu);
+    if (g_sticky_code.load() == MFH_OK) {
+        g_sticky_msg = msg;
+        g_sticky_code.store(code);
+    }
+    t_last_error = msg;
+}
+
+int check_hip(hipError_t err, const char* what)
+{
+    if (err == hipSuccess) return MFH_OK;
+    return fail(MFH_ERR_DEVICE, "%s: %s", what, hipGetErrorString(err));
+}
+
+int dtype_size(int dtype)
+{
+    switch (dtype) {
+    case kFloat64: case kInt64: case kUint64: return 8;
+    case kFloat32: case kInt32: case kUint32: return 4;
+    case kFloat16: case kBFloat16: case kInt16: case kUint16: return 2;
+    case kF8E4M3: case kF8E5M2: case kInt8: case kUint8: return 1;
+    default: return 0;
+    }
+}
+
+const char* dtype_name(int dtype)
+{
+    switch (dtype) {
+    case kFloat64: return "f64";
+    case kFloat32: return "f32";
+    case kFloat16: return "f16";
+    case kBFloat16: return "bf16";
+    case kF8E4M3: return "fp8e4m3";
+    case kF8E5M2: return "fp8e5m2";
+    case kInt64: return "i64";
+    case kInt32: return "i32";
+    case kInt16: return "i16";
+    case kInt8: return "i8";
+    case kInt4: return "i4";
+    case kUint64: return "u64";
+    case kUint32: return "u32";
+    case kUint16: return "u16";
+    case kUint8: return "u8";
+    case kBool: return "bool";
+    default: return "invalid";
+    }
+}
+
+int bind_device(const Device** out)
+{
+    if (!g_ready.load(std::memory_order_acquire))
+        return fail(MFH_ERR_NOT_INITIALIZED, "mfh: mfh_init has not been called");
+    int current = -1;
+    if (hipGetDevice(&current) != hipSuccess || current != g_device.ordinal)
+        MFH_TRY(check_hip(hipSetDevice(g_device.ordinal), "hipSetDevice"));
+    *out = &g_device;
+    return MFH_OK;
+}
+
+void release_kernel_cache();  // fusion.cpp
+
+}  // namespace mfh
+
+using namespace mfh;
+
+extern "C" {
+
+int mfh_version(void) { return 100; }
+
+const char* mfh_last_error(void) { return t_last_error.c_str(); }
+
+int mfh_take_sticky_error(void)
+{
+    std::lock_guard<std::mutex> lock(g_sticky_mu);
+    int code = g_sticky_code.exchange(MFH_OK);
+    if (code != MFH_OK) t_last_error = g_sticky_msg;
+    g_sticky_msg.clear();
+    return code;
+}
+
+int mfh_init(int device)
+{
+    std::lock_guard<std::mutex> lock(g_init_mu);
+    if (g_ready.load() && g_device.ordinal == device) return MFH_OK;
+    int count = 0;
+    MFH_TRY(check_hip(hipGetDeviceCount(&count), "hipGetDeviceCount"));
+    if (device < 0 || device >= count)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_init: device %d out of range [0, %d)", device, count);
+    MFH_TRY(check_hip(hipSetDevice(device), "hipSetDevice"));
+    hipDeviceProp_t prop;
+    MFH_TRY(check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties"));
+    g_device.ordinal = device;
+    g_device.compute_units = prop.multiProcessorCount;
+    g_device.total_bytes = (int64_t)prop.totalGlobalMem;
+    g_ready.store(true, std::memory_order_release);
+    return MFH_OK;
+}
+
+int mfh_shutdown(void)
+{
+    std::lock_guard<std::mutex> lock(g_init_mu);
+    release_kernel_cache();
+    g_ready.store(false);
+    return MFH_OK;
+}
+
+int mfh_capabilities(int64_t* max_bytes, int32_t* native_alignment, int32_t* compute_units)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    if (max_bytes) *max_bytes = dev->total_bytes;
+    if (native_alignment) *native_alignment = 256;
+    if (compute_units) *compute_units = dev->compute_units;
+    return MFH_OK;
+}
+
+int mfh_alloc(void** ptr, size_t bytes)
+{
+    if (!ptr) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_alloc: ptr is NULL");
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    *ptr = nullptr;
+    if (bytes == 0) return MFH_OK;
+    return check_hip(hipMalloc(ptr, bytes), "hipMalloc");
+}
+
+int mfh_free(void* ptr)
+{
+    if (!ptr) return MFH_OK;
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    return check_hip(hipFree(ptr), "hipFree");
+}
+
+int mfh_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    if (bytes == 0) return MFH_OK;
+    return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream),
+                     "hipMemcpyAsync(H2D)");
+}
+
+int mfh_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    if (bytes == 0) return MFH_OK;
+    MFH_TRY(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream),
+                      "hipMemcpyAsync(D2H)"));
+    return check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+int mfh_stream_sync(void* stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    MFH_TRY(check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize"));
+    return mfh_take_sticky_error();
+}
+
+}  // extern "C"

@@ -1,0 +1,143 @@
+"""CPU tests of the C ABI library: symbols, JIT codegen and error paths.
+
+No kernel is launched here; launches are the GPU tests.
+"""
+import os
+import re
+import subprocess
+
+import pytest
+
+import manifesto_amd as M
+from oracle import (N_ADD, N_GELU, N_INPUT, N_MUL, N_RELU, N_SILU, N_SIGMOID, N_SUB, N_CONSTANT,
+                    N_EXP, N_LEAKY_RELU, flatten)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mfh.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mfh_[a-z0-9_]+)\s*\(", text)))
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", M.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_library_exports_every_declared_symbol():
+    declared = declared_symbols()
+    assert len(declared) >= 20
+    missing = [s for s in declared if s not in exported_symbols()]
+    assert not missing, missing
+    for s in declared:
+        getattr(M.lib(), s)  # resolvable through ctypes too
+    assert M.lib().mfh_version() == 100
+
+
+def swiglu_nodes():
+    # Mul(Silu(In0), In1): what Fuse builds from swish -> mul (optimizer/fuse.go:199-265).
+    return flatten((N_MUL, (N_SILU, ("in", 0)), ("in", 1)))
+
+
+def test_emit_hip_swiglu_source_shape():
+    k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "mlp.swiglu-out")
+    src = k.source
+    assert k.kernel_name == "fused_mlp_swiglu_out"  # like metalKernelName (codegen/metal.go:281-290)
+    assert f'void {k.kernel_name}(' in src
+    assert "mfh_ld8_bf16(p0, e0, a0)" in src and "mfh_ld8_bf16(p1, e0, a1)" in src
+    assert "mfh_silu(x0)" in src and "mfh_st8_bf16(pout, e0, r)" in src
+    assert src.count("for (mfh_i64 i = nvec * 8 + tid; i < n; i += stride)") == 1
+
+
+def test_emit_hip_broadcast_operands():
+    # Add(Gelu(Mul(Add(x, bias), s)), residual), bias periodic over 4096, s scalar.
+    nodes = flatten((N_ADD, (N_GELU, (N_MUL, (N_ADD, ("in", 0), ("in", 1)), ("in", 2))), ("in", 3)))
+    ops = [(M.FLOAT16, M.OPERAND_FULL, 0), (M.FLOAT16, M.OPERAND_PERIODIC, 4096),
+           (M.FLOAT32, M.OPERAND_SCALAR, 0), (M.FLOAT16, M.OPERAND_FULL, 0)]
+    k = M.FusedKernel(nodes, ops, M.FLOAT16, "chain")
+    src = k.source
+    assert "mfh_ld8_f16(p1, (e0 % 4096LL), a1)" in src
+    assert "const float s2 = mfh_ld1_f32(p2, 0);" in src
+    assert "mfh_gelu(" in src
+    precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)
+    assert "mfh_gelu_ref(" in precise.source
+
+
+def test_emit_hip_constants_are_rounded_to_f32():
+    nodes = flatten((N_MUL, ("in", 0), ("const", 0.1)))
+    k = M.FusedKernel(nodes, [(M.FLOAT32, M.OPERAND_FULL, 0)], M.FLOAT32, "c")
+    assert "mfh_fromfbits(0x3dcccccdu)" in k.source  # float32(0.1)
+
+
+@pytest.mark.parametrize("nodes, n_in, msg", [
+    ([], 1, "fusion root is required"),
+    ([(N_ADD, 0, 0.0), (N_INPUT, 0, 0.0)], 1, "not one pre-order tree"),
+    ([(N_RELU, 0, 0.0), (N_INPUT, 3, 0.0)], 2, "input index 3 out of range"),
+    ([(42, 0, 0.0)], 1, "unsupported node type 42"),
+    ([(N_RELU, 0, 0.0), (N_INPUT, 0, 0.0), (N_INPUT, 0, 0.0)], 1, "not one pre-order tree"),
+])
+def test_emit_hip_rejects_malformed_trees(nodes, n_in, msg):
+    with pytest.raises(M.MFHError, match=msg):
+        M.FusedKernel(nodes, [(M.FLOAT32, M.OPERAND_FULL, 0)] * n_in, M.FLOAT32, "bad")
+
+
+def test_emit_hip_rejects_bad_dtypes_and_periods():
+    relu = flatten((N_RELU, ("in", 0)))
+    with pytest.raises(M.MFHError, match="output dtype"):
+        M.FusedKernel(relu, [(M.FLOAT32, M.OPERAND_FULL, 0)], M.F8E4M3, "x")
+    with pytest.raises(M.MFHError, match="input 0 dtype"):
+        M.FusedKernel(relu, [(M.INT32, M.OPERAND_FULL, 0)], M.FLOAT32, "x")
+    with pytest.raises(M.MFHError, match="period must be positive"):
+        M.FusedKernel(relu, [(M.FLOAT32, M.OPERAND_PERIODIC, 0)], M.FLOAT32, "x")
+
+
+def test_launch_rejects_input_count_like_the_cpu_kernel():
+    # codegen/codegen_test.go:52-56: "expects 2 inputs".
+    k = M.FusedKernel(flatten((N_RELU, (N_ADD, ("in", 0), ("in", 1)))),
+                      [(M.FLOAT32, M.OPERAND_FULL, 0)] * 2, M.FLOAT32, "result")
+    with pytest.raises(M.MFHError, match='kernel "result" expects 2 inputs, got 1'):
+        k.launch([1], 2, 2)
+
+
+def test_entry_points_require_init():
+    # Without mfh_init every device entry point fails cleanly.
+    if M.lib().mfh_capabilities(None, None, None) == 0:
+        pytest.skip("library already initialised on a device")
+    with pytest.raises(M.MFHError, match="mfh_init has not been called"):
+        M.dequant_fp8(1, M.BFLOAT16, 1, M.F8E4M3, 16, 1.0)
+    M.axpy(1, 1, 4, 1.0, M.FLOAT32)  # no error channel: the failure is sticky
+    with pytest.raises(M.MFHError, match="mfh_init has not been called"):
+        M.take_sticky_error()
+    M.take_sticky_error()  # cleared
+
+
+def _device_asm(source: str, tmp_path) -> str:
+    src = tmp_path / "k.hip"
+    src.write_text("#include <hip/hip_runtime.h>\n" + source)  # hiprtc pre-includes it
+    asm = tmp_path / "k.s"
+    cmd = ["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+           "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", str(src), "-o", str(asm)]
+    subprocess.run(cmd, check=True, capture_output=True)
+    return asm.read_text()
+
+
+def test_generated_arithmetic_is_not_contracted(tmp_path):
+    # Sub(Mul(x, y), z): Go rounds the product before the subtraction.
+    nodes = flatten((N_SUB, (N_MUL, ("in", 0), ("in", 1)), ("in", 2)))
+    k = M.FusedKernel(nodes, [(M.FLOAT32, M.OPERAND_FULL, 0)] * 3, M.FLOAT32, "fms")
+    asm = _device_asm(k.source, tmp_path)
+    body = asm[asm.index("fused_fms:"):]
+    assert "v_mul_f32" in body and "v_sub_f32" in body
+    assert not re.search(r"v_fma_f32|v_fmac_f32|v_mad_f32|v_pk_(fma|mul|add)_f32", body)
+
+
+def test_generated_activation_chain_uses_no_packed_fp32(tmp_path):
+    nodes = flatten((N_LEAKY_RELU, (N_ADD, (N_SIGMOID, ("in", 0)), (N_EXP, ("in", 1)))))
+    k = M.FusedKernel(nodes, [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "act")
+    asm = _device_asm(k.source, tmp_path)
+    assert not re.search(r"v_pk_(fma|mul|add)_f32", asm)

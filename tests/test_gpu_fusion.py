@@ -1,0 +1,207 @@
+"""GPU parity: JIT-compiled fused elementwise kernels (EmitHIP) against the
+CPU evaluator (codegen/cpu.go:59-214).
+
+Tolerances (the reference runs Sigmoid/Silu/Gelu/Exp/Log/Tanh in f64 and
+rounds once to f32): arithmetic, select and sqrt nodes bit-exact;
+Exp/Log/Tanh and Sigmoid <= 1 f32 ulp; Silu and Gelu <= 2 f32 ulp; results
+narrowed to bf16/f16 <= 1 ulp of the storage dtype.  FMA contraction is off.
+NaN results must be NaN where the oracle's are; NaN payloads of fused-chain
+results are not compared.  Where the reference's gelu form cancels
+(1 + tanh(inner) with inner < -9.3, i.e. v < -4.9) its f64 result is
+quantised to multiples of 2^-53 * |v|/2; there two runs of that same f64
+formula may differ by one quantum, so the check there is |diff| <= 2 quanta.
+"""
+import numpy as np
+import pytest
+
+import manifesto_amd as M
+import oracle as O
+
+from gpu_util import (compare_storage, empty_dev, log, oracle_run_parallel, stream, to_dev,
+                      to_host)
+
+pytestmark = pytest.mark.gpu
+
+SIZE = {O.FLOAT32: 4, O.BFLOAT16: 2, O.FLOAT16: 2}
+NP = {O.FLOAT32: np.float32, O.BFLOAT16: np.uint16, O.FLOAT16: np.uint16}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    M.init(0)
+
+
+def run_fused(nodes, operands, arrays, out_dt, count, flags=0, pads=None, name="f"):
+    """Compiles and launches one fusion; arrays are storage arrays.  `pads`
+    offsets each buffer by whole elements (so 16-byte alignment is lost but
+    element alignment is kept); the output gets the first input's offset."""
+    k = M.FusedKernel(nodes, operands, out_dt, name, flags)
+    pads = pads or [0] * len(arrays)
+    devs = [to_dev(a, pad=p * a.itemsize) for a, p in zip(arrays, pads)]
+    out_pad = (pads[0] if pads else 0) * SIZE[out_dt]
+    out, op = empty_dev(count * SIZE[out_dt], pad=out_pad)
+    k.launch([p for _, p in devs], op, count, stream())
+    got = to_host(out, NP[out_dt], pad=out_pad)
+    return got
+
+
+def test_relu_add_golden(golden):
+    g = golden["evaluator"]["relu_add"]
+    nodes = O.flatten((O.N_RELU, (O.N_ADD, ("in", 0), ("in", 1))))
+    got = run_fused(nodes, [(O.FLOAT32, 0, 0)] * 2,
+                    [np.array(g["x"], np.float32), np.array(g["y"], np.float32)], O.FLOAT32, 4)
+    assert got.tolist() == g["expected"]
+
+
+def probe_f32(n=1 << 20, seed=0):
+    rng = np.random.default_rng(seed)
+    a = np.concatenate([
+        rng.normal(0, 1, n // 4), rng.normal(0, 30, n // 4), rng.uniform(-120, 120, n // 4),
+        rng.integers(0, 2 ** 32, n // 4, dtype=np.uint64).astype(np.uint32).view(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 3e38, -3e38, 1.0, -1.0], np.float32),
+    ]).astype(np.float32)
+    return a
+
+
+@pytest.mark.parametrize("node", [O.N_ADD, O.N_SUB, O.N_MUL, O.N_DIV, O.N_MAX, O.N_MIN])
+def test_binary_nodes_bit_exact(node):
+    a = probe_f32(seed=1)
+    b = np.random.default_rng(2).permutation(a)
+    nodes = O.flatten((node, ("in", 0), ("in", 1)))
+    got = run_fused(nodes, [(O.FLOAT32, 0, 0)] * 2, [a, b], O.FLOAT32, a.size)
+    want = O.eval_binary(node, a, b)
+    compare_storage(got, want, O.FLOAT32, 0, f"node {node}")
+    if node in (O.N_MAX, O.N_MIN):  # select semantics keep the exact bits
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("node", [O.N_NEG, O.N_ABS, O.N_RELU, O.N_LEAKY_RELU, O.N_SQRT])
+def test_exact_unary_nodes(node):
+    a = probe_f32(seed=3)
+    got = run_fused(O.flatten((node, ("in", 0))), [(O.FLOAT32, 0, 0)], [a], O.FLOAT32, a.size)
+    want = O.eval_unary(node, a)
+    compare_storage(got, want, O.FLOAT32, 0, f"node {node}")
+
+
+def all_16bit_as_f32():
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    return np.concatenate([O.bytes_to_f32(O.BFLOAT16, codes), O.bytes_to_f32(O.FLOAT16, codes)])
+
+
+def strided_f32(stride=1021):
+    u = np.arange(0, 2 ** 32, stride, dtype=np.uint64).astype(np.uint32)
+    return u.view(np.float32)
+
+
+TOL = {O.N_EXP: 1, O.N_LOG: 1, O.N_TANH: 1, O.N_SIGMOID: 1, O.N_SILU: 2, O.N_GELU: 2}
+
+
+def gelu_quantum_ok(v, got, want):
+    """In the cancellation range the reference result is a multiple of
+    2^-53 * |v| / 2; allow two such quanta there."""
+    q = np.abs(v.astype(np.float64)) * 2.0 ** -53
+    return (v < -4.9) & (np.abs(got.astype(np.float64) - want.astype(np.float64)) <= 2 * q)
+
+
+@pytest.mark.parametrize("flags", [0, M.FUSION_PRECISE])
+@pytest.mark.parametrize("node", [O.N_SIGMOID, O.N_SILU, O.N_GELU, O.N_EXP, O.N_LOG, O.N_TANH])
+def test_transcendental_nodes(node, flags):
+    v = np.concatenate([all_16bit_as_f32(), strided_f32(), probe_f32(1 << 18, seed=9)])
+    log(f"node {node} flags {flags} over {v.size} inputs")
+    got = run_fused(O.flatten((node, ("in", 0))), [(O.FLOAT32, 0, 0)], [v], O.FLOAT32, v.size, flags)
+    want = O.eval_unary(node, v)
+    tol = 1 if flags else TOL[node]
+    gn, wn = np.isnan(got), np.isnan(want)
+    bad = np.flatnonzero(gn != wn)
+    assert bad.size == 0, f"NaN mismatch at v={v[bad[:5]]} got={got[bad[:5]]} want={want[bad[:5]]}"
+    keep = ~wn
+    d = np.abs(O_key(got[keep]) - O_key(want[keep]))
+    if node == O.N_GELU:
+        d = np.where(gelu_quantum_ok(v[keep], got[keep], want[keep]), 0, d)
+    worst = int(d.max())
+    i = np.flatnonzero(keep)[int(np.argmax(d))]
+    log(f"node {node} flags {flags}: max ulp {worst} at v={v[i]!r}")
+    assert worst <= tol, f"{worst} ulp at v={v[i]!r}: got {got[i]!r} want {want[i]!r}"
+
+
+def O_key(f):
+    u = f.view(np.uint32).astype(np.int64)
+    return np.where(u & 0x80000000, 0x80000000 - u, u)
+
+
+def test_constants_and_deep_tree():
+    # LeakyReLU(Max(Div(Sub(x, 0.1), Sqrt(Abs(y))), Neg(Mul(Min(x, y), 3.7))))
+    tree = (O.N_LEAKY_RELU, (O.N_MAX,
+            (O.N_DIV, (O.N_SUB, ("in", 0), ("const", 0.1)), (O.N_SQRT, (O.N_ABS, ("in", 1)))),
+            (O.N_NEG, (O.N_MUL, (O.N_MIN, ("in", 0), ("in", 1)), ("const", 3.7)))))
+    nodes = O.flatten(tree)
+    rng = np.random.default_rng(21)
+    x = rng.normal(0, 5, 100003).astype(np.float32)
+    y = rng.normal(0, 5, 100003).astype(np.float32)
+    got = run_fused(nodes, [(O.FLOAT32, 0, 0)] * 2, [x, y], O.FLOAT32, x.size)
+    compare_storage(got, O.run(nodes, [x, y], x.size), O.FLOAT32, 0, "deep tree")
+
+
+@pytest.mark.parametrize("in_dt, out_dt", [(O.BFLOAT16, O.BFLOAT16), (O.FLOAT16, O.FLOAT16),
+                                           (O.BFLOAT16, O.FLOAT32), (O.FLOAT32, O.FLOAT16)])
+@pytest.mark.parametrize("count, pad", [(8 * 1000, 0), (8 * 1000 + 5, 0), (3, 0), (10001, 2)])
+def test_storage_dtypes_tails_misaligned(in_dt, out_dt, count, pad):
+    nodes = O.flatten((O.N_ADD, (O.N_MUL, (O.N_SILU, ("in", 0)), ("in", 1)), ("const", -0.5)))
+    rng = np.random.default_rng(count + pad)
+    g = O.encode(rng.normal(0, 2, count).astype(np.float32), in_dt)
+    u = O.encode(rng.normal(0, 2, count).astype(np.float32), in_dt)
+    got = run_fused(nodes, [(in_dt, 0, 0)] * 2, [g, u], out_dt, count, pads=[pad, pad])
+    want = O.encode(O.run(nodes, [O.decode(g, in_dt), O.decode(u, in_dt)], count), out_dt)
+    compare_storage(got, want, out_dt, 1, f"{in_dt}->{out_dt} n={count} pad={pad}")
+
+
+def test_swiglu_config3_full_size():
+    # silu(gate) * up, bf16 [8192, 14336] ~ N(0, 1) -> bf16.
+    n = 8192 * 14336
+    rng = np.random.default_rng(0x5EED + 3)
+    log("swiglu config 3: inputs")
+    gate = O.f32_to_bf16(rng.standard_normal(n, dtype=np.float32))
+    up = O.f32_to_bf16(rng.standard_normal(n, dtype=np.float32))
+    nodes = O.flatten((O.N_MUL, (O.N_SILU, ("in", 0)), ("in", 1)))
+    got = run_fused(nodes, [(O.BFLOAT16, 0, 0)] * 2, [gate, up], O.BFLOAT16, n, name="swiglu")
+    log("swiglu config 3: oracle")
+    want = O.f32_to_bf16(oracle_run_parallel(nodes, [O.decode(gate, O.BFLOAT16), O.decode(up, O.BFLOAT16)], n))
+    worst = compare_storage(got, want, O.BFLOAT16, 1, "swiglu config 3")
+    exact = np.mean(got == want)
+    log(f"swiglu config 3: max bf16 ulp {worst}, bit-identical fraction {exact:.6f}")
+    assert exact > 0.999
+
+
+def test_gelu_chain_config4_full_size():
+    # gelu_tanh((x + bias) * s) + residual, f16 [4, 4096, 4096],
+    # bias [4096] ~ N(0, 0.02) broadcast along rows, s = fl32(1.1) scalar -> f16.
+    n = 4 * 4096 * 4096
+    rng = np.random.default_rng(0x5EED + 4)
+    log("gelu chain config 4: inputs")
+    x = O.f32_to_f16(rng.standard_normal(n, dtype=np.float32))
+    res = O.f32_to_f16(rng.standard_normal(n, dtype=np.float32))
+    bias = O.f32_to_f16(rng.normal(0, 0.02, 4096).astype(np.float32))
+    s = np.array([1.1], dtype=np.float32)
+    nodes = O.flatten((O.N_ADD, (O.N_GELU, (O.N_MUL, (O.N_ADD, ("in", 0), ("in", 1)), ("in", 2))), ("in", 3)))
+    ops = [(O.FLOAT16, M.OPERAND_FULL, 0), (O.FLOAT16, M.OPERAND_PERIODIC, 4096),
+           (O.FLOAT32, M.OPERAND_SCALAR, 0), (O.FLOAT16, M.OPERAND_FULL, 0)]
+    got = run_fused(nodes, ops, [x, bias, s, res], O.FLOAT16, n, name="gelu_chain")
+    log("gelu chain config 4: oracle")
+    want = O.f32_to_f16(oracle_run_parallel(
+        nodes, [O.decode(x, O.FLOAT16), O.decode(bias, O.FLOAT16), s, O.decode(res, O.FLOAT16)], n,
+        periods=[0, 4096, 1, 0]))
+    worst = compare_storage(got, want, O.FLOAT16, 1, "gelu chain config 4")
+    exact = np.mean(got == want)
+    log(f"gelu chain config 4: max f16 ulp {worst}, bit-identical fraction {exact:.6f}")
+    assert exact > 0.999
+
+
+def test_periodic_operand_not_multiple_of_8():
+    # period 12 forces the element-wise path; results must still match.
+    nodes = O.flatten((O.N_ADD, ("in", 0), ("in", 1)))
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=12 * 1000).astype(np.float32)
+    b = rng.normal(size=12).astype(np.float32)
+    got = run_fused(nodes, [(O.FLOAT32, 0, 0), (O.FLOAT32, M.OPERAND_PERIODIC, 12)], [x, b], O.FLOAT32, x.size)
+    want = O.run(nodes, [x, b], x.size, periods=[0, 12])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
