@@ -43,6 +43,14 @@ int bind_device(const Device** out);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Streaming kernels with their own grid-size setting.
+enum class Kern { kFp8, kInt4, kAxpy, kAxpy16, kConvert, kFused, kCount };
+
+// Workgroups per CU for a grid-stride kernel: a per-kernel default measured
+// on MI355X, overridable for sweeps with MFH_BPC_<NAME> (NAME = FP8, INT4,
+// AXPY, AXPY16, CONVERT, FUSED) or MFH_BLOCKS_PER_CU for all of them.
+int blocks_per_cu(Kern k);
+
 }  // namespace mfh
 
 #define MFH_TRY(expr)                  \

@@ -1,27 +1,46 @@
 // dequant.hip — FP8 / Int4 dequantisation and dtype conversion for gfx950.
 //
-// All three are HBM-bound streams.  Each thread moves 16-byte vectors
-// (global_load/store_dwordx4) in a grid-stride loop; a scalar tail loop
-// finishes counts that are not a multiple of the vector width, and the same
-// loop does everything when a pointer is not 16-byte aligned.
+// All of these are HBM streams.  A work item is the input that produces one
+// 16-byte output vector; item i of every thread sits next to item i of its
+// neighbours, so each store instruction of a wave writes 1 KiB contiguously
+// and each load instruction reads a contiguous span.  Threads take U items
+// per grid-stride step (loads first, then converts and stores).  A scalar
+// loop finishes the elements after the last whole item, and does all of them
+// when a pointer is not aligned for the vector path.
 //
 // FP8: the output for a code depends only on (code, format, scale), so each
 // workgroup first builds the 256-entry table in LDS with the exact rules of
-// codec.hpp and then every element is one LDS lookup.
+// codec.hpp; every element is then one LDS read.
 #include <cstdlib>
+#include <cstring>
 
 #include "launch.hpp"
 
 namespace mfh {
 
-int blocks_per_cu()
+int blocks_per_cu(Kern k)
 {
-    static const int value = [] {
-        const char* env = std::getenv("MFH_BLOCKS_PER_CU");
-        int v = env ? std::atoi(env) : 0;
-        return (v > 0 && v <= 64) ? v : 8;
-    }();
-    return value;
+    struct Table {
+        int v[(int)Kern::kCount];
+        Table()
+        {
+            // Defaults measured on MI355X (256 CUs): writes-heavy streams want
+            // a few hundred KB to a few MB in flight, not full occupancy.
+            static const char* names[] = {"FP8", "INT4", "AXPY", "AXPY16", "CONVERT", "FUSED"};
+            static const int defaults[] = {8, 4, 2, 2, 4, 8};
+            const char* all = std::getenv("MFH_BLOCKS_PER_CU");
+            for (int i = 0; i < (int)Kern::kCount; i++) {
+                char key[64];
+                snprintf(key, sizeof key, "MFH_BPC_%s", names[i]);
+                const char* env = std::getenv(key);
+                if (!env) env = all;
+                int x = env ? std::atoi(env) : 0;
+                v[i] = (x > 0 && x <= 64) ? x : defaults[i];
+            }
+        }
+    };
+    static const Table table;
+    return table.v[(int)k];
 }
 
 int launch_status(const char* what) { return check_hip(hipGetLastError(), what); }
@@ -37,6 +56,13 @@ MFH_DEV mfh_u32 encode_one(float v)
 }
 
 template <int OUT>
+MFH_DEV mfh_u32 encode_pair(float lo, float hi)
+{
+    if constexpr (OUT == kBFloat16) return mfh_bf16x2_rne(lo, hi);
+    else return mfh_f16x2_rne(lo, hi);
+}
+
+template <int OUT>
 MFH_DEV void store_one(void* out, mfh_i64 i, mfh_u32 enc)
 {
     if constexpr (OUT == kFloat32) static_cast<mfh_u32*>(out)[i] = enc;
@@ -47,7 +73,8 @@ MFH_DEV void store_one(void* out, mfh_i64 i, mfh_u32 enc)
 // FP8 -> {f32, bf16, f16}
 // ---------------------------------------------------------------------------
 
-template <int OUT>
+// Item = 8 codes (16-bit output) or 4 codes (f32 output) -> one 16-byte store.
+template <int OUT, int U>
 __global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict__ in,
                                                         void* __restrict__ out, mfh_i64 n,
                                                         float scale, int fmt, int vec_ok)
@@ -60,35 +87,36 @@ __global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict
     }
     __syncthreads();
 
+    constexpr int kCodes = OUT == kFloat32 ? 4 : 8;
     const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
-    const mfh_i64 nvec = vec_ok ? (n >> 4) : 0;
-    const u32x4* src = reinterpret_cast<const u32x4*>(in);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + t; v < nvec; v += stride) {
-        u32x4 w = src[v];
-        if constexpr (OUT == kFloat32) {
-            u32x4* dst = reinterpret_cast<u32x4*>(out) + 4 * v;
+    const mfh_i64 nitems = vec_ok ? n / kCodes : 0;
+    u32x4* dst = reinterpret_cast<u32x4*>(out);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + t; v < nitems; v += stride * U) {
+        u32x2 w[U];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                mfh_u32 x = w[q];
-                u32x4 o = {lut[x & 0xffu], lut[(x >> 8) & 0xffu], lut[(x >> 16) & 0xffu], lut[x >> 24]};
-                dst[q] = o;
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i < nitems) {
+                if constexpr (kCodes == 8) w[u] = reinterpret_cast<const u32x2*>(in)[i];
+                else w[u] = u32x2{reinterpret_cast<const mfh_u32*>(in)[i], 0u};
             }
-        } else {
-            u32x4* dst = reinterpret_cast<u32x4*>(out) + 2 * v;
-            mfh_u32 p[8];
+        }
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                mfh_u32 x = w[q];
-                p[2 * q] = lut[x & 0xffu] | (lut[(x >> 8) & 0xffu] << 16);
-                p[2 * q + 1] = lut[(x >> 16) & 0xffu] | (lut[x >> 24] << 16);
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i >= nitems) break;
+            mfh_u32 x = w[u][0], y = w[u][1];
+            if constexpr (OUT == kFloat32) {
+                dst[i] = u32x4{lut[x & 0xffu], lut[(x >> 8) & 0xffu], lut[(x >> 16) & 0xffu], lut[x >> 24]};
+            } else {
+                dst[i] = u32x4{lut[x & 0xffu] | (lut[(x >> 8) & 0xffu] << 16),
+                               lut[(x >> 16) & 0xffu] | (lut[x >> 24] << 16),
+                               lut[y & 0xffu] | (lut[(y >> 8) & 0xffu] << 16),
+                               lut[(y >> 16) & 0xffu] | (lut[y >> 24] << 16)};
             }
-            u32x4 o0 = {p[0], p[1], p[2], p[3]};
-            u32x4 o1 = {p[4], p[5], p[6], p[7]};
-            dst[0] = o0;
-            dst[1] = o1;
         }
     }
-    for (mfh_i64 i = nvec * 16 + (mfh_i64)blockIdx.x * kBlock + t; i < n; i += stride)
+    for (mfh_i64 i = nitems * kCodes + (mfh_i64)blockIdx.x * kBlock + t; i < n; i += stride)
         store_one<OUT>(out, i, lut[in[i]]);
 }
 
@@ -107,66 +135,51 @@ MFH_DEV float load_scale(const void* scales, mfh_i64 g)
 
 MFH_DEV bool finite_f32(float f) { return (mfh_bits(f) & 0x7f800000u) != 0x7f800000u; }
 
-// One 16-byte vector = 32 nibbles = 32 outputs sharing one scale.
-template <int OUT>
-MFH_DEV void int4_vector(u32x4 w, float s, void* out, mfh_i64 v)
-{
-    const bool fast = finite_f32(s);  // then no product is NaN
-    if constexpr (OUT == kFloat32) {
-        u32x4* dst = reinterpret_cast<u32x4*>(out) + 8 * v;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            float f[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                float qv = (float)mfh_int4_at(w[q], k);
-                f[k] = fast ? qv * s : mfh_scale_mul(qv, s);
-            }
-            u32x4 a = {mfh_bits(f[0]), mfh_bits(f[1]), mfh_bits(f[2]), mfh_bits(f[3])};
-            u32x4 b = {mfh_bits(f[4]), mfh_bits(f[5]), mfh_bits(f[6]), mfh_bits(f[7])};
-            dst[2 * q] = a;
-            dst[2 * q + 1] = b;
-        }
-    } else {
-        u32x4* dst = reinterpret_cast<u32x4*>(out) + 4 * v;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            mfh_u32 p[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                float lo = (float)mfh_int4_at(w[q], 2 * k);
-                float hi = (float)mfh_int4_at(w[q], 2 * k + 1);
-                if (fast) {
-                    lo = lo * s;
-                    hi = hi * s;
-                } else {
-                    lo = mfh_scale_mul(lo, s);
-                    hi = mfh_scale_mul(hi, s);
-                }
-                if constexpr (OUT == kBFloat16) p[k] = mfh_bf16x2_rne(lo, hi);
-                else p[k] = mfh_f16_rne(lo) | (mfh_f16_rne(hi) << 16);
-            }
-            u32x4 o = {p[0], p[1], p[2], p[3]};
-            dst[q] = o;
-        }
-    }
-}
-
-template <int OUT, int SDT>
+// Item = 8 nibbles (4 packed bytes, 16-bit output) or 4 nibbles (2 bytes,
+// f32 output) sharing one scale -> one 16-byte store.
+template <int OUT, int SDT, int U>
 __global__ __launch_bounds__(kBlock) void k_dequant_int4(const mfh_u8* __restrict__ packed,
                                                          const void* __restrict__ scales,
                                                          void* __restrict__ out, mfh_i64 n,
-                                                         mfh_i64 group, int vec_ok)
+                                                         mfh_i64 group, int group_shift, int vec_ok)
 {
+    constexpr int kElems = OUT == kFloat32 ? 4 : 8;
     const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
-    const mfh_i64 nvec = vec_ok ? (n >> 5) : 0;
-    const u32x4* src = reinterpret_cast<const u32x4*>(packed);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
-        u32x4 w = src[v];
-        float s = load_scale<SDT>(scales, (v * 32) / group);
-        int4_vector<OUT>(w, s, out, v);
+    const mfh_i64 nitems = vec_ok ? n / kElems : 0;
+    u32x4* dst = reinterpret_cast<u32x4*>(out);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride * U) {
+        mfh_u32 w[U];
+        float s[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i < nitems) {
+                if constexpr (kElems == 8) w[u] = reinterpret_cast<const mfh_u32*>(packed)[i];
+                else w[u] = reinterpret_cast<const mfh_u16*>(packed)[i];
+                mfh_i64 e = i * kElems;
+                s[u] = load_scale<SDT>(scales, group_shift >= 0 ? (e >> group_shift) : e / group);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i >= nitems) break;
+            float f[kElems];
+            if (finite_f32(s[u])) {  // then every product is finite: one IEEE multiply
+#pragma unroll
+                for (int k = 0; k < kElems; k++) f[k] = (float)mfh_int4_at(w[u], k) * s[u];
+            } else {
+#pragma unroll
+                for (int k = 0; k < kElems; k++) f[k] = mfh_scale_mul((float)mfh_int4_at(w[u], k), s[u]);
+            }
+            if constexpr (OUT == kFloat32)
+                dst[i] = u32x4{mfh_bits(f[0]), mfh_bits(f[1]), mfh_bits(f[2]), mfh_bits(f[3])};
+            else
+                dst[i] = u32x4{encode_pair<OUT>(f[0], f[1]), encode_pair<OUT>(f[2], f[3]),
+                               encode_pair<OUT>(f[4], f[5]), encode_pair<OUT>(f[6], f[7])};
+        }
     }
-    for (mfh_i64 i = nvec * 32 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    for (mfh_i64 i = nitems * kElems + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         mfh_u32 byte = packed[i >> 1];
         float q = (float)mfh_int4_at(byte, (mfh_u32)(i & 1));
         float s = load_scale<SDT>(scales, i / group);
@@ -215,60 +228,51 @@ __global__ __launch_bounds__(kBlock) void k_convert(const void* __restrict__ in,
         store_one<OUT>(out, i, encode_one<OUT>(decode_at<IN>(in, i)));
 }
 
-// 16-bit storage -> 16-bit storage, eight elements per thread (the cast that
-// sits between a bf16/f16 tensor and an f32 fusion in the reference).
+template <int IN>
+MFH_DEV float dec16(mfh_u32 h)
+{
+    return IN == kBFloat16 ? mfh_bf16_to_f32(h) : mfh_f16_to_f32(h);
+}
+
+// 16-bit storage -> any output, one 16-byte store per item: 8 elements for a
+// 16-bit output, 4 for f32.  (The cast that sits between a bf16/f16 tensor and
+// an f32 fusion in the reference.)
 template <int IN, int OUT>
-__global__ __launch_bounds__(kBlock) void k_convert16_vec(const u32x4* __restrict__ in,
-                                                          void* __restrict__ out, mfh_i64 nvec)
+__global__ __launch_bounds__(kBlock) void k_convert16_vec(const void* __restrict__ in, void* __restrict__ out,
+                                                          mfh_i64 nitems)
 {
     const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
-        u32x4 w = in[v];
-        float f[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            mfh_u32 h = (w[k / 2] >> (16 * (k & 1))) & 0xffffu;
-            f[k] = IN == kBFloat16 ? mfh_bf16_to_f32(h) : mfh_f16_to_f32(h);
-        }
+    u32x4* dst = reinterpret_cast<u32x4*>(out);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
         if constexpr (OUT == kFloat32) {
-            u32x4* dst = reinterpret_cast<u32x4*>(out) + 2 * v;
-            u32x4 a = {mfh_bits(f[0]), mfh_bits(f[1]), mfh_bits(f[2]), mfh_bits(f[3])};
-            u32x4 b = {mfh_bits(f[4]), mfh_bits(f[5]), mfh_bits(f[6]), mfh_bits(f[7])};
-            dst[0] = a;
-            dst[1] = b;
+            u32x2 w = reinterpret_cast<const u32x2*>(in)[v];
+            dst[v] = u32x4{mfh_bits(dec16<IN>(w[0] & 0xffffu)), mfh_bits(dec16<IN>(w[0] >> 16)),
+                           mfh_bits(dec16<IN>(w[1] & 0xffffu)), mfh_bits(dec16<IN>(w[1] >> 16))};
         } else {
-            mfh_u32 p[4];
+            u32x4 w = reinterpret_cast<const u32x4*>(in)[v];
+            u32x4 o;
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-                p[k] = OUT == kBFloat16 ? mfh_bf16x2_rne(f[2 * k], f[2 * k + 1])
-                                        : (mfh_f16_rne(f[2 * k]) | (mfh_f16_rne(f[2 * k + 1]) << 16));
-            u32x4 o = {p[0], p[1], p[2], p[3]};
-            reinterpret_cast<u32x4*>(out)[v] = o;
+            for (int k = 0; k < 4; k++) o[k] = encode_pair<OUT>(dec16<IN>(w[k] & 0xffffu), dec16<IN>(w[k] >> 16));
+            dst[v] = o;
         }
     }
 }
 
-// f32 -> 16-bit storage, eight elements per thread.
+// f32 -> 16-bit storage, 4 elements per item (16-byte load, 8-byte store).
 template <int OUT>
 __global__ __launch_bounds__(kBlock) void k_narrow_f32_vec(const u32x4* __restrict__ in,
-                                                           u32x4* __restrict__ out, mfh_i64 nvec)
+                                                           u32x2* __restrict__ out, mfh_i64 nitems)
 {
     const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
-        u32x4 a = in[2 * v], b = in[2 * v + 1];
-        float f[8] = {mfh_f32(a[0]), mfh_f32(a[1]), mfh_f32(a[2]), mfh_f32(a[3]),
-                      mfh_f32(b[0]), mfh_f32(b[1]), mfh_f32(b[2]), mfh_f32(b[3])};
-        mfh_u32 p[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-            p[k] = OUT == kBFloat16 ? mfh_bf16x2_rne(f[2 * k], f[2 * k + 1])
-                                    : (mfh_f16_rne(f[2 * k]) | (mfh_f16_rne(f[2 * k + 1]) << 16));
-        u32x4 o = {p[0], p[1], p[2], p[3]};
-        out[v] = o;
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
+        u32x4 a = in[v];
+        out[v] = u32x2{encode_pair<OUT>(mfh_f32(a[0]), mfh_f32(a[1])), encode_pair<OUT>(mfh_f32(a[2]), mfh_f32(a[3]))};
     }
 }
 
 bool is_out_dtype(int dt) { return dt == kFloat32 || dt == kBFloat16 || dt == kFloat16; }
+
+bool aligned(const void* p, unsigned bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
 
 template <template <int> class F, typename... A>
 int by_out(int out_dt, A... args)
@@ -281,33 +285,47 @@ int by_out(int out_dt, A... args)
     }
 }
 
+constexpr int kFp8U = 2;
+constexpr int kInt4U = 2;
+
 template <int OUT>
 struct Fp8Launch {
     static int run(const Device* dev, void* out, const void* in, int fmt, int64_t n, float scale,
                    hipStream_t stream)
     {
-        int vec_ok = aligned16(in) && aligned16(out);
-        int64_t items = vec_ok ? std::max<int64_t>(n >> 4, 1) : n;
-        k_dequant_fp8<OUT><<<grid_for(items, dev), kBlock, 0, stream>>>(
+        constexpr int codes = OUT == kFloat32 ? 4 : 8;
+        int vec_ok = aligned(in, codes) && aligned16(out);
+        int64_t items = vec_ok ? std::max<int64_t>(n / codes, 1) : n;
+        k_dequant_fp8<OUT, kFp8U><<<grid_for(items, dev, Kern::kFp8, kFp8U), kBlock, 0, stream>>>(
             static_cast<const mfh_u8*>(in), out, n, scale, fmt, vec_ok);
         return launch_status("k_dequant_fp8");
     }
 };
+
+int log2_exact(int64_t g)
+{
+    if (g <= 0 || (g & (g - 1)) != 0) return -1;
+    int s = 0;
+    while ((int64_t(1) << s) < g) s++;
+    return s;
+}
 
 template <int OUT>
 struct Int4Launch {
     static int run(const Device* dev, void* out, const void* packed, int64_t n, const void* scales,
                    int scale_dt, int64_t group, hipStream_t stream)
     {
-        int vec_ok = aligned16(packed) && aligned16(out) && group % 32 == 0;
-        int64_t items = vec_ok ? std::max<int64_t>(n >> 5, 1) : n;
-        unsigned grid = grid_for(items, dev);
+        constexpr int elems = OUT == kFloat32 ? 4 : 8;
+        int vec_ok = aligned(packed, elems / 2) && aligned16(out) && group % elems == 0;
+        int64_t items = vec_ok ? std::max<int64_t>(n / elems, 1) : n;
+        unsigned grid = grid_for(items, dev, Kern::kInt4, kInt4U);
+        int shift = log2_exact(group);
         const mfh_u8* p = static_cast<const mfh_u8*>(packed);
         switch (scale_dt) {
-        case kFloat32: k_dequant_int4<OUT, kFloat32><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, vec_ok); break;
-        case kFloat16: k_dequant_int4<OUT, kFloat16><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, vec_ok); break;
-        case kBFloat16: k_dequant_int4<OUT, kBFloat16><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, vec_ok); break;
-        default: k_dequant_int4<OUT, kInvalid><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, vec_ok); break;
+        case kFloat32: k_dequant_int4<OUT, kFloat32, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
+        case kFloat16: k_dequant_int4<OUT, kFloat16, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
+        case kBFloat16: k_dequant_int4<OUT, kBFloat16, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
+        default: k_dequant_int4<OUT, kInvalid, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
         }
         return launch_status("k_dequant_int4");
     }
@@ -317,23 +335,23 @@ template <int OUT>
 struct ConvertLaunch {
     static int run(const Device* dev, void* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
     {
-        if ((in_dt == kBFloat16 || in_dt == kFloat16) && aligned16(in) && aligned16(out) && n % 8 == 0) {
-            int64_t nvec = n / 8;
-            const u32x4* src = static_cast<const u32x4*>(in);
-            unsigned grid = grid_for(nvec, dev);
-            if (in_dt == kBFloat16) k_convert16_vec<kBFloat16, OUT><<<grid, kBlock, 0, stream>>>(src, out, nvec);
-            else k_convert16_vec<kFloat16, OUT><<<grid, kBlock, 0, stream>>>(src, out, nvec);
+        constexpr int per = OUT == kFloat32 ? 4 : 8;
+        if ((in_dt == kBFloat16 || in_dt == kFloat16) && aligned(in, per * 2) && aligned16(out) && n % per == 0) {
+            int64_t nitems = n / per;
+            unsigned grid = grid_for(nitems, dev, Kern::kConvert);
+            if (in_dt == kBFloat16) k_convert16_vec<kBFloat16, OUT><<<grid, kBlock, 0, stream>>>(in, out, nitems);
+            else k_convert16_vec<kFloat16, OUT><<<grid, kBlock, 0, stream>>>(in, out, nitems);
             return launch_status("k_convert16_vec");
         }
         if constexpr (OUT != kFloat32) {
-            if (in_dt == kFloat32 && aligned16(in) && aligned16(out) && n % 8 == 0) {
-                int64_t nvec = n / 8;
-                k_narrow_f32_vec<OUT><<<grid_for(nvec, dev), kBlock, 0, stream>>>(
-                    static_cast<const u32x4*>(in), static_cast<u32x4*>(out), nvec);
+            if (in_dt == kFloat32 && aligned16(in) && aligned(out, 8) && n % 4 == 0) {
+                int64_t nitems = n / 4;
+                k_narrow_f32_vec<OUT><<<grid_for(nitems, dev, Kern::kConvert), kBlock, 0, stream>>>(
+                    static_cast<const u32x4*>(in), static_cast<u32x2*>(out), nitems);
                 return launch_status("k_narrow_f32_vec");
             }
         }
-        unsigned grid = grid_for(n, dev);
+        unsigned grid = grid_for(n, dev, Kern::kConvert);
         switch (in_dt) {
 #define MFH_CONVERT_CASE(DT) \
     case DT: k_convert<DT, OUT><<<grid, kBlock, 0, stream>>>(in, out, n); break;
@@ -373,6 +391,8 @@ int mfh_dequant_fp8(void* out, uint8_t out_dtype, const void* in, uint8_t fp8_dt
     if (fp8_dtype != kF8E4M3 && fp8_dtype != kF8E5M2)
         return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_dequant_fp8: %s is not an FP8 dtype", dtype_name(fp8_dtype));
     if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_dequant_fp8: negative count %lld", (long long)count);
+    if (!is_out_dtype(out_dtype))
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "output dtype %s is not f32/bf16/f16", dtype_name(out_dtype));
     if (count == 0) return MFH_OK;
     if (!out || !in) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_dequant_fp8: NULL buffer");
     return by_out<Fp8Launch>(out_dtype, dev, out, in, (int)fp8_dtype, count, scale, (hipStream_t)stream);
@@ -388,6 +408,8 @@ int mfh_dequant_int4(void* out, uint8_t out_dtype, const void* packed, int64_t c
                     dtype_name(scale_dtype));
     if (group <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_dequant_int4: group must be positive, got %lld", (long long)group);
     if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_dequant_int4: negative count %lld", (long long)count);
+    if (!is_out_dtype(out_dtype))
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "output dtype %s is not f32/bf16/f16", dtype_name(out_dtype));
     if (count == 0) return MFH_OK;
     if (!out || !packed || !scales) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_dequant_int4: NULL buffer");
     return by_out<Int4Launch>(out_dtype, dev, out, packed, count, scales, (int)scale_dtype, group,

@@ -9,14 +9,16 @@
 // f32 with error-free corrections and stay within 2 f32 ulps of that; the
 // MFH_FUSION_PRECISE forms (mfh_*_ref) restate the f64 formulas.
 //
-//   e^a, a <= 0:  Cody & Waite reduction a = k ln2 + r (ln2 split into a
+//   e^a:          Cody & Waite reduction a = k ln2 + r (ln2 split into a
 //                 16-bit head and an f32 tail), e^r by a degree-6 polynomial
-//                 (constants from gen_exp_poly.py), result kept as p * 2^k so
-//                 that nothing underflows before the final scaling.
-//   v * sigmoid(z) = v / (1 + e^-z)            for z >= 0
-//                  = (v p / (1 + p 2^k)) 2^k   for z < 0, e^z = p 2^k
-//                 with the quotient corrected by one residual step that also
-//                 absorbs the rounding of 1 + e^-|z| and of v p.
+//                 (constants from gen_exp_poly.py), then scaled by 2^k.
+//   n * sigmoid(z) = n / (1 + E), E = e^-z, with z clamped (v_med3) to the
+//                 range where E is a finite f32, the exact tail of 1 + E
+//                 recovered by Fast2Sum, and the quotient corrected by one
+//                 residual step.  Arguments below that range (where the
+//                 result underflows or the reference cancels) and NaN take
+//                 the f64 reference form, a branch no wave enters for normal
+//                 data.
 #ifndef MFH_DEVMATH_HPP
 #define MFH_DEVMATH_HPP
 
@@ -26,15 +28,15 @@
 #define mfh_fmaf(a, b, c) std::fma((float)(a), (float)(b), (float)(c))
 #define mfh_fma(a, b, c) std::fma((double)(a), (double)(b), (double)(c))
 #define mfh_rintf(x) std::nearbyint((float)(x))
-#define mfh_rint(x) std::nearbyint((double)(x))
 #define mfh_ldexpf(x, k) std::ldexp((float)(x), (int)(k))
 #define mfh_rcpf(x) (1.0f / (float)(x))
-#define mfh_fmax(a, b) std::fmax((double)(a), (double)(b))
-#define mfh_fmaxf(a, b) std::fmax((float)(a), (float)(b))
 #define mfh_tanh_f64(x) std::tanh((double)(x))
 #define mfh_exp_f64(x) std::exp((double)(x))
 #define mfh_log_f64(x) std::log((double)(x))
 #define mfh_sqrtf(x) std::sqrt((float)(x))
+#define MFH_KEEP(x) ((void)0)
+#define mfh_med3f(x, lo, hi) std::fmin(std::fmax((float)(x), (float)(lo)), (float)(hi))
+#define mfh_is_nan_or_inf_class(v) (std::isnan(v) || std::isinf(v))
 inline unsigned mfh_fbits(float f) { unsigned u; __builtin_memcpy(&u, &f, 4); return u; }
 inline float mfh_fromfbits(unsigned u) { float f; __builtin_memcpy(&f, &u, 4); return f; }
 #else
@@ -45,15 +47,17 @@ extern "C" __device__ double __ocml_log_f64(double);
 #define mfh_fmaf(a, b, c) __builtin_fmaf((a), (b), (c))
 #define mfh_fma(a, b, c) __builtin_fma((a), (b), (c))
 #define mfh_rintf(x) __builtin_rintf(x)
-#define mfh_rint(x) __builtin_rint(x)
 #define mfh_ldexpf(x, k) __builtin_amdgcn_ldexpf((x), (k))
 #define mfh_rcpf(x) __builtin_amdgcn_rcpf(x)
-#define mfh_fmax(a, b) __builtin_fmax((a), (b))
-#define mfh_fmaxf(a, b) __builtin_fmaxf((a), (b))
 #define mfh_tanh_f64(x) __ocml_tanh_f64(x)
 #define mfh_exp_f64(x) __ocml_exp_f64(x)
 #define mfh_log_f64(x) __ocml_log_f64(x)
 #define mfh_sqrtf(x) __builtin_sqrtf(x)
+// Pins a value in a VGPR at this point: keeps LLVM from sinking the whole
+// computation of x into a divergent branch around a cheap special-case
+// select (which serialises the unrolled elements).  Emits no instruction.
+#define MFH_KEEP(x) __asm__ volatile("" : "+v"(x))
+#define mfh_med3f(x, lo, hi) __builtin_amdgcn_fmed3f((x), (lo), (hi))
 __device__ inline unsigned mfh_fbits(float f) { return __builtin_bit_cast(unsigned, f); }
 __device__ inline float mfh_fromfbits(unsigned u) { return __builtin_bit_cast(float, u); }
 #endif
@@ -78,10 +82,9 @@ MFH_MATH float mfh_exp_poly(float r)
     return mfh_fmaf(q, r, 1.0f);
 }
 
-// e^a = p * 2^k for a <= 0 (a clamped at -200, far below the f32 range).
-MFH_MATH float mfh_exp_neg(float a, int* k)
+// e^a = p * 2^k, for a in [-200, 200].
+MFH_MATH float mfh_exp_core(float a, int* k)
 {
-    a = mfh_fmaxf(a, -200.0f);
     float kf = mfh_rintf(a * MFH_LOG2E_F);
     float r = mfh_fmaf(kf, -MFH_LN2_HI_F, a);
     r = mfh_fmaf(kf, -MFH_LN2_LO_F, r);
@@ -89,84 +92,101 @@ MFH_MATH float mfh_exp_neg(float a, int* k)
     return mfh_exp_poly(r);
 }
 
-// Same with an f64 argument: the reduction runs in f64, so the argument's
-// own f64 accuracy carries through to r.
-MFH_MATH float mfh_exp_neg_d(double a, int* k)
+// Same with an f64 argument (|a| < 2^30): the reduction runs in f64, so the
+// argument's own f64 accuracy carries through to r.
+MFH_MATH float mfh_exp_core_d(double a, int* k)
 {
-    a = mfh_fmax(a, -200.0);
-    double kd = mfh_rint(a * MFH_LOG2E_D);
+    const double magic = 6755399441055744.0;  // 1.5 * 2^52: (x + magic) - magic rounds x to an integer
+    double kd = (a * MFH_LOG2E_D + magic) - magic;
     double r = mfh_fma(kd, -MFH_LN2_D, a);
     *k = (int)kd;
     return mfh_exp_poly((float)r);
 }
 
-// n * sigmoid(z) given e^-|z| = p * 2^k, z_neg = (z < 0).
-MFH_MATH float mfh_mul_sigmoid(float n, bool z_neg, float p, int k)
+// n / (1 + E) for E = p * 2^k >= 0: Fast2Sum gives 1 + E = d + dl exactly,
+// then one residual step corrects the quotient for both d's rounding and the
+// reciprocal's error.
+MFH_MATH float mfh_div_one_plus(float n, float p, int k)
 {
-    float t = mfh_ldexpf(p, k);
-    float d = 1.0f + t;
-    float dl = t - (d - 1.0f);              // 1 + t == d + dl exactly
-    float nh = z_neg ? n * p : n;
-    float nl = z_neg ? mfh_fmaf(n, p, -nh) : 0.0f;
+    float e = mfh_ldexpf(p, k);
+    float d = 1.0f + e;
+    float big = e > 1.0f ? e : 1.0f;
+    float small = e > 1.0f ? 1.0f : e;
+    float dl = small - (d - big);
     float r = mfh_rcpf(d);
-    float q = nh * r;
-    float e = mfh_fmaf(-q, d, nh);
-    e = e + nl;
-    e = mfh_fmaf(-q, dl, e);
-    q = mfh_fmaf(e, r, q);
-    return z_neg ? mfh_ldexpf(q, k) : q;
+    float q = n * r;
+    float res = mfh_fmaf(-q, d, n);
+    res = mfh_fmaf(-q, dl, res);
+    return mfh_fmaf(res, r, q);
 }
 
-// The reference's results at +-Inf: silu/gelu(+Inf) = +Inf, (-Inf) = NaN
-// (Inf/Inf and Inf*0 in f64); sigmoid(+-Inf) = 1, 0.
 MFH_MATH bool mfh_is_inf(float v) { return (mfh_fbits(v) & 0x7fffffffu) == 0x7f800000u; }
-
-MFH_MATH float mfh_sigmoid(float v)
-{
-    int k;
-    float p = mfh_exp_neg(-__builtin_fabsf(v), &k);
-    float s = mfh_mul_sigmoid(1.0f, v < 0.0f, p, k);
-    return mfh_is_inf(v) ? (v > 0.0f ? 1.0f : 0.0f) : s;
-}
-
-MFH_MATH float mfh_silu(float v)
-{
-    int k;
-    float p = mfh_exp_neg(-__builtin_fabsf(v), &k);
-    float s = mfh_mul_sigmoid(v, v < 0.0f, p, k);
-    s = v < -200.0f ? -0.0f : s;  // v e^v is below the f32 range (and v p could overflow)
-    return mfh_is_inf(v) ? (v > 0.0f ? v : mfh_fromfbits(0xffc00000u)) : s;
-}
+MFH_MATH bool mfh_is_nan(float v) { return (mfh_fbits(v) & 0x7fffffffu) > 0x7f800000u; }
 
 // Reference forms (codegen/cpu.go:186-200), f64 then one rounding.
 MFH_MATH float mfh_sigmoid_ref(float v) { return (float)(1.0 / (1.0 + mfh_exp_f64(-(double)v))); }
 MFH_MATH float mfh_silu_ref(float v) { return (float)((double)v / (1.0 + mfh_exp_f64(-(double)v))); }
 
-// Kept out of line on the device: it runs only for rare inputs.
-#ifdef MFH_HOST_MATH
-inline float mfh_gelu_ref(float v)
-#else
-__device__ __attribute__((noinline)) float mfh_gelu_ref(float v)
-#endif
+// gelu in the reference's f64 form 0.5 v (1 + tanh(inner)).  For
+// inner <= -0.625 tanh is formed as -(1 - 2 / (e^(2|inner|) + 1)), the form in
+// which Go's math.Tanh (and glibc's) evaluates it there, because in that range
+// 1 + tanh cancels and its result carries the f64 quantum of exactly that
+// expression.  Elsewhere any faithful f64 tanh gives the same f32 result.
+MFH_MATH float mfh_gelu_ref(float v)
 {
     double d = (double)v;
     double inner = MFH_SQRT_2_OVER_PI_D * (d + MFH_GELU_A_D * d * d * d);
-    return (float)(0.5 * d * (1.0 + mfh_tanh_f64(inner)));
+    double th;
+    if (inner > -0.625) {
+        th = mfh_tanh_f64(inner);
+    } else {
+        double s = mfh_exp_f64(-2.0 * inner);
+        th = -(1.0 - 2.0 / (s + 1.0));
+    }
+    return (float)(0.5 * d * (1.0 + th));
 }
 
-// Below v = -4.9 the reference's 1 + tanh(inner) cancels in f64, so its
-// result carries the f64 quantum of tanh; that rare range runs the reference
-// form itself.  Elsewhere inner is formed in f64 with the reference's
-// operation order and gelu = v * sigmoid(2 inner).
+// sigmoid(v) = 1 / (1 + e^-v); below -87 (e^-v past the f32 range) and for
+// NaN the f64 form.  +Inf gives 1 by itself.
+MFH_MATH float mfh_sigmoid(float v)
+{
+    int k;
+    float p = mfh_exp_core(-mfh_med3f(v, -87.0f, 104.0f), &k);
+    float s = mfh_div_one_plus(1.0f, p, k);
+    MFH_KEEP(s);
+    if (!(v >= -87.0f)) s = mfh_sigmoid_ref(v);
+    return s;
+}
+
+// silu(v) = v / (1 + e^-v); below -87 (and -Inf, NaN) the f64 form, where the
+// result underflows to denormals and -0.  +Inf gives +Inf.
+MFH_MATH float mfh_silu(float v)
+{
+    int k;
+    float p = mfh_exp_core(-mfh_med3f(v, -87.0f, 104.0f), &k);
+    float s = mfh_div_one_plus(v, p, k);
+    MFH_KEEP(s);
+    s = v == __builtin_inff() ? v : s;
+    if (!(v >= -87.0f)) s = mfh_silu_ref(v);
+    return s;
+}
+
+// Fast gelu = v / (1 + e^-z), z = 2 inner, inner formed in f64 in the
+// reference's operation order.  Above v = 14 the reference's tanh is exactly 1
+// in f64 and gelu(v) = v, which the clamped z reproduces.  Below v = -4.9
+// (inner < -9.3) the reference's 1 + tanh cancels in f64, so that rare range
+// (and NaN) runs the reference form itself.
 MFH_MATH float mfh_gelu(float v)
 {
-    if (v < -4.9f) return mfh_gelu_ref(v);
-    double d = (double)v;
+    double d = (double)mfh_med3f(v, -5.0f, 14.0f);
     double z = 2.0 * (MFH_SQRT_2_OVER_PI_D * (d + MFH_GELU_A_D * d * d * d));
     int k;
-    float p = mfh_exp_neg_d(-__builtin_fabs(z), &k);
-    float s = mfh_mul_sigmoid(v, z < 0.0, p, k);
-    return mfh_is_inf(v) ? v : s;  // -Inf took the reference path
+    float p = mfh_exp_core_d(-z, &k);
+    float s = mfh_div_one_plus(v, p, k);
+    MFH_KEEP(s);
+    s = v == __builtin_inff() ? v : s;
+    if (!(v >= -4.9f)) s = mfh_gelu_ref(v);
+    return s;
 }
 
 MFH_MATH float mfh_exp_ref(float v) { return (float)mfh_exp_f64((double)v); }

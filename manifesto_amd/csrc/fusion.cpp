@@ -29,11 +29,8 @@ namespace mfh {
 
 #include "mfh_prelude.inc"  // kPrelude: codec.hpp + devmath.hpp + fusion_io.hpp
 
-int blocks_per_cu();  // dequant.hip
-
 namespace {
 
-constexpr int kVec = 8;
 constexpr int kBlockThreads = 256;
 
 const char* io_suffix(int dtype)
@@ -234,6 +231,8 @@ struct mfh_kernel {
     std::string source;
     std::vector<mfh_operand> inputs;
     uint8_t out_dtype = mfh::kFloat32;
+    int vec = 8;     // elements per work item
+    int unroll = 1;  // work items per thread per grid-stride step
     bool periods_vectorizable = true;
     std::shared_ptr<mfh::CodeObject> code;
 };
@@ -262,7 +261,9 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     if (link(list, 0, c0, c1) != n_nodes)
         return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: the node list is not one pre-order tree");
 
-    bool periods_vectorizable = true;
+    // Work item width: 8 elements when the output and every streamed operand
+    // are 16-bit (one 16-byte access per lane), 4 when any is f32.
+    int vec = out_dtype == kFloat32 ? 4 : 8;
     for (int k = 0; k < n_inputs; k++) {
         const mfh_operand& op = inputs[k];
         if (!io_suffix(op.dtype))
@@ -271,8 +272,20 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
             return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: input %d has unknown mode %d", k, op.mode);
         if (op.mode == MFH_OPERAND_PERIODIC && op.period <= 0)
             return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: input %d period must be positive", k);
-        if (op.mode == MFH_OPERAND_PERIODIC && op.period % kVec != 0) periods_vectorizable = false;
+        if (op.mode != MFH_OPERAND_SCALAR && op.dtype == kFloat32) vec = 4;
     }
+    bool periods_vectorizable = true;
+    for (int k = 0; k < n_inputs; k++)
+        if (inputs[k].mode == MFH_OPERAND_PERIODIC && inputs[k].period % vec != 0) periods_vectorizable = false;
+
+    // Items per thread per step: two when the chain is cheap arithmetic (more
+    // loads in flight), one when it has transcendental nodes (VALU-bound).
+    bool heavy = false;
+    for (const mfh_ast_node& nd : list)
+        if (nd.type == kNodeExp || nd.type == kNodeLog || nd.type == kNodeTanh || nd.type == kNodeSigmoid ||
+            nd.type == kNodeSilu || nd.type == kNodeGelu || nd.type == kNodeSqrt || nd.type == kNodeDiv)
+            heavy = true;
+    const int unroll = heavy ? 1 : 2;
 
     const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
     Emitter em{list, c0, c1, precise, "", 0};
@@ -281,11 +294,13 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     std::string identifier = output_port && *output_port ? output_port : "anon";
     std::string kernel_name = "fused_" + sanitize(output_port ? output_port : "");
     const char* osfx = io_suffix(out_dtype);
+    const std::string V = std::to_string(vec), U = std::to_string(unroll);
 
     std::string src;
     src.reserve(sizeof(kPrelude) + 4096);
     src += kPrelude;
-    src += "\n// EmitHIP: fusion '" + identifier + "'" + (precise ? " (precise transcendentals)" : "") + "\n";
+    src += "\n// EmitHIP: fusion '" + identifier + "'" + (precise ? " (precise transcendentals)" : "") +
+           ", " + V + " elements per item, " + U + " item(s) per thread per step\n";
     src += "extern \"C\" __global__ __launch_bounds__(256) void " + kernel_name + "(\n";
     for (int k = 0; k < n_inputs; k++) src += "    const void* __restrict__ p" + std::to_string(k) + ",\n";
     src += "    void* __restrict__ pout, mfh_i64 n, mfh_i64 nvec)\n{\n";
@@ -295,26 +310,33 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
         if (inputs[k].mode == MFH_OPERAND_SCALAR)
             src += "    const float s" + std::to_string(k) + " = mfh_ld1_" + io_suffix(inputs[k].dtype) + "(p" +
                    std::to_string(k) + ", 0);\n";
-    // vector loop
-    src += "    for (mfh_i64 v = tid; v < nvec; v += stride) {\n";
-    src += "        const mfh_i64 e0 = v * 8;\n";
+    // vector loop: loads of all items first, then compute and store
+    src += "    for (mfh_i64 v = tid; v < nvec; v += stride * " + U + ") {\n";
+    for (int k = 0; k < n_inputs; k++)
+        if (inputs[k].mode != MFH_OPERAND_SCALAR) src += "        float a" + std::to_string(k) + "[" + U + "][" + V + "];\n";
+    src += "#pragma unroll\n        for (int u = 0; u < " + U + "; u++) {\n";
+    src += "            const mfh_i64 it = v + u * stride;\n            if (it < nvec) {\n";
+    src += "                const mfh_i64 e0 = it * " + V + ";\n";
     for (int k = 0; k < n_inputs; k++) {
         if (inputs[k].mode == MFH_OPERAND_SCALAR) continue;
         std::string ks = std::to_string(k);
-        src += "        float a" + ks + "[8];\n";
-        src += "        mfh_ld8_" + std::string(io_suffix(inputs[k].dtype)) + "(p" + ks + ", " +
-               operand_index(inputs[k], "e0") + ", a" + ks + ");\n";
+        src += "                mfh_ld" + V + "_" + io_suffix(inputs[k].dtype) + "(p" + ks + ", " +
+               operand_index(inputs[k], "e0") + ", a" + ks + "[u]);\n";
     }
-    src += "        float r[8];\n#pragma unroll\n        for (int j = 0; j < 8; j++) {\n";
+    src += "            }\n        }\n";
+    src += "#pragma unroll\n        for (int u = 0; u < " + U + "; u++) {\n";
+    src += "            const mfh_i64 it = v + u * stride;\n            if (it >= nvec) break;\n";
+    src += "            float r[" + V + "];\n#pragma unroll\n            for (int j = 0; j < " + V + "; j++) {\n";
     for (int k = 0; k < n_inputs; k++) {
         std::string ks = std::to_string(k);
-        src += "        const float x" + ks + " = " + (inputs[k].mode == MFH_OPERAND_SCALAR ? "s" + ks : "a" + ks + "[j]") + ";\n";
+        src += "        const float x" + ks + " = " +
+               (inputs[k].mode == MFH_OPERAND_SCALAR ? "s" + ks : "a" + ks + "[u][j]") + ";\n";
     }
     src += em.body;
-    src += "        r[j] = " + result + ";\n        }\n";
-    src += std::string("        mfh_st8_") + osfx + "(pout, e0, r);\n    }\n";
+    src += "                r[j] = " + result + ";\n            }\n";
+    src += "            mfh_st" + V + "_" + osfx + "(pout, it * " + V + ", r);\n        }\n    }\n";
     // scalar tail (and the whole range when the vector path is off)
-    src += "    for (mfh_i64 i = nvec * 8 + tid; i < n; i += stride) {\n";
+    src += "    for (mfh_i64 i = nvec * " + V + " + tid; i < n; i += stride) {\n";
     for (int k = 0; k < n_inputs; k++) {
         std::string ks = std::to_string(k);
         if (inputs[k].mode == MFH_OPERAND_SCALAR)
@@ -332,6 +354,8 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     kernel->source = std::move(src);
     kernel->inputs.assign(inputs, inputs + n_inputs);
     kernel->out_dtype = out_dtype;
+    kernel->vec = vec;
+    kernel->unroll = unroll;
     kernel->periods_vectorizable = periods_vectorizable;
     MFH_TRY(compile_source(kernel->source, kernel_name, &kernel->code));
     *out = kernel.release();
@@ -350,18 +374,24 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
     MFH_TRY(bind_device(&dev));
     if (count == 0) return MFH_OK;
     if (!out) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: output buffer is NULL");
-    bool vec_ok = kernel->periods_vectorizable && aligned16(out);
+    // The vector path needs every streamed buffer aligned to one item's bytes.
+    auto item_aligned = [&](const void* p, int dtype) {
+        uintptr_t bytes = (uintptr_t)kernel->vec * (dtype == kFloat32 ? 4 : 2);
+        return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+    };
+    bool vec_ok = kernel->periods_vectorizable && item_aligned(out, kernel->out_dtype);
     for (int k = 0; k < n_inputs; k++) {
         if (!inputs[k])
             return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: input %d is NULL", k);
-        if (kernel->inputs[k].mode != MFH_OPERAND_SCALAR && !aligned16(inputs[k])) vec_ok = false;
+        if (kernel->inputs[k].mode != MFH_OPERAND_SCALAR && !item_aligned(inputs[k], kernel->inputs[k].dtype))
+            vec_ok = false;
     }
     hipFunction_t fn;
     MFH_TRY(load_function(*kernel->code, dev->ordinal, &fn));
-    int64_t nvec = vec_ok ? count / kVec : 0;
-    int64_t items = nvec > 0 ? nvec : count;
+    int64_t nvec = vec_ok ? count / kernel->vec : 0;
+    int64_t items = nvec > 0 ? (nvec + kernel->unroll - 1) / kernel->unroll : count;
     int64_t need = (items + kBlockThreads - 1) / kBlockThreads;
-    int64_t cap = (int64_t)dev->compute_units * blocks_per_cu();
+    int64_t cap = (int64_t)dev->compute_units * blocks_per_cu(Kern::kFused);
     unsigned grid = (unsigned)std::max<int64_t>(1, std::min(need, cap));
     std::vector<const void*> ptrs(inputs, inputs + n_inputs);
     std::vector<void*> args;

@@ -20,7 +20,7 @@ template <int DT>
 MFH_DEV mfh_u32 enc16x2(float lo, float hi)
 {
     if constexpr (DT == kBFloat16) return mfh_bf16x2_rne(lo, hi);
-    else return mfh_f16_rne(lo) | (mfh_f16_rne(hi) << 16);
+    else return mfh_f16x2_rne(lo, hi);
 }
 
 MFH_DEV float axpy_step(float y, float x, float alpha)
@@ -167,14 +167,14 @@ void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype,
     switch (dtype) {
     case kFloat32: {
         int64_t items = vec_ok ? std::max<int64_t>(count >> 2, 1) : count;
-        k_axpy_f32<<<grid_for(items, dev), kBlock, 0, s>>>(static_cast<float*>(y), static_cast<const float*>(x),
+        k_axpy_f32<<<grid_for(items, dev, Kern::kAxpy), kBlock, 0, s>>>(static_cast<float*>(y), static_cast<const float*>(x),
                                                            count, alpha, vec_ok);
         break;
     }
     case kBFloat16:
     case kFloat16: {
         int64_t items = vec_ok ? std::max<int64_t>(count >> 3, 1) : count;
-        unsigned grid = grid_for(items, dev);
+        unsigned grid = grid_for(items, dev, Kern::kAxpy16);
         auto* yy = static_cast<mfh_u16*>(y);
         auto* xx = static_cast<const mfh_u16*>(x);
         if (dtype == kBFloat16) k_axpy16<kBFloat16><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
@@ -202,7 +202,7 @@ int mfh_scalar_broadcast(void* out, uint8_t out_dtype, const void* in, uint8_t i
     if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: negative count");
     if (count == 0) return MFH_OK;
     if (!out || !in) return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: NULL buffer");
-    unsigned grid = grid_for(count, dev);
+    unsigned grid = grid_for(count, dev, Kern::kConvert);
     hipStream_t s = (hipStream_t)stream;
     switch (in_dtype) {
     case kFloat32: return launch_broadcast<kFloat32>(out_dtype, grid, s, out, in, count, scalar, op);
@@ -225,7 +225,7 @@ int mfh_linspace(void* out, uint8_t out_dtype, int64_t count, float start, float
     // count == 1 returns start itself; with the endpoint both ends are pinned.
     int pin_first = (count == 1 || endpoint) ? 1 : 0;
     int pin_last = (count > 1 && endpoint) ? 1 : 0;
-    unsigned grid = grid_for(count, dev);
+    unsigned grid = grid_for(count, dev, Kern::kConvert);
     hipStream_t s = (hipStream_t)stream;
     switch (out_dtype) {
     case kFloat32: k_linspace<kFloat32><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;

@@ -107,3 +107,44 @@ def oracle_run_parallel(nodes, inputs, count: int, periods=None, threads: int = 
     with cf.ThreadPoolExecutor(max_workers=threads) as ex:
         list(ex.map(work, range(0, count, chunk)))
     return out
+
+
+def nudge(s: np.ndarray, ulps: int, up: bool) -> np.ndarray:
+    """s moved by `ulps` f32 ulps toward +Inf (up) or -Inf."""
+    t = s.astype(np.float32)
+    target = np.float32(np.inf if up else -np.inf)
+    for _ in range(ulps):
+        t = np.nextafter(t, target)
+    return t
+
+
+def storage_key(bits: np.ndarray, dtype: int) -> np.ndarray:
+    width = 32 if dtype == O.FLOAT32 else 16
+    return ulp_key(bits.view(np.uint32 if width == 32 else np.uint16), width)
+
+
+def check_envelope(got, node_value, tail, out_dt, ulps, what, min_exact=0.99):
+    """The fused result must equal the reference chain evaluated with one
+    transcendental node's value anywhere within `ulps` f32 ulps of the
+    reference's (every other operation exact).  `tail` maps node values (f32)
+    to encoded outputs with the reference's remaining operations; it must be
+    monotone in the node value.  NaN outputs must agree in position."""
+    want = tail(node_value)
+    lo = tail(nudge(node_value, ulps, up=False))
+    hi = tail(nudge(node_value, ulps, up=True))
+    gb = got.view(np.uint32 if out_dt == O.FLOAT32 else np.uint16)
+    wb = want.view(gb.dtype)
+    gn, wn = nan_mask(gb, out_dt), nan_mask(wb, out_dt)
+    bad = np.flatnonzero(gn != wn)
+    assert bad.size == 0, f"{what}: NaN mismatch at {bad[:5]}"
+    keep = ~wn & ~nan_mask(lo.view(gb.dtype), out_dt) & ~nan_mask(hi.view(gb.dtype), out_dt)
+    kg, kl, kh = (storage_key(a.view(gb.dtype)[keep], out_dt) for a in (got, lo, hi))
+    lo_k, hi_k = np.minimum(kl, kh), np.maximum(kl, kh)
+    out = np.flatnonzero((kg < lo_k) | (kg > hi_k))
+    if out.size:
+        i = np.flatnonzero(keep)[out[0]]
+        raise AssertionError(f"{what}: {out.size} results outside the +-{ulps} ulp envelope, first at {i}: "
+                             f"got {gb[i]:#x} want {wb[i]:#x} node {node_value[i]!r}")
+    exact = float(np.mean(gb == wb))
+    assert exact >= min_exact, f"{what}: only {exact:.5f} bit-identical"
+    return exact

@@ -48,8 +48,8 @@ def test_emit_hip_swiglu_source_shape():
     src = k.source
     assert k.kernel_name == "fused_mlp_swiglu_out"  # like metalKernelName (codegen/metal.go:281-290)
     assert f'void {k.kernel_name}(' in src
-    assert "mfh_ld8_bf16(p0, e0, a0)" in src and "mfh_ld8_bf16(p1, e0, a1)" in src
-    assert "mfh_silu(x0)" in src and "mfh_st8_bf16(pout, e0, r)" in src
+    assert "mfh_ld8_bf16(p0, e0, a0[u])" in src and "mfh_ld8_bf16(p1, e0, a1[u])" in src
+    assert "mfh_silu(x0)" in src and "mfh_st8_bf16(pout, it * 8, r)" in src
     assert src.count("for (mfh_i64 i = nvec * 8 + tid; i < n; i += stride)") == 1
 
 
@@ -60,11 +60,22 @@ def test_emit_hip_broadcast_operands():
            (M.FLOAT32, M.OPERAND_SCALAR, 0), (M.FLOAT16, M.OPERAND_FULL, 0)]
     k = M.FusedKernel(nodes, ops, M.FLOAT16, "chain")
     src = k.source
-    assert "mfh_ld8_f16(p1, (e0 % 4096LL), a1)" in src
+    assert "mfh_ld8_f16(p1, (e0 % 4096LL), a1[u])" in src
     assert "const float s2 = mfh_ld1_f32(p2, 0);" in src
     assert "mfh_gelu(" in src
     precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)
     assert "mfh_gelu_ref(" in precise.source
+
+
+def test_emit_hip_item_width_follows_the_widest_operand():
+    relu_add = flatten((N_RELU, (N_ADD, ("in", 0), ("in", 1))))
+    k16 = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT16, M.OPERAND_FULL, 0)], M.BFLOAT16, "a")
+    assert "mfh_ld8_bf16(p0" in k16.source and "8 elements per item, 2 item(s)" in k16.source
+    k32 = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_FULL, 0)], M.BFLOAT16, "b")
+    assert "mfh_ld4_bf16(p0" in k32.source and "mfh_ld4_f32(p1" in k32.source and "mfh_st4_bf16(pout" in k32.source
+    # a scalar f32 operand does not narrow the item
+    ks = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_SCALAR, 0)], M.BFLOAT16, "c")
+    assert "mfh_ld8_bf16(p0" in ks.source
 
 
 def test_emit_hip_constants_are_rounded_to_f32():

@@ -167,6 +167,31 @@ def f32_probe(rng):
 
 
 @pytest.mark.parametrize("out_dt", [O.BFLOAT16, O.FLOAT16])
+def test_convert_f32_narrowing_every_input(out_dt):
+    # All 2^32 f32 bit patterns through mfh_convert (the gfx950 conversion
+    # instructions it uses must reproduce the Go rules everywhere: NaN
+    # payloads, ties, denormals, overflow).
+    import concurrent.futures as cf
+    torch = __import__("torch")
+    chunk = 1 << 28
+    narrow = O.f32_to_bf16 if out_dt == O.BFLOAT16 else O.f32_to_f16
+    src = torch.empty(chunk, dtype=torch.int32, device="cuda")
+    out = torch.empty(chunk, dtype=torch.int16, device="cuda")
+    for start in range(0, 1 << 32, chunk):
+        host = np.arange(start, start + chunk, dtype=np.uint64).astype(np.uint32)
+        src.copy_(torch.from_numpy(host.view(np.int32)))
+        M.convert(out.data_ptr(), out_dt, src.data_ptr(), O.FLOAT32, chunk, stream())
+        got = out.cpu().numpy().view(np.uint16)
+        x = host.view(np.float32)
+        parts = np.array_split(np.arange(chunk), 16)
+        with cf.ThreadPoolExecutor(16) as ex:
+            want = np.concatenate(list(ex.map(lambda ix: narrow(x[ix[0]:ix[-1] + 1]), parts)))
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"f32->{out_dt}: input {host[bad[0]]:#010x} gave {got[bad[0]]:#06x}, want {want[bad[0]]:#06x}"
+        log(f"f32->{out_dt}: inputs {start:#x}.. ok")
+
+
+@pytest.mark.parametrize("out_dt", [O.BFLOAT16, O.FLOAT16])
 def test_convert_f32_narrowing_rounding_classes(out_dt):
     # Every sign/exponent/top-mantissa pattern with the low bits at each
     # rounding class (ties, just above/below, NaN payloads, subnormals).

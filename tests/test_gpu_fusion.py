@@ -3,8 +3,12 @@ CPU evaluator (codegen/cpu.go:59-214).
 
 Tolerances (the reference runs Sigmoid/Silu/Gelu/Exp/Log/Tanh in f64 and
 rounds once to f32): arithmetic, select and sqrt nodes bit-exact;
-Exp/Log/Tanh and Sigmoid <= 1 f32 ulp; Silu and Gelu <= 2 f32 ulp; results
-narrowed to bf16/f16 <= 1 ulp of the storage dtype.  FMA contraction is off.
+Exp/Log/Tanh and Sigmoid <= 1 f32 ulp; Silu and Gelu <= 2 f32 ulp.  A chain
+is checked as the reference chain evaluated with its transcendental node
+anywhere within that node's tolerance and every other operation exact
+(gpu_util.check_envelope); where the chain cancels, a 2-ulp node error can be
+many ulps of the result, so a fixed ulp bound on the result would be wrong.
+FMA contraction is off.
 NaN results must be NaN where the oracle's are; NaN payloads of fused-chain
 results are not compared.  Where the reference's gelu form cancels
 (1 + tanh(inner) with inner < -9.3, i.e. v < -4.9) its f64 result is
@@ -17,8 +21,8 @@ import pytest
 import manifesto_amd as M
 import oracle as O
 
-from gpu_util import (compare_storage, empty_dev, log, oracle_run_parallel, stream, to_dev,
-                      to_host)
+from gpu_util import (check_envelope, compare_storage, empty_dev, log, oracle_run_parallel, stream,
+                      to_dev, to_host)
 
 pytestmark = pytest.mark.gpu
 
@@ -151,8 +155,12 @@ def test_storage_dtypes_tails_misaligned(in_dt, out_dt, count, pad):
     g = O.encode(rng.normal(0, 2, count).astype(np.float32), in_dt)
     u = O.encode(rng.normal(0, 2, count).astype(np.float32), in_dt)
     got = run_fused(nodes, [(in_dt, 0, 0)] * 2, [g, u], out_dt, count, pads=[pad, pad])
-    want = O.encode(O.run(nodes, [O.decode(g, in_dt), O.decode(u, in_dt)], count), out_dt)
-    compare_storage(got, want, out_dt, 1, f"{in_dt}->{out_dt} n={count} pad={pad}")
+    gf, uf = O.decode(g, in_dt), O.decode(u, in_dt)
+    silu = O.eval_unary(O.N_SILU, gf)
+    tail = lambda s: O.encode((s * uf).astype(np.float32) + np.float32(-0.5), out_dt)  # noqa: E731
+    check_envelope(got, silu, tail, out_dt, 2, f"{in_dt}->{out_dt} n={count} pad={pad}", min_exact=0.95)
+    want = O.encode(O.run(nodes, [gf, uf], count), out_dt)
+    assert np.array_equal(want.view(np.uint8), tail(silu).view(np.uint8))  # the tail restates the chain
 
 
 def test_swiglu_config3_full_size():
@@ -165,11 +173,12 @@ def test_swiglu_config3_full_size():
     nodes = O.flatten((O.N_MUL, (O.N_SILU, ("in", 0)), ("in", 1)))
     got = run_fused(nodes, [(O.BFLOAT16, 0, 0)] * 2, [gate, up], O.BFLOAT16, n, name="swiglu")
     log("swiglu config 3: oracle")
-    want = O.f32_to_bf16(oracle_run_parallel(nodes, [O.decode(gate, O.BFLOAT16), O.decode(up, O.BFLOAT16)], n))
-    worst = compare_storage(got, want, O.BFLOAT16, 1, "swiglu config 3")
-    exact = np.mean(got == want)
+    gf, uf = O.decode(gate, O.BFLOAT16), O.decode(up, O.BFLOAT16)
+    silu = oracle_run_parallel(O.flatten((O.N_SILU, ("in", 0))), [gf], n)
+    tail = lambda s: O.f32_to_bf16((s * uf).astype(np.float32))  # noqa: E731
+    exact = check_envelope(got, silu, tail, O.BFLOAT16, 2, "swiglu config 3", min_exact=0.999)
+    worst = compare_storage(got, tail(silu), O.BFLOAT16, 1, "swiglu config 3")
     log(f"swiglu config 3: max bf16 ulp {worst}, bit-identical fraction {exact:.6f}")
-    assert exact > 0.999
 
 
 def test_gelu_chain_config4_full_size():
@@ -187,13 +196,16 @@ def test_gelu_chain_config4_full_size():
            (O.FLOAT32, M.OPERAND_SCALAR, 0), (O.FLOAT16, M.OPERAND_FULL, 0)]
     got = run_fused(nodes, ops, [x, bias, s, res], O.FLOAT16, n, name="gelu_chain")
     log("gelu chain config 4: oracle")
-    want = O.f32_to_f16(oracle_run_parallel(
-        nodes, [O.decode(x, O.FLOAT16), O.decode(bias, O.FLOAT16), s, O.decode(res, O.FLOAT16)], n,
-        periods=[0, 4096, 1, 0]))
-    worst = compare_storage(got, want, O.FLOAT16, 1, "gelu chain config 4")
-    exact = np.mean(got == want)
-    log(f"gelu chain config 4: max f16 ulp {worst}, bit-identical fraction {exact:.6f}")
-    assert exact > 0.999
+    xf, bf, rf = O.decode(x, O.FLOAT16), O.decode(bias, O.FLOAT16), O.decode(res, O.FLOAT16)
+    inner = O.flatten((O.N_GELU, (O.N_MUL, (O.N_ADD, ("in", 0), ("in", 1)), ("in", 2))))
+    g = oracle_run_parallel(inner, [xf, bf, s], n, periods=[0, 4096, 1])
+    tail = lambda v: O.f32_to_f16((v + rf).astype(np.float32))  # noqa: E731
+    exact = check_envelope(got, g, tail, O.FLOAT16, 2, "gelu chain config 4", min_exact=0.999)
+    want = O.f32_to_f16(oracle_run_parallel(nodes, [xf, bf, s, rf], n, periods=[0, 4096, 1, 0]))
+    assert np.array_equal(want, tail(g))  # the tail restates the chain
+    d = np.abs(got.astype(np.int64) - want.astype(np.int64))
+    log(f"gelu chain config 4: bit-identical fraction {exact:.6f}, results differing by >1 f16 ulp: "
+        f"{int(np.sum(d > 1))} (all inside the gelu-node envelope)")
 
 
 def test_periodic_operand_not_multiple_of_8():
