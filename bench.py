@@ -293,6 +293,38 @@ def time_cpu(w, budget_s=3.0):
             "sample": f"{what}; {reps} repetition(s), {el:.1f} s; GOMAXPROCS-equivalent 1 (serial loops)"}
 
 
+def profile_run(torch, M, O, reps):
+    """Eager launches for rocprofv3: every workload kernel `reps` times, then a
+    plain f32 copy of 64 MiB (mfh_convert f32->f32, the k_convert kernel) whose
+    FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes."""
+    for cls in WORKLOADS:
+        w = cls(torch, M, O)
+        w.setup()
+        for i in range(reps):
+            w.step(i)
+        torch.cuda.synchronize()
+        log(f"profiled config {cls.cfg}: {w.kernel} x{reps}")
+        del w
+        torch.cuda.empty_cache()
+    n = 16 << 20
+    src = torch.rand(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        M.convert(dst.data_ptr(), M.FLOAT32, src.data_ptr(), M.FLOAT32, n, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    log(f"profiled calibration copy: k_convert<f32,f32> {n * 4} bytes read + {n * 4} written, x{reps}")
+
+
+def load_traffic():
+    """HBM bytes per dispatch of the headline kernel from the committed
+    rocprofv3 PMC summary (profiles/pmc_traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("fp8_e4m3_to_bf16", {}).get("traffic_bytes_per_dispatch")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -301,6 +333,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", type=int, default=0, help="measure only this BASELINE config")
+    ap.add_argument("--profile", type=int, default=0, metavar="REPS",
+                    help="eager launches of every kernel REPS times (for rocprofv3), no timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -314,6 +348,9 @@ def main():
     M.init(0)
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} ({props.multi_processor_count} CUs)")
+    if args.profile:
+        profile_run(torch, M, O, args.profile)
+        return
 
     results = {}
     for cls in WORKLOADS:
@@ -345,7 +382,7 @@ def main():
                    "elements": Fp8.n, "algorithmic_bytes_per_step": Fp8.bytes_per_step,
                    "timing": "HIP events on the launch stream around graph replays of rotated buffer sets"},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": None, "kernel": head["kernel"]},
+                     "frac": head["frac_of_peak"], "traffic": load_traffic(), "kernel": head["kernel"]},
         "cpu_baseline": head.get("cpu_baseline"),
         "elements_per_s": head["elements_per_s"],
         "configs": [results[k] for k in sorted(results)],

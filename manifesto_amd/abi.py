@@ -73,6 +73,8 @@ def _declare(L):
         "mfh_memcpy_h2d": (c.c_int, [vp, vp, c.c_size_t, vp]),
         "mfh_memcpy_d2h": (c.c_int, [vp, vp, c.c_size_t, vp]),
         "mfh_stream_sync": (c.c_int, [vp]),
+        "mfh_set_launch_config": (c.c_int, [c.c_char_p, i32, i32]),
+        "mfh_get_launch_config": (c.c_int, [c.c_char_p, c.POINTER(i32), c.POINTER(i32)]),
         "mfh_axpy": (None, [vp, vp, i64, f32, u8, vp]),
         "mfh_scalar_broadcast": (c.c_int, [vp, u8, vp, u8, i64, f32, i32, vp]),
         "mfh_linspace": (c.c_int, [vp, u8, i64, f32, f32, i32, vp]),
@@ -113,6 +115,17 @@ def take_sticky_error() -> None:
 
 def stream_sync(stream: int = 0) -> None:
     check(lib().mfh_stream_sync(stream))
+
+
+def set_launch_config(kernel: str, blocks_per_cu: int = 0, items_per_thread: int = 0) -> None:
+    """Launch shape of a streaming-kernel family (0 keeps the current value)."""
+    check(lib().mfh_set_launch_config(kernel.encode(), blocks_per_cu, items_per_thread))
+
+
+def get_launch_config(kernel: str):
+    bpc, ipt = ctypes.c_int32(), ctypes.c_int32()
+    check(lib().mfh_get_launch_config(kernel.encode(), ctypes.byref(bpc), ctypes.byref(ipt)))
+    return bpc.value, ipt.value
 
 
 # ---- runtime math / conversion wrappers ------------------------------------

@@ -120,16 +120,18 @@ MFH_DEV mfh_i32 mfh_int4_at(mfh_u32 word, mfh_u32 k)
 // ---- scale multiply -----------------------------------------------------------
 
 // One IEEE multiply with the NaN rules of an x86 mulss(decoded, scale) made
-// explicit, so the result never depends on which NaN the hardware forwards.
+// explicit, so the result never depends on which NaN the hardware forwards:
+// a NaN operand comes back quieted (the decoded value first) and Inf * 0 is
+// the x86 default NaN 0xffc00000.  Branch-free.
 MFH_DEV float mfh_scale_mul(float decoded, float scale)
 {
     mfh_u32 d = mfh_bits(decoded), s = mfh_bits(scale);
-    if ((d & 0x7fffffffu) > 0x7f800000u) return mfh_f32(d | 0x00400000u);
-    if ((s & 0x7fffffffu) > 0x7f800000u) return mfh_f32(s | 0x00400000u);
-    bool d_inf = (d & 0x7fffffffu) == 0x7f800000u, s_inf = (s & 0x7fffffffu) == 0x7f800000u;
-    bool d_zero = (d & 0x7fffffffu) == 0u, s_zero = (s & 0x7fffffffu) == 0u;
-    if ((d_inf && s_zero) || (d_zero && s_inf)) return mfh_f32(0xffc00000u);
-    return decoded * scale;
+    mfh_u32 da = d & 0x7fffffffu, sa = s & 0x7fffffffu;
+    mfh_u32 r = mfh_bits(decoded * scale);
+    r = ((da == 0x7f800000u && sa == 0u) || (da == 0u && sa == 0x7f800000u)) ? 0xffc00000u : r;
+    r = sa > 0x7f800000u ? (s | 0x00400000u) : r;
+    r = da > 0x7f800000u ? (d | 0x00400000u) : r;
+    return mfh_f32(r);
 }
 
 #endif  // MFH_CODEC_HPP

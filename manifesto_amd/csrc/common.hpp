@@ -46,10 +46,12 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Streaming kernels with their own grid-size setting.
 enum class Kern { kFp8, kInt4, kAxpy, kAxpy16, kConvert, kFused, kCount };
 
-// Workgroups per CU for a grid-stride kernel: a per-kernel default measured
-// on MI355X, overridable for sweeps with MFH_BPC_<NAME> (NAME = FP8, INT4,
-// AXPY, AXPY16, CONVERT, FUSED) or MFH_BLOCKS_PER_CU for all of them.
+// Launch shape of a grid-stride kernel family: workgroups per CU and work
+// items per thread per step.  Per-kernel defaults measured on MI355X;
+// mfh_set_launch_config or MFH_BPC_<NAME> / MFH_UNROLL_<NAME> (NAME = FP8,
+// INT4, AXPY, AXPY16, CONVERT, FUSED) change them.
 int blocks_per_cu(Kern k);
+int items_per_thread(Kern k);
 
 }  // namespace mfh
 

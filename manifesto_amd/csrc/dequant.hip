@@ -11,37 +11,9 @@
 // FP8: the output for a code depends only on (code, format, scale), so each
 // workgroup first builds the 256-entry table in LDS with the exact rules of
 // codec.hpp; every element is then one LDS read.
-#include <cstdlib>
-#include <cstring>
-
 #include "launch.hpp"
 
 namespace mfh {
-
-int blocks_per_cu(Kern k)
-{
-    struct Table {
-        int v[(int)Kern::kCount];
-        Table()
-        {
-            // Defaults measured on MI355X (256 CUs): writes-heavy streams want
-            // a few hundred KB to a few MB in flight, not full occupancy.
-            static const char* names[] = {"FP8", "INT4", "AXPY", "AXPY16", "CONVERT", "FUSED"};
-            static const int defaults[] = {8, 4, 2, 2, 4, 8};
-            const char* all = std::getenv("MFH_BLOCKS_PER_CU");
-            for (int i = 0; i < (int)Kern::kCount; i++) {
-                char key[64];
-                snprintf(key, sizeof key, "MFH_BPC_%s", names[i]);
-                const char* env = std::getenv(key);
-                if (!env) env = all;
-                int x = env ? std::atoi(env) : 0;
-                v[i] = (x > 0 && x <= 64) ? x : defaults[i];
-            }
-        }
-    };
-    static const Table table;
-    return table.v[(int)k];
-}
 
 int launch_status(const char* what) { return check_hip(hipGetLastError(), what); }
 
@@ -136,7 +108,9 @@ MFH_DEV float load_scale(const void* scales, mfh_i64 g)
 MFH_DEV bool finite_f32(float f) { return (mfh_bits(f) & 0x7f800000u) != 0x7f800000u; }
 
 // Item = 8 nibbles (4 packed bytes, 16-bit output) or 4 nibbles (2 bytes,
-// f32 output) sharing one scale -> one 16-byte store.
+// f32 output) sharing one scale -> one 16-byte store.  The vector path needs
+// a power-of-two group (2^group_shift >= the item); other groups run the
+// element loop.
 template <int OUT, int SDT, int U>
 __global__ __launch_bounds__(kBlock) void k_dequant_int4(const mfh_u8* __restrict__ packed,
                                                          const void* __restrict__ scales,
@@ -156,8 +130,7 @@ __global__ __launch_bounds__(kBlock) void k_dequant_int4(const mfh_u8* __restric
             if (i < nitems) {
                 if constexpr (kElems == 8) w[u] = reinterpret_cast<const mfh_u32*>(packed)[i];
                 else w[u] = reinterpret_cast<const mfh_u16*>(packed)[i];
-                mfh_i64 e = i * kElems;
-                s[u] = load_scale<SDT>(scales, group_shift >= 0 ? (e >> group_shift) : e / group);
+                s[u] = load_scale<SDT>(scales, (i * kElems) >> group_shift);
             }
         }
 #pragma unroll
@@ -165,10 +138,9 @@ __global__ __launch_bounds__(kBlock) void k_dequant_int4(const mfh_u8* __restric
             mfh_i64 i = v + u * stride;
             if (i >= nitems) break;
             float f[kElems];
-            if (finite_f32(s[u])) {  // then every product is finite: one IEEE multiply
 #pragma unroll
-                for (int k = 0; k < kElems; k++) f[k] = (float)mfh_int4_at(w[u], k) * s[u];
-            } else {
+            for (int k = 0; k < kElems; k++) f[k] = (float)mfh_int4_at(w[u], k) * s[u];
+            if (!finite_f32(s[u])) {  // Inf/NaN scale: apply the explicit NaN rules (rare)
 #pragma unroll
                 for (int k = 0; k < kElems; k++) f[k] = mfh_scale_mul((float)mfh_int4_at(w[u], k), s[u]);
             }
@@ -285,9 +257,6 @@ int by_out(int out_dt, A... args)
     }
 }
 
-constexpr int kFp8U = 2;
-constexpr int kInt4U = 2;
-
 template <int OUT>
 struct Fp8Launch {
     static int run(const Device* dev, void* out, const void* in, int fmt, int64_t n, float scale,
@@ -296,8 +265,12 @@ struct Fp8Launch {
         constexpr int codes = OUT == kFloat32 ? 4 : 8;
         int vec_ok = aligned(in, codes) && aligned16(out);
         int64_t items = vec_ok ? std::max<int64_t>(n / codes, 1) : n;
-        k_dequant_fp8<OUT, kFp8U><<<grid_for(items, dev, Kern::kFp8, kFp8U), kBlock, 0, stream>>>(
-            static_cast<const mfh_u8*>(in), out, n, scale, fmt, vec_ok);
+        const mfh_u8* src = static_cast<const mfh_u8*>(in);
+        const int u = items_per_thread(Kern::kFp8);
+        unsigned grid = grid_for(items, dev, Kern::kFp8, u);
+        if (u == 4) k_dequant_fp8<OUT, 4><<<grid, kBlock, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
+        else if (u == 2) k_dequant_fp8<OUT, 2><<<grid, kBlock, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
+        else k_dequant_fp8<OUT, 1><<<grid, kBlock, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
         return launch_status("k_dequant_fp8");
     }
 };
@@ -316,18 +289,28 @@ struct Int4Launch {
                    int scale_dt, int64_t group, hipStream_t stream)
     {
         constexpr int elems = OUT == kFloat32 ? 4 : 8;
-        int vec_ok = aligned(packed, elems / 2) && aligned16(out) && group % elems == 0;
-        int64_t items = vec_ok ? std::max<int64_t>(n / elems, 1) : n;
-        unsigned grid = grid_for(items, dev, Kern::kInt4, kInt4U);
         int shift = log2_exact(group);
+        int vec_ok = aligned(packed, elems / 2) && aligned16(out) && shift >= 0 && group >= elems;
+        int64_t items = vec_ok ? std::max<int64_t>(n / elems, 1) : n;
+        const int u = items_per_thread(Kern::kInt4);
+        unsigned grid = grid_for(items, dev, Kern::kInt4, u);
         const mfh_u8* p = static_cast<const mfh_u8*>(packed);
-        switch (scale_dt) {
-        case kFloat32: k_dequant_int4<OUT, kFloat32, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
-        case kFloat16: k_dequant_int4<OUT, kFloat16, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
-        case kBFloat16: k_dequant_int4<OUT, kBFloat16, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
-        default: k_dequant_int4<OUT, kInvalid, kInt4U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
-        }
+        if (u == 4) launch<4>(grid, p, scales, scale_dt, out, n, group, shift, vec_ok, stream);
+        else if (u == 2) launch<2>(grid, p, scales, scale_dt, out, n, group, shift, vec_ok, stream);
+        else launch<1>(grid, p, scales, scale_dt, out, n, group, shift, vec_ok, stream);
         return launch_status("k_dequant_int4");
+    }
+
+    template <int U>
+    static void launch(unsigned grid, const mfh_u8* p, const void* scales, int scale_dt, void* out, int64_t n,
+                       int64_t group, int shift, int vec_ok, hipStream_t stream)
+    {
+        switch (scale_dt) {
+        case kFloat32: k_dequant_int4<OUT, kFloat32, U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
+        case kFloat16: k_dequant_int4<OUT, kFloat16, U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
+        case kBFloat16: k_dequant_int4<OUT, kBFloat16, U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
+        default: k_dequant_int4<OUT, kInvalid, U><<<grid, kBlock, 0, stream>>>(p, scales, out, n, group, shift, vec_ok); break;
+        }
     }
 };
 

@@ -233,6 +233,7 @@ struct mfh_kernel {
     uint8_t out_dtype = mfh::kFloat32;
     int vec = 8;     // elements per work item
     int unroll = 1;  // work items per thread per grid-stride step
+    int auto_bpc = 4;  // workgroups per CU unless the launch config sets one
     bool periods_vectorizable = true;
     std::shared_ptr<mfh::CodeObject> code;
 };
@@ -278,14 +279,24 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     for (int k = 0; k < n_inputs; k++)
         if (inputs[k].mode == MFH_OPERAND_PERIODIC && inputs[k].period % vec != 0) periods_vectorizable = false;
 
-    // Items per thread per step: two when the chain is cheap arithmetic (more
-    // loads in flight), one when it has transcendental nodes (VALU-bound).
-    bool heavy = false;
-    for (const mfh_ast_node& nd : list)
-        if (nd.type == kNodeExp || nd.type == kNodeLog || nd.type == kNodeTanh || nd.type == kNodeSigmoid ||
-            nd.type == kNodeSilu || nd.type == kNodeGelu || nd.type == kNodeSqrt || nd.type == kNodeDiv)
-            heavy = true;
-    const int unroll = heavy ? 1 : 2;
+    // Launch shape from the chain's VALU cost per element (instruction slots,
+    // quarter-rate ops counted four times): a memory-bound chain wants two
+    // items per thread and few workgroups (writes in flight, not occupancy);
+    // a VALU-bound one wants one item and high occupancy to cover latency.
+    // Measured on MI355X with the SwiGLU (~35 slots) and f16 gelu (~45) chains.
+    int cost = 0;
+    for (const mfh_ast_node& nd : list) {
+        switch (nd.type) {
+        case kNodeGelu: cost += 40; break;
+        case kNodeSilu: case kNodeSigmoid: cost += 30; break;
+        case kNodeExp: case kNodeLog: case kNodeTanh: cost += 60; break;
+        case kNodeDiv: case kNodeSqrt: cost += 10; break;
+        default: cost += 1; break;
+        }
+    }
+    const bool heavy = cost > 8;
+    const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : (heavy ? 1 : 2);
+    const int auto_bpc = cost > 38 ? 24 : 4;
 
     const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
     Emitter em{list, c0, c1, precise, "", 0};
@@ -356,6 +367,7 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     kernel->out_dtype = out_dtype;
     kernel->vec = vec;
     kernel->unroll = unroll;
+    kernel->auto_bpc = auto_bpc;
     kernel->periods_vectorizable = periods_vectorizable;
     MFH_TRY(compile_source(kernel->source, kernel_name, &kernel->code));
     *out = kernel.release();
@@ -391,7 +403,8 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
     int64_t nvec = vec_ok ? count / kernel->vec : 0;
     int64_t items = nvec > 0 ? (nvec + kernel->unroll - 1) / kernel->unroll : count;
     int64_t need = (items + kBlockThreads - 1) / kBlockThreads;
-    int64_t cap = (int64_t)dev->compute_units * blocks_per_cu(Kern::kFused);
+    int bpc = blocks_per_cu(Kern::kFused) > 0 ? blocks_per_cu(Kern::kFused) : kernel->auto_bpc;
+    int64_t cap = (int64_t)dev->compute_units * bpc;
     unsigned grid = (unsigned)std::max<int64_t>(1, std::min(need, cap));
     std::vector<const void*> ptrs(inputs, inputs + n_inputs);
     std::vector<void*> args;

@@ -29,6 +29,7 @@ MFH_DEV float axpy_step(float y, float x, float alpha)
     return y + product;
 }
 
+template <int U>
 __global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, const float* __restrict__ x,
                                                      mfh_i64 n, float alpha, int vec_ok)
 {
@@ -36,12 +37,25 @@ __global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, cons
     const mfh_i64 nvec = vec_ok ? (n >> 2) : 0;
     u32x4* yv = reinterpret_cast<u32x4*>(y);
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
-        u32x4 a = xv[v], b = yv[v];
-        u32x4 o;
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride * U) {
+        u32x4 a[U], b[U];
 #pragma unroll
-        for (int k = 0; k < 4; k++) o[k] = mfh_bits(axpy_step(mfh_f32(b[k]), mfh_f32(a[k]), alpha));
-        yv[v] = o;
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i < nvec) {
+                a[u] = xv[i];
+                b[u] = yv[i];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i >= nvec) break;
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; k++) o[k] = mfh_bits(axpy_step(mfh_f32(b[u][k]), mfh_f32(a[u][k]), alpha));
+            yv[i] = o;
+        }
     }
     for (mfh_i64 i = nvec * 4 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
         y[i] = axpy_step(y[i], x[i], alpha);
@@ -49,7 +63,7 @@ __global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, cons
 
 // 16-bit storage: decode, the same f32 step, re-encode (axpyOntoHost tensor
 // path, runtime/axpy.go:120-161, in one pass instead of five).
-template <int DT>
+template <int DT, int U>
 __global__ __launch_bounds__(kBlock) void k_axpy16(mfh_u16* __restrict__ y, const mfh_u16* __restrict__ x,
                                                    mfh_i64 n, float alpha, int vec_ok)
 {
@@ -57,21 +71,40 @@ __global__ __launch_bounds__(kBlock) void k_axpy16(mfh_u16* __restrict__ y, cons
     const mfh_i64 nvec = vec_ok ? (n >> 3) : 0;
     u32x4* yv = reinterpret_cast<u32x4*>(y);
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride) {
-        u32x4 a = xv[v], b = yv[v];
-        u32x4 o;
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride * U) {
+        u32x4 a[U], b[U];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float lo = axpy_step(dec16<DT>(b[k] & 0xffffu), dec16<DT>(a[k] & 0xffffu), alpha);
-            float hi = axpy_step(dec16<DT>(b[k] >> 16), dec16<DT>(a[k] >> 16), alpha);
-            o[k] = enc16x2<DT>(lo, hi);
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i < nvec) {
+                a[u] = xv[i];
+                b[u] = yv[i];
+            }
         }
-        yv[v] = o;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            mfh_i64 i = v + u * stride;
+            if (i >= nvec) break;
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float lo = axpy_step(dec16<DT>(b[u][k] & 0xffffu), dec16<DT>(a[u][k] & 0xffffu), alpha);
+                float hi = axpy_step(dec16<DT>(b[u][k] >> 16), dec16<DT>(a[u][k] >> 16), alpha);
+                o[k] = enc16x2<DT>(lo, hi);
+            }
+            yv[i] = o;
+        }
     }
     for (mfh_i64 i = nvec * 8 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         float r = axpy_step(dec16<DT>(y[i]), dec16<DT>(x[i]), alpha);
         y[i] = (mfh_u16)(enc16x2<DT>(r, 0.0f) & 0xffffu);
     }
+}
+
+template <int DT, int U>
+void launch_axpy16(unsigned grid, hipStream_t s, mfh_u16* y, const mfh_u16* x, int64_t n, float alpha, int vec_ok)
+{
+    k_axpy16<DT, U><<<grid, kBlock, 0, s>>>(y, x, n, alpha, vec_ok);
 }
 
 template <int DT>
@@ -167,18 +200,31 @@ void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype,
     switch (dtype) {
     case kFloat32: {
         int64_t items = vec_ok ? std::max<int64_t>(count >> 2, 1) : count;
-        k_axpy_f32<<<grid_for(items, dev, Kern::kAxpy), kBlock, 0, s>>>(static_cast<float*>(y), static_cast<const float*>(x),
-                                                           count, alpha, vec_ok);
+        const int u = items_per_thread(Kern::kAxpy);
+        unsigned grid = grid_for(items, dev, Kern::kAxpy, u);
+        auto* yy = static_cast<float*>(y);
+        auto* xx = static_cast<const float*>(x);
+        if (u == 4) k_axpy_f32<4><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
+        else if (u == 2) k_axpy_f32<2><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
+        else k_axpy_f32<1><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
         break;
     }
     case kBFloat16:
     case kFloat16: {
         int64_t items = vec_ok ? std::max<int64_t>(count >> 3, 1) : count;
-        unsigned grid = grid_for(items, dev, Kern::kAxpy16);
+        const int u = items_per_thread(Kern::kAxpy16);
+        unsigned grid = grid_for(items, dev, Kern::kAxpy16, u);
         auto* yy = static_cast<mfh_u16*>(y);
         auto* xx = static_cast<const mfh_u16*>(x);
-        if (dtype == kBFloat16) k_axpy16<kBFloat16><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
-        else k_axpy16<kFloat16><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
+        if (dtype == kBFloat16) {
+            if (u == 4) launch_axpy16<kBFloat16, 4>(grid, s, yy, xx, count, alpha, vec_ok);
+            else if (u == 2) launch_axpy16<kBFloat16, 2>(grid, s, yy, xx, count, alpha, vec_ok);
+            else launch_axpy16<kBFloat16, 1>(grid, s, yy, xx, count, alpha, vec_ok);
+        } else {
+            if (u == 4) launch_axpy16<kFloat16, 4>(grid, s, yy, xx, count, alpha, vec_ok);
+            else if (u == 2) launch_axpy16<kFloat16, 2>(grid, s, yy, xx, count, alpha, vec_ok);
+            else launch_axpy16<kFloat16, 1>(grid, s, yy, xx, count, alpha, vec_ok);
+        }
         break;
     }
     default:

@@ -1,6 +1,9 @@
 // runtime.cpp — device binding, memory, copies, streams and error state.
 #include <atomic>
+#include <cctype>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "common.hpp"
@@ -100,6 +103,60 @@ int bind_device(const Device** out)
 
 void release_kernel_cache();  // fusion.cpp
 
+// ---- launch shapes ------------------------------------------------------------
+
+namespace {
+struct LaunchCfg {
+    const char* name;
+    std::atomic<int> bpc;
+    std::atomic<int> unroll;  // 0: the kernel family chooses (fused: by chain cost)
+};
+// Defaults measured on MI355X (256 CUs): the write-heavy streams run best
+// with a few MB of stores in flight, well below full occupancy.  0 for the
+// fused family means "per kernel": each generated kernel carries a shape
+// chosen from its estimated VALU cost (see fusion.cpp).
+LaunchCfg g_cfg[(int)Kern::kCount] = {
+    {"fp8", {6}, {1}}, {"int4", {8}, {2}}, {"axpy", {2}, {1}},
+    {"axpy16", {2}, {1}}, {"convert", {4}, {1}}, {"fused", {0}, {0}},
+};
+std::once_flag g_cfg_env_once;
+
+void read_cfg_env()
+{
+    const char* all = std::getenv("MFH_BLOCKS_PER_CU");
+    for (auto& c : g_cfg) {
+        std::string upper(c.name);
+        for (auto& ch : upper) ch = (char)toupper(ch);
+        const char* bpc = std::getenv(("MFH_BPC_" + upper).c_str());
+        if (!bpc) bpc = all;
+        const char* un = std::getenv(("MFH_UNROLL_" + upper).c_str());
+        if (bpc && atoi(bpc) > 0 && atoi(bpc) <= 64) c.bpc = atoi(bpc);
+        if (un && (atoi(un) == 1 || atoi(un) == 2 || atoi(un) == 4)) c.unroll = atoi(un);
+    }
+}
+
+LaunchCfg* find_cfg(const char* name)
+{
+    std::call_once(g_cfg_env_once, read_cfg_env);
+    if (!name) return nullptr;
+    for (auto& c : g_cfg)
+        if (strcmp(c.name, name) == 0) return &c;
+    return nullptr;
+}
+}  // namespace
+
+int blocks_per_cu(Kern k)
+{
+    std::call_once(g_cfg_env_once, read_cfg_env);
+    return g_cfg[(int)k].bpc.load(std::memory_order_relaxed);
+}
+
+int items_per_thread(Kern k)
+{
+    std::call_once(g_cfg_env_once, read_cfg_env);
+    return g_cfg[(int)k].unroll.load(std::memory_order_relaxed);
+}
+
 }  // namespace mfh
 
 using namespace mfh;
@@ -152,6 +209,27 @@ int mfh_capabilities(int64_t* max_bytes, int32_t* native_alignment, int32_t* com
     if (max_bytes) *max_bytes = dev->total_bytes;
     if (native_alignment) *native_alignment = 256;
     if (compute_units) *compute_units = dev->compute_units;
+    return MFH_OK;
+}
+
+int mfh_set_launch_config(const char* kernel, int32_t blocks_per_cu, int32_t items_per_thread)
+{
+    LaunchCfg* c = find_cfg(kernel);
+    if (!c) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: unknown kernel family \"%s\"", kernel ? kernel : "(null)");
+    if (blocks_per_cu > 64) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: blocks_per_cu %d > 64", blocks_per_cu);
+    if (items_per_thread > 0 && items_per_thread != 1 && items_per_thread != 2 && items_per_thread != 4)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: items_per_thread must be 1, 2 or 4");
+    if (blocks_per_cu > 0) c->bpc = blocks_per_cu;
+    if (items_per_thread > 0) c->unroll = items_per_thread;
+    return MFH_OK;
+}
+
+int mfh_get_launch_config(const char* kernel, int32_t* blocks_per_cu, int32_t* items_per_thread)
+{
+    LaunchCfg* c = find_cfg(kernel);
+    if (!c) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_get_launch_config: unknown kernel family \"%s\"", kernel ? kernel : "(null)");
+    if (blocks_per_cu) *blocks_per_cu = c->bpc;
+    if (items_per_thread) *items_per_thread = c->unroll;
     return MFH_OK;
 }
 
