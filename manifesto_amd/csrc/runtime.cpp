@@ -116,7 +116,7 @@ struct LaunchCfg {
 // fused family means "per kernel": each generated kernel carries a shape
 // chosen from its estimated VALU cost (see fusion.cpp).
 LaunchCfg g_cfg[(int)Kern::kCount] = {
-    {"fp8", {6}, {1}}, {"int4", {8}, {2}}, {"axpy", {2}, {1}},
+    {"fp8", {6}, {1}}, {"int4", {6}, {1}}, {"axpy", {2}, {1}},
     {"axpy16", {2}, {1}}, {"convert", {4}, {1}}, {"fused", {0}, {0}},
 };
 std::once_flag g_cfg_env_once;
