@@ -20,6 +20,12 @@ enum NodeType : int32_t {
 // NodeType.Arity (optimizer/fusion_ast.go:168-180); -1 for unknown types.
 int node_arity(int type);
 
+// EmitHIP and HIPKernel.Run behind mfh_fusion_compile / mfh_fusion_launch.
+int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, int n_inputs,
+             uint8_t out_dtype, const char* output_port, uint32_t flags, mfh_kernel** out);
+int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
+            hipStream_t stream);
+
 }  // namespace mfh
 
 #endif  // MFH_FUSION_HPP

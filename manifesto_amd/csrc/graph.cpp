@@ -1,0 +1,1140 @@
+// graph.cpp — the compile-and-dispatch layer around the HIP codegen target:
+// the manifest compute graph (ast.Graph), the optimizer's ConstantFold and
+// Fuse passes, codegen's AttachKernels with a HIP target, and CallGraph-style
+// execution of the lowered graph on one stream.
+//
+// The passes restate the reference's Go semantics (file:line at each) so that
+// a C++ host gets the FusionASTs the Go compiler would hand to EmitHIP.
+// Execution runs the nodes in graph order; a value passed between nodes lives
+// in one per-graph device workspace whose offsets come from value lifetimes
+// (first-fit over a free list), so a steady-state call allocates nothing.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <set>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/mfh_graph.h"
+#include "common.hpp"
+#include "fusion.hpp"
+
+namespace mfh {
+namespace {
+
+const char* const kFuseOp = "optimizer.fusion";        // optimizer/fuse.go:16
+const char* const kFuseAttributeAST = "fusion_ast";    // optimizer/fuse.go:22
+const char* const kConstantOp = "math.constant";       // optimizer/constant_fold.go:23
+const char* const kConstantValue = "value";            // optimizer/constant_fold.go:16
+const char* const kFusedNodeCount = "fused_node_count";  // optimizer/fuse.go:131
+
+bool hip_storage(int dt) { return dt == kFloat32 || dt == kFloat16 || dt == kBFloat16; }
+
+// ---- elementwise table (optimizer/elementwise.go:15-36) ---------------------
+
+struct OpEntry {
+    const char* op;
+    int32_t type;
+};
+
+// Op string -> NodeType.  kNodeInvalid rows exist but are disabled, as in the
+// reference (sin/cos).  "math.sign" maps to Neg there as a placeholder; the
+// mapping is kept so that graphs fuse identically.
+const OpEntry kElementwiseTable[] = {
+    {"math.add", kNodeAdd},   {"math.sub", kNodeSub},   {"math.mul", kNodeMul},
+    {"math.div", kNodeDiv},   {"math.max", kNodeMax},   {"math.min", kNodeMin},
+    {"math.neg", kNodeNeg},   {"math.abs", kNodeAbs},   {"math.sqrt", kNodeSqrt},
+    {"math.exp", kNodeExp},   {"math.log", kNodeLog},   {"math.sign", kNodeNeg},
+    {"math.sin", kNodeInvalid}, {"math.cos", kNodeInvalid},
+    {"activation.relu", kNodeReLU},       {"activation.sigmoid", kNodeSigmoid},
+    {"activation.tanh", kNodeTanh},       {"activation.swish", kNodeSilu},
+    {"activation.gelu", kNodeGelu},       {"activation.leaky_relu", kNodeLeakyReLU},
+};
+
+bool is_space(unsigned char c) { return c == ' ' || c == '\t' || c == '\n' || c == '\v' || c == '\f' || c == '\r'; }
+
+// isElementwiseOp (optimizer/elementwise.go:44-54): strings.TrimSpace +
+// strings.ToLower, then the table; disabled rows are not eligible.  Only
+// ASCII white space and letters are folded (every table key is ASCII).
+int32_t elementwise_type(const std::string& op)
+{
+    size_t b = 0, e = op.size();
+    while (b < e && is_space((unsigned char)op[b])) b++;
+    while (e > b && is_space((unsigned char)op[e - 1])) e--;
+    std::string key = op.substr(b, e - b);
+    for (char& c : key)
+        if (c >= 'A' && c <= 'Z') c = (char)(c - 'A' + 'a');
+    for (const OpEntry& row : kElementwiseTable)
+        if (key == row.op) return row.type;
+    return kNodeInvalid;
+}
+
+// ---- FusionAST (optimizer/fusion_ast.go:70-113) -----------------------------
+
+struct ASTNode {
+    int32_t type = kNodeInvalid;
+    int32_t input_index = 0;
+    double value = 0.0;
+    std::vector<std::unique_ptr<ASTNode>> children;
+};
+
+std::unique_ptr<ASTNode> input_leaf(int index)
+{
+    auto n = std::make_unique<ASTNode>();
+    n->type = kNodeInput;
+    n->input_index = index;
+    return n;
+}
+
+struct FusionAST {
+    std::unique_ptr<ASTNode> root;
+    std::vector<std::string> input_ports;
+    std::string output_port;
+    std::string count_expr;  // never set by Fuse (optimizer/fuse.go:108-114)
+    uint8_t dtype = kInvalid;
+    std::vector<std::string> contained_node_ids;
+
+    // pre-order view for the ABI, rebuilt on demand
+    std::vector<mfh_ast_node> flat;
+    std::vector<int32_t> child_counts;
+    void flatten()
+    {
+        flat.clear();
+        child_counts.clear();
+        if (root) walk(*root);
+    }
+    void walk(const ASTNode& n)
+    {
+        flat.push_back(mfh_ast_node{n.type, n.input_index, n.value});
+        child_counts.push_back((int32_t)n.children.size());
+        for (const auto& c : n.children) walk(*c);
+    }
+};
+
+// ---- HIP kernels (the TargetHIP member of a KernelSet) -----------------------
+
+struct KernelDeleter {
+    void operator()(mfh_kernel* k) const { (void)mfh_fusion_release(k); }
+};
+using KernelPtr = std::unique_ptr<mfh_kernel, KernelDeleter>;
+
+std::string signature(const std::vector<mfh_operand>& ops)
+{
+    std::string s;
+    for (const mfh_operand& op : ops)
+        s += std::to_string(op.dtype) + ":" + std::to_string(op.mode) + ":" + std::to_string(op.period) + ";";
+    return s;
+}
+
+// One FusionAST lowered for gfx950.  Operand dtypes and broadcast modes are
+// only known at dispatch, so the kernel keeps one compiled variant per operand
+// signature; the full-length variant of the declared dtypes is compiled when
+// the kernel is emitted (and is what KernelSet.For hands out).
+struct HIPKernel {
+    std::string identifier;
+    std::vector<std::string> inputs;
+    std::vector<mfh_ast_node> nodes;  // pre-order, child counts == arity
+    std::vector<uint8_t> declared;    // per input: declared dtype or kInvalid
+    uint8_t out_dtype = kFloat32;
+    uint32_t flags = 0;
+    std::map<std::string, KernelPtr> variants;
+    const mfh_kernel* full = nullptr;
+
+    int variant(const std::vector<mfh_operand>& ops, const mfh_kernel** out)
+    {
+        std::string key = signature(ops);
+        auto it = variants.find(key);
+        if (it == variants.end()) {
+            mfh_kernel* k = nullptr;
+            MFH_TRY(emit_hip(nodes.data(), (int)nodes.size(), ops.data(), (int)ops.size(), out_dtype,
+                             identifier.c_str(), flags, &k));
+            it = variants.emplace(key, KernelPtr(k)).first;
+        }
+        *out = it->second.get();
+        return MFH_OK;
+    }
+};
+
+struct KernelSet {  // codegen/attach.go:14-16
+    std::map<int32_t, std::shared_ptr<HIPKernel>> kernels;
+    HIPKernel* For(int32_t target) const
+    {
+        auto it = kernels.find(target);
+        return it == kernels.end() ? nullptr : it->second.get();
+    }
+};
+
+// ---- ast.Graph ---------------------------------------------------------------
+
+struct GraphNode {
+    std::string id;
+    std::string op;
+    std::vector<std::string> inputs;
+    std::map<std::string, double> attributes;  // numeric Attributes
+    std::map<std::string, int64_t> metadata;
+    std::shared_ptr<FusionAST> fusion;  // Attributes["fusion_ast"]
+    std::shared_ptr<KernelSet> kernels;  // Attributes["compiled_kernel"]
+    std::vector<uint8_t> input_types;    // InputTypes[k].DType
+    uint8_t output_type = kInvalid;      // OutputType.DType
+    std::shared_ptr<HIPKernel> solo;     // one-node kernel of an unfused elementwise node
+};
+
+}  // namespace
+}  // namespace mfh
+
+struct mfh_graph {
+    std::vector<std::unique_ptr<mfh::GraphNode>> nodes;
+    std::vector<std::string> inputs;
+    std::vector<std::pair<std::string, std::string>> outputs;  // key -> value
+    uint8_t execution_dtype = mfh::kInvalid;
+    // device workspace: constants first, then the intermediate values
+    void* ws = nullptr;
+    int64_t ws_bytes = 0;
+    std::vector<float> ws_constants;  // the constants the workspace holds
+    bool ws_constants_valid = false;
+    uint32_t codegen_flags = 0;  // of the last AttachKernels; also used for unfused nodes
+};
+
+namespace mfh {
+namespace {
+
+using Graph = mfh_graph;
+
+// ---- Fuse (optimizer/fuse.go:54-265) -----------------------------------------
+
+struct ClusterBuilder {
+    const Graph& graph;
+    const std::unordered_map<std::string, int>& producers;
+    const std::unordered_map<std::string, int>& consumers;
+    const std::vector<char>& absorbed;
+    std::set<int> members;  // absorbedIndices
+    std::vector<std::string> inputs;
+    std::unordered_map<std::string, int> input_index;
+
+    std::unique_ptr<ASTNode> external(const std::string& name)
+    {
+        auto it = input_index.find(name);
+        if (it != input_index.end()) return input_leaf(it->second);
+        int k = (int)inputs.size();
+        inputs.push_back(name);
+        input_index.emplace(name, k);
+        return input_leaf(k);
+    }
+
+    // build (optimizer/fuse.go:203-223)
+    std::unique_ptr<ASTNode> build(const GraphNode& node)
+    {
+        int32_t type = elementwise_type(node.op);
+        if (type == kNodeInvalid) return external(node.id);
+        members.insert(producers.at(node.id));
+        auto n = std::make_unique<ASTNode>();
+        n->type = type;
+        for (const std::string& name : node.inputs) n->children.push_back(operand(name));
+        return n;
+    }
+
+    // buildOperand (optimizer/fuse.go:228-256): inline the producer only when
+    // it is an elementwise node with exactly one consumer that no cluster has
+    // taken yet.
+    std::unique_ptr<ASTNode> operand(const std::string& name)
+    {
+        auto p = producers.find(name);
+        if (p == producers.end()) return external(name);
+        const int index = p->second;
+        if (absorbed[index] || members.count(index)) return external(name);
+        auto c = consumers.find(name);
+        if (c == consumers.end() || c->second != 1) return external(name);
+        const GraphNode& producer = *graph.nodes[index];
+        if (elementwise_type(producer.op) == kNodeInvalid) return external(name);
+        return build(producer);
+    }
+};
+
+// fusionInputTypes / boundaryInputPortType (optimizer/fuse.go:303-350): a
+// port's type is its producer's OutputType, else the InputTypes slot of the
+// first node that reads it.
+std::vector<uint8_t> fusion_input_types(const Graph& g, const std::vector<std::string>& names)
+{
+    std::unordered_map<std::string, uint8_t> produced;
+    for (const auto& n : g.nodes)
+        if (n && n->output_type != kInvalid) produced[n->id] = n->output_type;
+    std::vector<uint8_t> out(names.size(), kInvalid);
+    for (size_t k = 0; k < names.size(); k++) {
+        auto it = produced.find(names[k]);
+        if (it != produced.end()) {
+            out[k] = it->second;
+            continue;
+        }
+        bool found = false;
+        for (const auto& n : g.nodes) {
+            if (!n) continue;
+            for (size_t s = 0; s < n->inputs.size() && !found; s++)
+                if (n->inputs[s] == names[k] && s < n->input_types.size()) {
+                    out[k] = n->input_types[s];
+                    found = true;
+                }
+            if (found) break;
+        }
+    }
+    return out;
+}
+
+int fuse(Graph& g, mfh_fusion_stats* stats)
+{
+    mfh_fusion_stats st{0, 0, 0};
+    const int n = (int)g.nodes.size();
+    std::unordered_map<std::string, int> producers;
+    for (int i = 0; i < n; i++) producers[g.nodes[i]->id] = i;
+    std::unordered_map<std::string, int> consumers;
+    for (const auto& node : g.nodes)
+        for (const std::string& name : node->inputs) consumers[name]++;
+    for (const auto& kv : g.outputs) consumers[kv.second]++;  // outputs stay materialised
+
+    std::vector<char> visited(n, 0), absorbed(n, 0);
+    // Reverse walk: a consumer absorbs its eligible producers before they can
+    // become roots of their own (optimizer/fuse.go:82-140).
+    for (int index = n - 1; index >= 0; index--) {
+        if (visited[index] || absorbed[index]) continue;
+        GraphNode& node = *g.nodes[index];
+        if (elementwise_type(node.op) == kNodeInvalid) {
+            visited[index] = 1;
+            continue;
+        }
+        ClusterBuilder cb{g, producers, consumers, absorbed, {}, {}, {}};
+        std::unique_ptr<ASTNode> root = cb.build(node);
+        const int size = (int)cb.members.size();
+        if (size <= 1) {  // a lone node is not worth a fused kernel
+            visited[index] = 1;
+            continue;
+        }
+        auto fusion = std::make_shared<FusionAST>();
+        fusion->root = std::move(root);
+        fusion->input_ports = cb.inputs;
+        fusion->output_port = node.id;
+        fusion->dtype = g.execution_dtype;
+        for (int m : cb.members) fusion->contained_node_ids.push_back(g.nodes[m]->id);
+
+        auto fused = std::make_unique<GraphNode>();
+        fused->id = node.id;
+        fused->op = kFuseOp;
+        fused->inputs = cb.inputs;
+        fused->input_types = fusion_input_types(g, cb.inputs);
+        fused->output_type = node.output_type;
+        fused->fusion = std::move(fusion);
+        fused->metadata[kFusedNodeCount] = size;
+        g.nodes[index] = std::move(fused);
+        visited[index] = 1;
+        for (int m : cb.members)
+            if (m != index) absorbed[m] = 1;
+        st.clusters++;
+        st.nodes_fused += size;
+        st.nodes_removed += size - 1;
+    }
+    std::vector<std::unique_ptr<GraphNode>> kept;
+    kept.reserve(n);
+    for (int i = 0; i < n; i++)
+        if (!absorbed[i]) kept.push_back(std::move(g.nodes[i]));
+    g.nodes = std::move(kept);
+    if (stats) *stats = st;
+    return MFH_OK;
+}
+
+// ---- ConstantFold (optimizer/constant_fold.go:40-225) ------------------------
+
+// math.Max / math.Min of Go: NaN wins, +0 > -0, then the ordinary order.
+double go_max(double a, double b)
+{
+    if (std::isinf(a) && a > 0) return a;
+    if (std::isinf(b) && b > 0) return b;
+    if (std::isnan(a) || std::isnan(b)) return std::nan("");
+    if (a == 0 && a == b) return std::signbit(a) ? b : a;
+    return a > b ? a : b;
+}
+
+double go_min(double a, double b)
+{
+    if (std::isinf(a) && a < 0) return a;
+    if (std::isinf(b) && b < 0) return b;
+    if (std::isnan(a) || std::isnan(b)) return std::nan("");
+    if (a == 0 && a == b) return std::signbit(a) ? a : b;
+    return a < b ? a : b;
+}
+
+double bits_f64(uint64_t b)
+{
+    double d;
+    std::memcpy(&d, &b, sizeof d);
+    return d;
+}
+
+// evaluateUnary (optimizer/constant_fold.go:165-203), f64 throughout; the
+// libm functions are the C library's (within an f64 ulp of Go's math).
+bool evaluate_unary(int32_t type, double x, double* r)
+{
+    switch (type) {
+    case kNodeNeg: *r = -x; return true;
+    case kNodeAbs: *r = std::fabs(x); return true;
+    case kNodeSqrt: *r = std::sqrt(x); return true;
+    case kNodeExp: *r = std::exp(x); return true;
+    case kNodeLog: *r = std::log(x); return true;
+    case kNodeReLU: *r = x > 0 ? x : 0.0; return true;  // NaN and -0 fold to +0
+    case kNodeSigmoid: *r = 1.0 / (1.0 + std::exp(-x)); return true;
+    case kNodeTanh: *r = std::tanh(x); return true;
+    case kNodeSilu: *r = x / (1.0 + std::exp(-x)); return true;
+    case kNodeGelu: {
+        // 2/pi as Go's constant arithmetic rounds it (exact, then to f64)
+        const double inner = std::sqrt(bits_f64(0x3FE45F306DC9C883ull)) * (x + 0.044715 * x * x * x);
+        *r = 0.5 * x * (1.0 + std::tanh(inner));
+        return true;
+    }
+    case kNodeLeakyReLU: *r = x >= 0 ? x : 0.01 * x; return true;
+    default: return false;
+    }
+}
+
+// evaluateBinary (optimizer/constant_fold.go:205-225); x/0 is not folded.
+bool evaluate_binary(int32_t type, double a, double b, double* r)
+{
+    switch (type) {
+    case kNodeAdd: *r = a + b; return true;
+    case kNodeSub: *r = a - b; return true;
+    case kNodeMul: *r = a * b; return true;
+    case kNodeDiv:
+        if (b == 0) return false;
+        *r = a / b;
+        return true;
+    case kNodeMax: *r = go_max(a, b); return true;
+    case kNodeMin: *r = go_min(a, b); return true;
+    default: return false;
+    }
+}
+
+int constant_fold(Graph& g, int32_t* folded_out)
+{
+    int32_t folded = 0;
+    std::unordered_map<std::string, double> values;
+    for (const auto& node : g.nodes) {
+        if (node->op != kConstantOp) continue;
+        auto it = node->attributes.find(kConstantValue);
+        if (it != node->attributes.end()) values[node->id] = it->second;
+    }
+    // One forward sweep: a node folds when every input is a known constant,
+    // which chains through nodes folded earlier in the sweep.
+    for (auto& node : g.nodes) {
+        if (node->op == kConstantOp) continue;
+        const int32_t type = elementwise_type(node->op);
+        if (type == kNodeInvalid) continue;
+        std::vector<double> operands;
+        bool all = true;
+        for (const std::string& name : node->inputs) {
+            auto it = values.find(name);
+            if (it == values.end()) {
+                all = false;
+                break;
+            }
+            operands.push_back(it->second);
+        }
+        if (!all) continue;
+        double r = 0.0;
+        bool ok = false;
+        const int arity = node_arity(type);
+        if (arity == 1 && operands.size() == 1) ok = evaluate_unary(type, operands[0], &r);
+        if (arity == 2 && operands.size() == 2) ok = evaluate_binary(type, operands[0], operands[1], &r);
+        if (!ok) continue;
+        node->op = kConstantOp;
+        node->inputs.clear();
+        node->attributes[kConstantValue] = r;
+        values[node->id] = r;
+        folded++;
+    }
+    if (folded_out) *folded_out = folded;
+    return MFH_OK;
+}
+
+// ---- EmitHIP for a fused node ------------------------------------------------
+
+int flatten_checked(const ASTNode& n, std::vector<mfh_ast_node>& out)
+{
+    const int arity = node_arity(n.type);
+    if (arity < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: unsupported node type %d", n.type);
+    if ((int)n.children.size() != arity)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: a node of type %d has %d children, its arity is %d",
+                    n.type, (int)n.children.size(), arity);
+    out.push_back(mfh_ast_node{n.type, n.input_index, n.value});
+    for (const auto& c : n.children) MFH_TRY(flatten_checked(*c, out));
+    return MFH_OK;
+}
+
+// The dtype a node's output is stored in: OutputType, else the FusionAST /
+// graph execution dtype, else Float32 (CPUKernel's output, codegen/cpu.go:59).
+int output_dtype(uint8_t output_type, uint8_t fallback, uint8_t* out)
+{
+    uint8_t dt = output_type != kInvalid ? output_type : fallback != kInvalid ? fallback : (uint8_t)kFloat32;
+    if (!hip_storage(dt))
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "codegen hip: output dtype %s is not Float32/Float16/BFloat16",
+                    dtype_name(dt));
+    *out = dt;
+    return MFH_OK;
+}
+
+int emit_node_kernel(const ASTNode& root, const std::vector<std::string>& ports, const std::string& identifier,
+                     const std::vector<uint8_t>& input_types, uint8_t out_dtype, uint32_t flags,
+                     std::shared_ptr<HIPKernel>* out)
+{
+    auto k = std::make_shared<HIPKernel>();
+    k->identifier = identifier;
+    k->inputs = ports;
+    k->out_dtype = out_dtype;
+    k->flags = flags;
+    MFH_TRY(flatten_checked(root, k->nodes));
+    std::vector<mfh_operand> ops(ports.size());
+    for (size_t i = 0; i < ports.size(); i++) {
+        uint8_t dt = i < input_types.size() ? input_types[i] : (uint8_t)kInvalid;
+        if (dt != kInvalid && !hip_storage(dt))
+            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "codegen hip: input %d (\"%s\") is %s; the HIP target reads "
+                        "Float32, Float16 and BFloat16", (int)i, ports[i].c_str(), dtype_name(dt));
+        k->declared.push_back(dt);
+        ops[i] = mfh_operand{dt != kInvalid ? dt : (uint8_t)kFloat32, MFH_OPERAND_FULL, {0}, 0};
+    }
+    MFH_TRY(k->variant(ops, &k->full));
+    *out = std::move(k);
+    return MFH_OK;
+}
+
+int attach_kernels(Graph& g, const int32_t* targets, int32_t n_targets, uint32_t flags, int32_t* attached_out)
+{
+    int32_t attached = 0;
+    auto done = [&](int rc) {
+        if (attached_out) *attached_out = attached;
+        return rc;
+    };
+    if (g.codegen_flags != flags)
+        for (auto& node : g.nodes) node->solo.reset();
+    g.codegen_flags = flags;
+    std::vector<int32_t> ts;
+    if (targets && n_targets > 0) ts.assign(targets, targets + n_targets);
+    else ts.push_back(MFH_TARGET_HIP);
+    for (auto& node : g.nodes) {
+        if (!node || node->op != kFuseOp) continue;
+        if (!node->fusion || !node->fusion->root)
+            return done(fail(MFH_ERR_INVALID_ARGUMENT, "codegen: fused node \"%s\" missing \"%s\" attribute",
+                             node->id.c_str(), kFuseAttributeAST));
+        auto set = std::make_shared<KernelSet>();
+        for (int32_t t : ts) {
+            if (t != MFH_TARGET_HIP) continue;  // no CPU / Metal emitter in this library
+            uint8_t odt;
+            std::shared_ptr<HIPKernel> k;
+            int rc = output_dtype(node->output_type, node->fusion->dtype, &odt);
+            if (rc == MFH_OK)
+                rc = emit_node_kernel(*node->fusion->root, node->fusion->input_ports, node->fusion->output_port,
+                                      node->input_types, odt, flags, &k);
+            if (rc != MFH_OK) {
+                std::string msg = mfh_last_error();
+                return done(fail(rc, "codegen: emit \"%s\": %s", node->id.c_str(), msg.c_str()));
+            }
+            set->kernels[t] = std::move(k);
+        }
+        node->kernels = std::move(set);
+        attached++;
+    }
+    return done(MFH_OK);
+}
+
+// ---- execution ---------------------------------------------------------------
+
+constexpr int64_t kAlign = 256;
+int64_t align_up(int64_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct Slot {
+    enum Kind { kInput, kConst, kArena, kBound } kind = kArena;
+    void* ptr = nullptr;  // inputs and bound outputs
+    int64_t offset = 0;   // arena / constant offset in the workspace
+    uint8_t dtype = kFloat32;
+    int64_t count = 0;
+    int last_use = -1;
+};
+
+struct Step {
+    HIPKernel* kernel = nullptr;
+    std::vector<int> operands;
+    std::vector<mfh_operand> ops;
+    int result = -1;
+    int64_t count = 0;
+};
+
+struct Copy {
+    int slot;
+    const mfh_value* to;
+};
+
+// First-fit placement of lifetimes in one region.
+struct Placer {
+    std::map<int64_t, int64_t> free;  // offset -> bytes
+    int64_t top = 0;
+    int64_t take(int64_t bytes)
+    {
+        for (auto it = free.begin(); it != free.end(); ++it) {
+            if (it->second < bytes) continue;
+            int64_t at = it->first, left = it->second - bytes;
+            free.erase(it);
+            if (left > 0) free.emplace(at + bytes, left);
+            return at;
+        }
+        int64_t at = top;
+        top += bytes;
+        return at;
+    }
+    void give(int64_t at, int64_t bytes)
+    {
+        auto it = free.emplace(at, bytes).first;
+        auto next = std::next(it);
+        if (next != free.end() && it->first + it->second == next->first) {
+            it->second += next->second;
+            free.erase(next);
+        }
+        if (it != free.begin()) {
+            auto prev = std::prev(it);
+            if (prev->first + prev->second == it->first) {
+                prev->second += it->second;
+                free.erase(it);
+            }
+        }
+    }
+};
+
+int operand_mode(int64_t c, int64_t n, mfh_operand* op)
+{
+    if (c == n) op->mode = MFH_OPERAND_FULL;
+    else if (c == 1) op->mode = MFH_OPERAND_SCALAR;
+    else if (c > 1 && n % c == 0) {
+        op->mode = MFH_OPERAND_PERIODIC;
+        op->period = c;
+    } else
+        return MFH_ERR_SHAPE_MISMATCH;
+    return MFH_OK;
+}
+
+int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
+               hipStream_t stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    if ((n_inputs > 0 && !inputs) || (n_outputs > 0 && !outputs) || n_inputs < 0 || n_outputs < 0)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: bad value list");
+
+    std::vector<Slot> slots;
+    std::unordered_map<std::string, int> named;  // value name -> latest slot
+    std::set<std::string> graph_inputs(g.inputs.begin(), g.inputs.end());
+    for (int32_t i = 0; i < n_inputs; i++) {
+        const mfh_value& v = inputs[i];
+        std::string name = v.name ? v.name : "";
+        if (!graph_inputs.count(name)) return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: unknown input \"%s\"", name.c_str());
+        if (named.count(name)) return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: input \"%s\" bound twice", name.c_str());
+        if (!hip_storage(v.dtype))
+            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "graph call: input \"%s\" is %s; values are Float32/Float16/BFloat16",
+                        name.c_str(), dtype_name(v.dtype));
+        if (v.count < 0 || (v.count > 0 && !v.data))
+            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: input \"%s\" has no data", name.c_str());
+        Slot s;
+        s.kind = Slot::kInput;
+        s.ptr = v.data;
+        s.dtype = v.dtype;
+        s.count = v.count;
+        named[name] = (int)slots.size();
+        slots.push_back(s);
+    }
+    // Output bindings by value name.
+    std::multimap<std::string, const mfh_value*> bound;
+    for (int32_t i = 0; i < n_outputs; i++) {
+        std::string key = outputs[i].name ? outputs[i].name : "";
+        auto it = std::find_if(g.outputs.begin(), g.outputs.end(), [&](const auto& kv) { return kv.first == key; });
+        if (it == g.outputs.end()) return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: unknown output \"%s\"", key.c_str());
+        bound.emplace(it->second, &outputs[i]);
+    }
+    std::unordered_map<std::string, int> last_def;
+    for (int i = 0; i < (int)g.nodes.size(); i++) last_def[g.nodes[i]->id] = i;
+
+    std::vector<float> constants;
+    std::vector<Step> steps;
+    std::vector<Copy> copies;
+    for (int i = 0; i < (int)g.nodes.size(); i++) {
+        GraphNode& node = *g.nodes[i];
+        if (node.op == kConstantOp) {
+            auto it = node.attributes.find(kConstantValue);
+            if (it == node.attributes.end())
+                return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: constant \"%s\" has no value", node.id.c_str());
+            Slot s;
+            s.kind = Slot::kConst;
+            s.offset = (int64_t)constants.size() * 4;
+            s.count = 1;
+            constants.push_back((float)it->second);  // fl32(Value), codegen/cpu.go:130-131
+            named[node.id] = (int)slots.size();
+            slots.push_back(s);
+            continue;
+        }
+        HIPKernel* kernel = nullptr;
+        if (node.op == kFuseOp) {
+            kernel = node.kernels ? node.kernels->For(MFH_TARGET_HIP) : nullptr;
+            if (!kernel)
+                return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: fused node \"%s\" has no HIP kernel attached",
+                            node.id.c_str());
+            if (kernel->inputs.size() != node.inputs.size())
+                return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: fused node \"%s\" has %d inputs, its kernel %d",
+                            node.id.c_str(), (int)node.inputs.size(), (int)kernel->inputs.size());
+        } else if (int32_t type = elementwise_type(node.op)) {
+            if (!node.solo) {
+                if ((int)node.inputs.size() != node_arity(type))
+                    return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" (%s) has %d inputs, want %d",
+                                node.id.c_str(), node.op.c_str(), (int)node.inputs.size(), node_arity(type));
+                ASTNode root;
+                root.type = type;
+                for (size_t k = 0; k < node.inputs.size(); k++) root.children.push_back(input_leaf((int)k));
+                uint8_t odt;
+                MFH_TRY(output_dtype(node.output_type, g.execution_dtype, &odt));
+                MFH_TRY(emit_node_kernel(root, node.inputs, node.id, node.input_types, odt, g.codegen_flags,
+                                         &node.solo));
+            }
+            kernel = node.solo.get();
+        } else {
+            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\": op \"%s\" has no HIP lowering",
+                        node.id.c_str(), node.op.c_str());
+        }
+        Step st;
+        st.kernel = kernel;
+        for (const std::string& name : node.inputs) {
+            auto it = named.find(name);
+            if (it == named.end())
+                return fail(MFH_ERR_INVALID_ARGUMENT,
+                            "graph call: node \"%s\" reads \"%s\", which is neither a bound input nor an earlier node",
+                            node.id.c_str(), name.c_str());
+            st.operands.push_back(it->second);
+            st.count = std::max(st.count, slots[it->second].count);
+        }
+        for (size_t k = 0; k < st.operands.size(); k++) {
+            Slot& s = slots[st.operands[k]];
+            mfh_operand op{s.dtype, MFH_OPERAND_FULL, {0}, 0};
+            if (operand_mode(s.count, st.count, &op) != MFH_OK)
+                return fail(MFH_ERR_SHAPE_MISMATCH, "graph call: node \"%s\": operand \"%s\" has %lld elements, "
+                            "the node %lld", node.id.c_str(), node.inputs[k].c_str(), (long long)s.count,
+                            (long long)st.count);
+            if (k < kernel->declared.size() && kernel->declared[k] != kInvalid && kernel->declared[k] != s.dtype)
+                return fail(MFH_ERR_DTYPE_UNSUPPORTED, "graph call: node \"%s\": operand \"%s\" is %s, declared %s",
+                            node.id.c_str(), node.inputs[k].c_str(), dtype_name(s.dtype),
+                            dtype_name(kernel->declared[k]));
+            st.ops.push_back(op);
+            s.last_use = (int)steps.size();  // index of the step being built
+        }
+        Slot out;
+        out.dtype = kernel->out_dtype;
+        out.count = st.count;
+        out.kind = Slot::kArena;
+        // The node that finally defines a bound output writes straight into
+        // the caller's buffer when it matches.
+        auto range = bound.equal_range(node.id);
+        if (last_def[node.id] == i && range.first != range.second) {
+            const mfh_value* b = range.first->second;
+            if (b->dtype == out.dtype && b->count == out.count && b->data) {
+                out.kind = Slot::kBound;
+                out.ptr = b->data;
+            }
+        }
+        st.result = (int)slots.size();
+        named[node.id] = st.result;
+        slots.push_back(out);
+        steps.push_back(std::move(st));
+    }
+    // Bound outputs not written in place are copied at the end.
+    for (const auto& kv : bound) {
+        auto it = named.find(kv.first);
+        if (it == named.end())
+            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: output value \"%s\" is never defined", kv.first.c_str());
+        Slot& s = slots[it->second];
+        const mfh_value* b = kv.second;
+        if (b->dtype != s.dtype || b->count != s.count)
+            return fail(b->dtype != s.dtype ? MFH_ERR_DTYPE_UNSUPPORTED : MFH_ERR_SHAPE_MISMATCH,
+                        "graph call: output \"%s\" holds %s[%lld]; value \"%s\" is %s[%lld]", b->name,
+                        dtype_name(b->dtype), (long long)b->count, kv.first.c_str(), dtype_name(s.dtype),
+                        (long long)s.count);
+        if (s.count > 0 && !b->data)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: output \"%s\" has no data", b->name);
+        if (s.kind == Slot::kBound && s.ptr == b->data) continue;
+        s.last_use = (int)steps.size() + 1;  // alive until the copies
+        copies.push_back(Copy{it->second, b});
+    }
+
+    // Workspace layout: constants, then intermediates placed by lifetime.  A
+    // value is released after the last step that reads it (at once if none
+    // does); the result of a step is placed before its operands are released,
+    // so a kernel never writes over its own inputs.
+    const int n_steps = (int)steps.size();
+    const int64_t const_bytes = align_up((int64_t)constants.size() * 4);
+    std::vector<std::vector<int>> frees(n_steps);
+    for (int t = 0; t < n_steps; t++) {
+        const int r = steps[t].result;
+        if (slots[r].kind == Slot::kArena && slots[r].last_use < 0) slots[r].last_use = t;
+    }
+    for (int i = 0; i < (int)slots.size(); i++)
+        if (slots[i].kind == Slot::kArena && slots[i].last_use >= 0 && slots[i].last_use < n_steps)
+            frees[slots[i].last_use].push_back(i);
+    auto slot_bytes = [](const Slot& s) { return align_up(std::max<int64_t>(1, s.count) * dtype_size(s.dtype)); };
+    Placer placer;
+    for (int t = 0; t < n_steps; t++) {
+        Slot& r = slots[steps[t].result];
+        if (r.kind == Slot::kArena) r.offset = const_bytes + placer.take(slot_bytes(r));
+        for (int i : frees[t]) placer.give(slots[i].offset - const_bytes, slot_bytes(slots[i]));
+    }
+    const int64_t need = const_bytes + placer.top;
+    if (need > g.ws_bytes) {
+        if (g.ws) {
+            // the previous workspace may still be read by queued work
+            MFH_TRY(check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize"));
+            MFH_TRY(check_hip(hipFree(g.ws), "hipFree"));
+            g.ws = nullptr;
+            g.ws_bytes = 0;
+        }
+        MFH_TRY(check_hip(hipMalloc(&g.ws, (size_t)need), "hipMalloc(graph workspace)"));
+        g.ws_bytes = need;
+        g.ws_constants_valid = false;
+    }
+    if (!constants.empty() && (!g.ws_constants_valid || g.ws_constants != constants)) {
+        g.ws_constants = constants;
+        MFH_TRY(check_hip(hipMemcpyAsync(g.ws, g.ws_constants.data(), constants.size() * 4, hipMemcpyHostToDevice,
+                                         stream), "hipMemcpyAsync(graph constants)"));
+        g.ws_constants_valid = true;
+    }
+    char* base = static_cast<char*>(g.ws);
+    auto addr = [&](const Slot& s) -> void* {
+        return s.kind == Slot::kInput || s.kind == Slot::kBound ? s.ptr : base + s.offset;
+    };
+    std::vector<const void*> ptrs;
+    for (const Step& st : steps) {
+        const mfh_kernel* k = nullptr;
+        MFH_TRY(st.kernel->variant(st.ops, &k));
+        ptrs.clear();
+        for (int o : st.operands) ptrs.push_back(addr(slots[o]));
+        MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, stream));
+    }
+    for (const Copy& c : copies) {
+        const Slot& s = slots[c.slot];
+        const size_t bytes = (size_t)s.count * dtype_size(s.dtype);
+        if (bytes)
+            MFH_TRY(check_hip(hipMemcpyAsync(c.to->data, addr(s), bytes, hipMemcpyDeviceToDevice, stream),
+                              "hipMemcpyAsync(graph output)"));
+    }
+    return MFH_OK;
+}
+
+}  // namespace
+}  // namespace mfh
+using namespace mfh;
+
+namespace {
+
+GraphNode* node_at(const mfh_graph* g, int32_t i)
+{
+    if (!g || i < 0 || i >= (int32_t)g->nodes.size()) return nullptr;
+    return g->nodes[i].get();
+}
+
+int bad_node(const char* what, int32_t i)
+{
+    return fail(MFH_ERR_INVALID_ARGUMENT, "%s: no node %d", what, (int)i);
+}
+
+std::string str_or_empty(const char* s) { return s ? s : ""; }
+
+// Rebuilds a tree from its pre-order list; `pos` advances past the subtree.
+int parse_tree(const mfh_ast_node* nodes, const int32_t* child_counts, int32_t n, int32_t* pos,
+               std::unique_ptr<ASTNode>* out, int depth)
+{
+    if (*pos >= n) return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: the node list ends inside the tree");
+    if (depth > 4096) return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: tree deeper than 4096");
+    const int32_t at = (*pos)++;
+    auto node = std::make_unique<ASTNode>();
+    node->type = nodes[at].type;
+    node->input_index = nodes[at].input_index;
+    node->value = nodes[at].value;
+    int32_t kids = child_counts ? child_counts[at] : node_arity(node->type);
+    if (kids < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: node %d has unknown type %d", (int)at, node->type);
+    for (int32_t c = 0; c < kids; c++) {
+        std::unique_ptr<ASTNode> child;
+        MFH_TRY(parse_tree(nodes, child_counts, n, pos, &child, depth + 1));
+        node->children.push_back(std::move(child));
+    }
+    *out = std::move(node);
+    return MFH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mfh_graph_create(uint8_t execution_dtype, mfh_graph** graph)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_create: graph out-pointer is NULL");
+    *graph = new mfh_graph();
+    (*graph)->execution_dtype = execution_dtype;
+    return MFH_OK;
+}
+
+int mfh_graph_release(mfh_graph* graph)
+{
+    if (!graph) return MFH_OK;
+    int rc = MFH_OK;
+    if (graph->ws) {
+        const Device* dev;
+        rc = bind_device(&dev);
+        if (rc == MFH_OK) rc = check_hip(hipFree(graph->ws), "hipFree(graph workspace)");
+    }
+    delete graph;
+    return rc;
+}
+
+int mfh_graph_add_input(mfh_graph* graph, const char* name)
+{
+    if (!graph || !name) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_input: graph and name are required");
+    graph->inputs.push_back(name);
+    return MFH_OK;
+}
+
+int mfh_graph_set_output(mfh_graph* graph, const char* key, const char* value)
+{
+    if (!graph || !key || !value)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_output: graph, key and value are required");
+    for (auto& kv : graph->outputs)
+        if (kv.first == key) {
+            kv.second = value;
+            return MFH_OK;
+        }
+    graph->outputs.emplace_back(key, value);
+    return MFH_OK;
+}
+
+int mfh_graph_add_node(mfh_graph* graph, const char* id, const char* op, const char* const* inputs, int32_t n_inputs)
+{
+    if (!graph || !id || !op) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_node: graph, id and op are required");
+    if (n_inputs < 0 || (n_inputs > 0 && !inputs))
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_node: bad input list");
+    auto node = std::make_unique<GraphNode>();
+    node->id = id;
+    node->op = op;
+    for (int32_t k = 0; k < n_inputs; k++) {
+        if (!inputs[k]) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_node: input %d is NULL", (int)k);
+        node->inputs.push_back(inputs[k]);
+    }
+    graph->nodes.push_back(std::move(node));
+    return MFH_OK;
+}
+
+int mfh_graph_set_attribute(mfh_graph* graph, int32_t node, const char* key, double value)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n) return bad_node("mfh_graph_set_attribute", node);
+    if (!key) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_attribute: key is NULL");
+    n->attributes[key] = value;
+    return MFH_OK;
+}
+
+int mfh_graph_set_types(mfh_graph* graph, int32_t node, const uint8_t* input_types, int32_t n_input_types,
+                        uint8_t output_type)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n) return bad_node("mfh_graph_set_types", node);
+    if (n_input_types < 0 || (n_input_types > 0 && !input_types))
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_types: bad type list");
+    n->input_types.assign(input_types, input_types + n_input_types);
+    n->output_type = output_type;
+    return MFH_OK;
+}
+
+int mfh_graph_set_fusion(mfh_graph* graph, int32_t node, const mfh_ast_node* nodes, const int32_t* child_counts,
+                         int32_t n_nodes, const char* const* input_ports, int32_t n_input_ports,
+                         const char* output_port, uint8_t dtype)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n) return bad_node("mfh_graph_set_fusion", node);
+    if (!nodes || n_nodes <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: root is required");
+    if (n_input_ports < 0 || (n_input_ports > 0 && !input_ports))
+        return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: bad input port list");
+    auto f = std::make_shared<FusionAST>();
+    int32_t pos = 0;
+    MFH_TRY(parse_tree(nodes, child_counts, n_nodes, &pos, &f->root, 0));
+    if (pos != n_nodes)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: %d node(s) after the end of the tree", (int)(n_nodes - pos));
+    for (int32_t k = 0; k < n_input_ports; k++) f->input_ports.push_back(str_or_empty(input_ports[k]));
+    f->output_port = str_or_empty(output_port);
+    f->dtype = dtype;
+    n->fusion = std::move(f);
+    n->kernels.reset();
+    return MFH_OK;
+}
+
+int32_t mfh_graph_num_nodes(const mfh_graph* graph) { return graph ? (int32_t)graph->nodes.size() : -1; }
+
+const char* mfh_graph_node_id(const mfh_graph* graph, int32_t node)
+{
+    GraphNode* n = node_at(graph, node);
+    return n ? n->id.c_str() : nullptr;
+}
+
+const char* mfh_graph_node_op(const mfh_graph* graph, int32_t node)
+{
+    GraphNode* n = node_at(graph, node);
+    return n ? n->op.c_str() : nullptr;
+}
+
+int32_t mfh_graph_node_num_inputs(const mfh_graph* graph, int32_t node)
+{
+    GraphNode* n = node_at(graph, node);
+    return n ? (int32_t)n->inputs.size() : -1;
+}
+
+const char* mfh_graph_node_input(const mfh_graph* graph, int32_t node, int32_t slot)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n || slot < 0 || slot >= (int32_t)n->inputs.size()) return nullptr;
+    return n->inputs[slot].c_str();
+}
+
+int mfh_graph_node_attribute(const mfh_graph* graph, int32_t node, const char* key, double* value)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n) return bad_node("mfh_graph_node_attribute", node);
+    auto it = key ? n->attributes.find(key) : n->attributes.end();
+    if (it == n->attributes.end())
+        return fail(MFH_ERR_INVALID_ARGUMENT, "node \"%s\" has no attribute \"%s\"", n->id.c_str(), key ? key : "");
+    if (value) *value = it->second;
+    return MFH_OK;
+}
+
+const char* mfh_graph_node_attribute_key(const mfh_graph* graph, int32_t node, int32_t k)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n || k < 0 || k >= (int32_t)n->attributes.size()) return nullptr;
+    auto it = n->attributes.begin();
+    std::advance(it, k);
+    return it->first.c_str();
+}
+
+int mfh_graph_node_metadata(const mfh_graph* graph, int32_t node, const char* key, int64_t* value)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n) return bad_node("mfh_graph_node_metadata", node);
+    auto it = key ? n->metadata.find(key) : n->metadata.end();
+    if (it == n->metadata.end())
+        return fail(MFH_ERR_INVALID_ARGUMENT, "node \"%s\" has no metadata \"%s\"", n->id.c_str(), key ? key : "");
+    if (value) *value = it->second;
+    return MFH_OK;
+}
+
+int32_t mfh_graph_node_types(const mfh_graph* graph, int32_t node, uint8_t* input_types, int32_t cap,
+                             uint8_t* output_type)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n) return -1;
+    for (int32_t k = 0; input_types && k < cap && k < (int32_t)n->input_types.size(); k++)
+        input_types[k] = n->input_types[k];
+    if (output_type) *output_type = n->output_type;
+    return (int32_t)n->input_types.size();
+}
+
+int mfh_graph_fusion(const mfh_graph* graph, int32_t node, mfh_fusion_info* info)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n) return bad_node("mfh_graph_fusion", node);
+    if (!n->fusion) return fail(MFH_ERR_INVALID_ARGUMENT, "node \"%s\" holds no FusionAST", n->id.c_str());
+    if (!info) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_fusion: info is NULL");
+    FusionAST& f = *n->fusion;
+    f.flatten();
+    info->nodes = f.flat.data();
+    info->child_counts = f.child_counts.data();
+    info->n_nodes = (int32_t)f.flat.size();
+    info->n_input_ports = (int32_t)f.input_ports.size();
+    info->n_contained = (int32_t)f.contained_node_ids.size();
+    info->dtype = f.dtype;
+    info->output_port = f.output_port.c_str();
+    info->count_expr = f.count_expr.c_str();
+    return MFH_OK;
+}
+
+const char* mfh_graph_fusion_input_port(const mfh_graph* graph, int32_t node, int32_t k)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n || !n->fusion || k < 0 || k >= (int32_t)n->fusion->input_ports.size()) return nullptr;
+    return n->fusion->input_ports[k].c_str();
+}
+
+const char* mfh_graph_fusion_contained_id(const mfh_graph* graph, int32_t node, int32_t k)
+{
+    GraphNode* n = node_at(graph, node);
+    if (!n || !n->fusion || k < 0 || k >= (int32_t)n->fusion->contained_node_ids.size()) return nullptr;
+    return n->fusion->contained_node_ids[k].c_str();
+}
+
+int32_t mfh_optimizer_is_elementwise_op(const char* op) { return op ? elementwise_type(op) : kNodeInvalid; }
+
+int32_t mfh_optimizer_elementwise_ops(const char** ops, int32_t cap)
+{
+    int32_t count = 0;
+    for (const OpEntry& row : kElementwiseTable) {
+        if (row.type == kNodeInvalid) continue;
+        if (ops && count < cap) ops[count] = row.op;
+        count++;
+    }
+    return count;
+}
+
+int mfh_optimizer_constant_fold(mfh_graph* graph, int32_t* nodes_folded)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
+    return constant_fold(*graph, nodes_folded);
+}
+
+int mfh_optimizer_fuse(mfh_graph* graph, mfh_fusion_stats* stats)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
+    return fuse(*graph, stats);
+}
+
+int mfh_optimizer_run(mfh_graph* graph, uint32_t options, int32_t* nodes_folded, mfh_fusion_stats* stats)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
+    if (nodes_folded) *nodes_folded = 0;
+    if (stats) *stats = mfh_fusion_stats{0, 0, 0};
+    if (!(options & MFH_OPT_DISABLE_CONSTANT_FOLD)) MFH_TRY(constant_fold(*graph, nodes_folded));
+    if (!(options & MFH_OPT_DISABLE_FUSION)) MFH_TRY(fuse(*graph, stats));
+    return MFH_OK;
+}
+
+int mfh_codegen_attach_kernels(mfh_graph* graph, const int32_t* targets, int32_t n_targets, uint32_t flags,
+                               int32_t* attached)
+{
+    if (attached) *attached = 0;
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen: graph is required");
+    return attach_kernels(*graph, targets, n_targets, flags, attached);
+}
+
+int mfh_graph_kernel(const mfh_graph* graph, int32_t node, int32_t target, const mfh_kernel** kernel)
+{
+    if (!kernel) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_kernel: kernel out-pointer is NULL");
+    *kernel = nullptr;
+    GraphNode* n = node_at(graph, node);
+    if (!n) return bad_node("mfh_graph_kernel", node);
+    HIPKernel* k = n->kernels ? n->kernels->For(target) : nullptr;
+    if (k) *kernel = k->full;
+    return MFH_OK;
+}
+
+int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
+                   int32_t n_outputs, void* stream)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: graph is required");
+    return graph_call(*graph, inputs, n_inputs, outputs, n_outputs, (hipStream_t)stream);
+}
+
+int64_t mfh_graph_workspace_bytes(const mfh_graph* graph) { return graph ? graph->ws_bytes : -1; }
+
+}  // extern "C"
