@@ -231,36 +231,34 @@ WORKLOADS = [Axpy, Fp8, SwiGLU, GeluChain, Int4]
 
 
 def time_gpu(w, steps, warmup, use_graph=True):
+    """Runs `warmup` untimed steps, then times exactly `steps` steps (each one
+    launch over the next rotated buffer set) between two events on the
+    launch stream.  With use_graph the `steps` launches are captured into one
+    HIP graph that is replayed once untimed and once timed, so the timed
+    region holds back-to-back kernels with no host launch gaps."""
     torch = w.torch
     for i in range(max(warmup, len(w.sets))):
         w.step(i)
     torch.cuda.synchronize()
-    reps = len(w.sets)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if use_graph:
         graph = torch.cuda.CUDAGraph()
         cap = torch.cuda.Stream()
         with torch.cuda.stream(cap):
             with torch.cuda.graph(graph, stream=cap):
-                for i in range(reps):
+                for i in range(steps):
                     w.step(i)
         torch.cuda.synchronize()
-        replays = max(1, -(-steps // reps))
         graph.replay()  # warm
         torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s = torch.cuda.current_stream()
-        torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record(s)
-        for _ in range(replays):
-            graph.replay()
+        graph.replay()
         end.record(s)
         end.synchronize()
-        torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        n = replays * reps
     else:
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s = torch.cuda.current_stream()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -269,9 +267,8 @@ def time_gpu(w, steps, warmup, use_graph=True):
             w.step(i)
         end.record(s)
         end.synchronize()
-        torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        n = steps
+    n = steps
     ms = start.elapsed_time(end) / n
     return ms, n, wall
 
@@ -380,7 +377,7 @@ def main():
         "data": "synthetic (seeded torch RNG on device; uniform bytes over all 256 codes)",
         "config": {"workload": "BASELINE config 2: fp8_e4m3 -> bf16 dequant [4096,14336], scale 0.0125",
                    "elements": Fp8.n, "algorithmic_bytes_per_step": Fp8.bytes_per_step,
-                   "timing": "HIP events on the launch stream around graph replays of rotated buffer sets"},
+                   "timing": "HIP events on the launch stream around one replay of a graph of K launches over rotated buffer sets"},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": load_traffic(), "kernel": head["kernel"]},
         "cpu_baseline": head.get("cpu_baseline"),

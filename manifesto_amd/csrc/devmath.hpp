@@ -12,6 +12,8 @@
 //   e^a:          Cody & Waite reduction a = k ln2 + r (ln2 split into a
 //                 16-bit head and an f32 tail), e^r by a degree-6 polynomial
 //                 (constants from gen_exp_poly.py), then scaled by 2^k.
+//   2^f:          for |f| <= 1/2 a degree-6 polynomial (gen_exp_poly.py),
+//                 used where the argument is formed and reduced in f64.
 //   n * sigmoid(z) = n / (1 + E), E = e^-z, with z clamped (v_med3) to the
 //                 range where E is a finite f32, the exact tail of 1 + E
 //                 recovered by Fast2Sum, and the quotient corrected by one
@@ -19,6 +21,13 @@
 //                 result underflows or the reference cancels) and NaN take
 //                 the f64 reference form, a branch no wave enters for normal
 //                 data.
+//
+// Cost on gfx950 (measured issue rates, in units of one f32 FMA): f32
+// add/mul/fma 1; conversions, ldexp, rndne, med3, min/max, compares and
+// selects ~1.5; f64 add/mul ~1.7; f64 fma 2; v_rcp_f32 3.3; v_rcp_f64 6.
+// Plain f32 arithmetic is what is cheap, so the kernels reduce in f32 where
+// the argument allows and use f64 only to form an argument that f32 cannot
+// hold precisely enough (gelu's cubic).
 #ifndef MFH_DEVMATH_HPP
 #define MFH_DEVMATH_HPP
 
@@ -28,6 +37,7 @@
 #define mfh_fmaf(a, b, c) std::fma((float)(a), (float)(b), (float)(c))
 #define mfh_fma(a, b, c) std::fma((double)(a), (double)(b), (double)(c))
 #define mfh_rintf(x) std::nearbyint((float)(x))
+#define mfh_rint(x) std::nearbyint((double)(x))
 #define mfh_ldexpf(x, k) std::ldexp((float)(x), (int)(k))
 #define mfh_rcpf(x) (1.0f / (float)(x))
 #define mfh_tanh_f64(x) std::tanh((double)(x))
@@ -47,6 +57,7 @@ extern "C" __device__ double __ocml_log_f64(double);
 #define mfh_fmaf(a, b, c) __builtin_fmaf((a), (b), (c))
 #define mfh_fma(a, b, c) __builtin_fma((a), (b), (c))
 #define mfh_rintf(x) __builtin_rintf(x)
+#define mfh_rint(x) __builtin_rint(x)
 #define mfh_ldexpf(x, k) __builtin_amdgcn_ldexpf((x), (k))
 #define mfh_rcpf(x) __builtin_amdgcn_rcpf(x)
 #define mfh_tanh_f64(x) __ocml_tanh_f64(x)
@@ -82,6 +93,18 @@ MFH_MATH float mfh_exp_poly(float r)
     return mfh_fmaf(q, r, 1.0f);
 }
 
+// 2^f for |f| <= 1/2: 1 + f(c1 + f(c2 + ... + f c6)), within 0.94 f32 ulp.
+MFH_MATH float mfh_exp2_poly(float f)
+{
+    float q = 0.00015370704932138324f;           // 0x39212c6c
+    q = mfh_fmaf(q, f, 0.0013399848248809576f);  // 0x3aafa26e
+    q = mfh_fmaf(q, f, 0.009618373587727547f);   // 0x3c1d9662
+    q = mfh_fmaf(q, f, 0.05550329014658928f);    // 0x3d63576b
+    q = mfh_fmaf(q, f, 0.24022647738456726f);    // 0x3e75fdee
+    q = mfh_fmaf(q, f, 0.6931471824645996f);     // 0x3f317218
+    return mfh_fmaf(q, f, 1.0f);
+}
+
 // e^a = p * 2^k, for a in [-200, 200].
 MFH_MATH float mfh_exp_core(float a, int* k)
 {
@@ -90,17 +113,6 @@ MFH_MATH float mfh_exp_core(float a, int* k)
     r = mfh_fmaf(kf, -MFH_LN2_LO_F, r);
     *k = (int)kf;
     return mfh_exp_poly(r);
-}
-
-// Same with an f64 argument (|a| < 2^30): the reduction runs in f64, so the
-// argument's own f64 accuracy carries through to r.
-MFH_MATH float mfh_exp_core_d(double a, int* k)
-{
-    const double magic = 6755399441055744.0;  // 1.5 * 2^52: (x + magic) - magic rounds x to an integer
-    double kd = (a * MFH_LOG2E_D + magic) - magic;
-    double r = mfh_fma(kd, -MFH_LN2_D, a);
-    *k = (int)kd;
-    return mfh_exp_poly((float)r);
 }
 
 // n / (1 + E) for E = p * 2^k >= 0: Fast2Sum gives 1 + E = d + dl exactly,
@@ -117,6 +129,19 @@ MFH_MATH float mfh_div_one_plus(float n, float p, int k)
     float q = n * r;
     float res = mfh_fmaf(-q, d, n);
     res = mfh_fmaf(-q, dl, res);
+    return mfh_fmaf(res, r, q);
+}
+
+// n / (1 + E) without the tail of 1 + E: the rounding of d = fl(1 + E) is
+// left in (at most half an ulp of the quotient), which the 2-ulp Gelu budget
+// allows and saves five instructions per element.
+MFH_MATH float mfh_div_one_plus_short(float n, float p, int k)
+{
+    float e = mfh_ldexpf(p, k);
+    float d = 1.0f + e;
+    float r = mfh_rcpf(d);
+    float q = n * r;
+    float res = mfh_fmaf(-q, d, n);
     return mfh_fmaf(res, r, q);
 }
 
@@ -171,18 +196,23 @@ MFH_MATH float mfh_silu(float v)
     return s;
 }
 
-// Fast gelu = v / (1 + e^-z), z = 2 inner, inner formed in f64 in the
-// reference's operation order.  Above v = 14 the reference's tanh is exactly 1
-// in f64 and gelu(v) = v, which the clamped z reproduces.  Below v = -4.9
-// (inner < -9.3) the reference's 1 + tanh cancels in f64, so that rare range
-// (and NaN) runs the reference form itself.
+// Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
+// t = -2 inner log2(e) = d (KA + KB d^2) formed in f64 (the cubic needs more
+// than f32's 24 bits where E is large), reduced in f64 (t = k + f exactly) and
+// 2^f evaluated in f32.  Within 2 f32 ulps of the reference over every f32
+// input.  Above v = 14 the reference's tanh is exactly 1 in f64 and
+// gelu(v) = v, which the clamped d reproduces.  Below v = -4.9 (inner < -9.3)
+// the reference's 1 + tanh cancels in f64, so that rare range (and NaN) runs
+// the reference form itself.
+#define MFH_GELU_KA (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_LOG2E_D)
+#define MFH_GELU_KB (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_GELU_A_D * MFH_LOG2E_D)
 MFH_MATH float mfh_gelu(float v)
 {
     double d = (double)mfh_med3f(v, -5.0f, 14.0f);
-    double z = 2.0 * (MFH_SQRT_2_OVER_PI_D * (d + MFH_GELU_A_D * d * d * d));
-    int k;
-    float p = mfh_exp_core_d(-z, &k);
-    float s = mfh_div_one_plus(v, p, k);
+    double t = d * mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA);
+    double kd = mfh_rint(t);
+    float p = mfh_exp2_poly((float)(t - kd));
+    float s = mfh_div_one_plus_short(v, p, (int)kd);
     MFH_KEEP(s);
     s = v == __builtin_inff() ? v : s;
     if (!(v >= -4.9f)) s = mfh_gelu_ref(v);

@@ -74,6 +74,9 @@ struct Emitter {
     bool precise;
     std::string body;
     int tmp = 0;
+    // Vector loop only: inputs held as packed f16 words w<k>[u][j >> 1]
+    // (empty in the element loop).
+    std::vector<bool> packed16 = {};
 
     std::string fresh() { return "t" + std::to_string(tmp++); }
 
@@ -92,6 +95,19 @@ struct Emitter {
         case kNodeInput: return "x" + std::to_string(n.input_index);
         case kNodeConstant: return let(hex32((float)n.value));  // float32(node.Value)
         default: break;
+        }
+        if (n.type == kNodeAdd) {
+            // An f16 input leaf is added straight from its packed word.
+            auto word = [&](int child) -> std::string {
+                const mfh_ast_node& leaf = nodes[child];
+                if (leaf.type != kNodeInput || leaf.input_index >= (int)packed16.size() || !packed16[leaf.input_index])
+                    return "";
+                return "w" + std::to_string(leaf.input_index) + "[u][j >> 1]";
+            };
+            std::string wa = word(c0[idx]), wb = word(c1[idx]);
+            if (!wa.empty() && !wb.empty()) return let("mfh_add_hh(" + wa + ", j & 1, " + wb + ", j & 1)");
+            if (!wb.empty()) return let("mfh_add_fh(" + emit(c0[idx]) + ", " + wb + ", j & 1)");
+            if (!wa.empty()) return let("mfh_add_fh(" + emit(c1[idx]) + ", " + wa + ", j & 1)");
         }
         std::string a = emit(c0[idx]);
         if (node_arity(n.type) == 2) {
@@ -299,8 +315,15 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     const int auto_bpc = cost > 38 ? 24 : 4;
 
     const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
+    // Element loop: every operand decoded to f32.  Vector loop: f16 operands
+    // stay packed words so that adds can take them directly.
     Emitter em{list, c0, c1, precise, "", 0};
     std::string result = em.emit(0);
+    std::vector<bool> packed16(n_inputs, false);
+    for (int k = 0; k < n_inputs; k++)
+        packed16[k] = inputs[k].mode != MFH_OPERAND_SCALAR && inputs[k].dtype == kFloat16;
+    Emitter emv{list, c0, c1, precise, "", 0, packed16};
+    std::string vresult = emv.emit(0);
 
     std::string identifier = output_port && *output_port ? output_port : "anon";
     std::string kernel_name = "fused_" + sanitize(output_port ? output_port : "");
@@ -323,16 +346,23 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
                    std::to_string(k) + ", 0);\n";
     // vector loop: loads of all items first, then compute and store
     src += "    for (mfh_i64 v = tid; v < nvec; v += stride * " + U + ") {\n";
-    for (int k = 0; k < n_inputs; k++)
-        if (inputs[k].mode != MFH_OPERAND_SCALAR) src += "        float a" + std::to_string(k) + "[" + U + "][" + V + "];\n";
+    for (int k = 0; k < n_inputs; k++) {
+        if (inputs[k].mode == MFH_OPERAND_SCALAR) continue;
+        if (packed16[k]) src += "        mfh_u32 w" + std::to_string(k) + "[" + U + "][" + std::to_string(vec / 2) + "];\n";
+        else src += "        float a" + std::to_string(k) + "[" + U + "][" + V + "];\n";
+    }
     src += "#pragma unroll\n        for (int u = 0; u < " + U + "; u++) {\n";
     src += "            const mfh_i64 it = v + u * stride;\n            if (it < nvec) {\n";
     src += "                const mfh_i64 e0 = it * " + V + ";\n";
     for (int k = 0; k < n_inputs; k++) {
         if (inputs[k].mode == MFH_OPERAND_SCALAR) continue;
         std::string ks = std::to_string(k);
-        src += "                mfh_ld" + V + "_" + io_suffix(inputs[k].dtype) + "(p" + ks + ", " +
-               operand_index(inputs[k], "e0") + ", a" + ks + "[u]);\n";
+        if (packed16[k])
+            src += "                mfh_ldw" + V + "_f16(p" + ks + ", " + operand_index(inputs[k], "e0") + ", w" + ks +
+                   "[u]);\n";
+        else
+            src += "                mfh_ld" + V + "_" + io_suffix(inputs[k].dtype) + "(p" + ks + ", " +
+                   operand_index(inputs[k], "e0") + ", a" + ks + "[u]);\n";
     }
     src += "            }\n        }\n";
     src += "#pragma unroll\n        for (int u = 0; u < " + U + "; u++) {\n";
@@ -340,11 +370,13 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     src += "            float r[" + V + "];\n#pragma unroll\n            for (int j = 0; j < " + V + "; j++) {\n";
     for (int k = 0; k < n_inputs; k++) {
         std::string ks = std::to_string(k);
-        src += "        const float x" + ks + " = " +
-               (inputs[k].mode == MFH_OPERAND_SCALAR ? "s" + ks : "a" + ks + "[u][j]") + ";\n";
+        std::string value = inputs[k].mode == MFH_OPERAND_SCALAR ? "s" + ks
+                            : packed16[k] ? "mfh_h2f(w" + ks + "[u][j >> 1], j & 1)"
+                                          : "a" + ks + "[u][j]";
+        src += "        const float x" + ks + " = " + value + ";\n";
     }
-    src += em.body;
-    src += "                r[j] = " + result + ";\n            }\n";
+    src += emv.body;
+    src += "                r[j] = " + vresult + ";\n            }\n";
     src += "            mfh_st" + V + "_" + osfx + "(pout, it * " + V + ", r);\n        }\n    }\n";
     // scalar tail (and the whole range when the vector path is off)
     src += "    for (mfh_i64 i = nvec * " + V + " + tid; i < n; i += stride) {\n";

@@ -95,6 +95,51 @@ MFH_DEV void mfh_st4_f16(void* p, mfh_i64 e, const float* r)
     *reinterpret_cast<mfh_u32x2*>(static_cast<mfh_u16*>(p) + e) = x;
 }
 
+// ---- f16 operands kept as packed words ----
+//
+// An f16 operand of the vector path is loaded as its packed 32-bit words; an
+// element is word k/2, low half for even k.  Where the value feeds an Add the
+// kernel adds the half directly with v_fma_mix_f32 (f16 source converted
+// exactly inside the FMA, times 1.0, plus the other term, one rounding): the
+// same f32 sum as converting first and adding, in one instruction instead of
+// two or three.
+
+MFH_DEV void mfh_ldw8_f16(const void* p, mfh_i64 e, mfh_u32* w)
+{
+    mfh_u32x4 x = *reinterpret_cast<const mfh_u32x4*>(static_cast<const mfh_u16*>(p) + e);
+#pragma unroll
+    for (int k = 0; k < 4; k++) w[k] = x[k];
+}
+
+MFH_DEV void mfh_ldw4_f16(const void* p, mfh_i64 e, mfh_u32* w)
+{
+    mfh_u32x2 x = *reinterpret_cast<const mfh_u32x2*>(static_cast<const mfh_u16*>(p) + e);
+    w[0] = x[0];
+    w[1] = x[1];
+}
+
+MFH_DEV float mfh_h2f(mfh_u32 w, int hi) { return mfh_f16_to_f32(hi ? w >> 16 : w & 0xffffu); }
+
+// x + half `hi` of w.  `hi` must fold to a constant (an unrolled index).
+MFH_DEV float mfh_add_fh(float x, mfh_u32 w, int hi)
+{
+    float r;
+    if (hi) __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(x));
+    else __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(x));
+    return r;
+}
+
+// half `ha` of a + half `hb` of b.
+MFH_DEV float mfh_add_hh(mfh_u32 a, int ha, mfh_u32 b, int hb)
+{
+    float r;
+    if (ha && hb) __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+    else if (ha) __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+    else if (hb) __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+    else __asm__("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // ---- single elements (tails, unaligned buffers, scalar operands) ----
 
 MFH_DEV float mfh_ld1_f32(const void* p, mfh_i64 i) { return static_cast<const float*>(p)[i]; }

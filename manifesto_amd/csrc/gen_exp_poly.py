@@ -1,11 +1,16 @@
-"""Derives the constants of the f32 exp kernel in devmath.hpp.
+"""Derives the constants of the f32 exponential kernels in devmath.hpp.
 
 e^x = 2^k * e^r with k = rint(x / ln2) and r = x - k*ln2 (Cody & Waite range
 reduction, ln2 split into a 16-bit head, so k*head is exact for |k| < 256, and
 an f32 tail).  e^r on |r| <= ln2/2 (plus a margin for the f32 rounding of
 x/ln2) is a degree-6 polynomial with the constant term pinned to 1, fitted by
 weighted least squares on Chebyshev nodes for relative error and rounded to
-f32.  Run: python3 gen_exp_poly.py
+f32.
+
+2^f on |f| <= 1/2 (the fraction left when the argument is already in log2
+units and reduced in f64) is fitted the same way.
+
+Run: python3 gen_exp_poly.py
 """
 import math
 
@@ -35,6 +40,16 @@ def fit(degree=6, half_width=0.3466 + 2e-5, nodes=4000):
     return [F32(c) for c in coef]
 
 
+def fit_exp2(degree=6, half_width=0.5, nodes=4000):
+    k = np.arange(nodes)
+    f = half_width * np.cos(np.pi * (k + 0.5) / nodes)
+    target = np.expm1(f * math.log(2.0))  # 2^f - 1 = f * q(f)
+    basis = np.stack([f ** (j + 1) for j in range(degree)], axis=1)
+    w = 1.0 / np.exp2(f)
+    coef, *_ = np.linalg.lstsq(basis * w[:, None], target * w, rcond=None)
+    return [F32(c) for c in coef]
+
+
 def horner_f32(coef, r):
     """Evaluates 1 + r*(c1 + r*(c2 + ...)) with f32 fma rounding."""
     r64 = r.astype(np.float64)
@@ -57,6 +72,14 @@ def main():
     for j, c in enumerate(coef, start=1):
         print(f"c{j}", f32_hex(c), repr(float(c)))
     print("max error of e^r in f32 ulps (incl. Horner rounding):", err.max())
+    coef2 = fit_exp2()
+    f = np.linspace(-0.5, 0.5, 2_000_001).astype(np.float32)
+    approx = horner_f32(coef2, f).astype(np.float64)
+    exact = np.exp2(f.astype(np.float64))
+    err = np.abs(approx - exact) / np.spacing(exact.astype(np.float32)).astype(np.float64)
+    for j, c in enumerate(coef2, start=1):
+        print(f"2^f c{j}", f32_hex(c), repr(float(c)))
+    print("max error of 2^f in f32 ulps (incl. Horner rounding):", err.max())
 
 
 if __name__ == "__main__":

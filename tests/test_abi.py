@@ -65,7 +65,11 @@ def test_emit_hip_broadcast_operands():
            (M.FLOAT32, M.OPERAND_SCALAR, 0), (M.FLOAT16, M.OPERAND_FULL, 0)]
     k = M.FusedKernel(nodes, ops, M.FLOAT16, "chain")
     src = k.source
-    assert "mfh_ld8_f16(p1, (e0 % 4096LL), a1[u])" in src
+    # f16 operands stay packed in the vector loop; adds take them directly
+    assert "mfh_ldw8_f16(p1, (e0 % 4096LL), w1[u])" in src
+    assert "mfh_add_hh(w0[u][j >> 1], j & 1, w1[u][j >> 1], j & 1)" in src
+    assert "mfh_add_fh(t2, w3[u][j >> 1], j & 1)" in src
+    assert "const float x1 = mfh_ld1_f16(p1, (i % 4096LL));" in src  # element loop decodes
     assert "const float s2 = mfh_ld1_f32(p2, 0);" in src
     assert "mfh_gelu(" in src
     precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)

@@ -79,6 +79,37 @@ def test_binary_nodes_bit_exact(node):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def f16_partners():
+    """f16 codes that stress an f16 + f16 sum: zeros, denormals, the normal
+    boundary, ones, the largest finite, infinities, NaNs and random codes."""
+    fixed = [0x0000, 0x8000, 0x0001, 0x8001, 0x03ff, 0x83ff, 0x0400, 0x8400, 0x3c00, 0xbc00, 0x3c01, 0xbbff,
+             0x7bff, 0xfbff, 0x7c00, 0xfc00, 0x7e00, 0x7c01, 0xfe00, 0x1400, 0x6800]
+    rnd = np.random.default_rng(11).integers(0, 65536, 43).tolist()
+    return np.array(fixed + rnd, dtype=np.uint16)
+
+
+@pytest.mark.parametrize("other_dt", [O.FLOAT16, O.FLOAT32])
+def test_f16_add_every_code(other_dt):
+    # Add with an f16 operand runs as one mixed-precision FMA in the vector
+    # path; every f16 code against every partner must give the f32 sum.
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    partners = f16_partners()
+    a = np.tile(codes, partners.size)
+    b16 = np.repeat(partners, codes.size)
+    b = b16 if other_dt == O.FLOAT16 else O.bytes_to_f32(O.FLOAT16, b16) * np.float32(1.0009765625)
+    for nodes in (O.flatten((O.N_ADD, ("in", 0), ("in", 1))), O.flatten((O.N_ADD, ("in", 1), ("in", 0)))):
+        got = run_fused(nodes, [(O.FLOAT16, 0, 0), (other_dt, 0, 0)], [a, b], O.FLOAT32, a.size)
+        want = O.run(nodes, [O.bytes_to_f32(O.FLOAT16, a), O.decode(b, other_dt)], a.size)
+        compare_storage(got, want, O.FLOAT32, 0, f"f16 + {other_dt}")
+        nan = (want.view(np.uint32) & 0x7fffffff) > 0x7f800000
+        assert np.array_equal(got.view(np.uint32)[~nan], want.view(np.uint32)[~nan])
+    # the f16-output form of the same sum (vector path, 8 per item)
+    nodes = O.flatten((O.N_ADD, ("in", 0), ("in", 1)))
+    got = run_fused(nodes, [(O.FLOAT16, 0, 0), (other_dt, 0, 0)], [a, b], O.FLOAT16, a.size)
+    want = O.encode(O.run(nodes, [O.bytes_to_f32(O.FLOAT16, a), O.decode(b, other_dt)], a.size), O.FLOAT16)
+    compare_storage(got, want, O.FLOAT16, 0, f"f16 + {other_dt} -> f16")
+
+
 @pytest.mark.parametrize("node", [O.N_NEG, O.N_ABS, O.N_RELU, O.N_LEAKY_RELU, O.N_SQRT])
 def test_exact_unary_nodes(node):
     a = probe_f32(seed=3)

@@ -122,16 +122,17 @@ def test_graph_call_mixed_nodes_workspace_and_outputs():
     # n1 = exp(x)          f32   (shared: read by n2 and n4 -> not absorbed)
     # n2 = n1 * y          bf16  \ fused with n3
     # n3 = relu(n2)        bf16  /
-    # n4 = max(n1, k)      f16   (k: constant, a scalar operand; a singleton)
+    # n4 = max(n1, k)      f16   (k: constant, a scalar operand; a graph output,
+    #                            so not absorbed: a one-node kernel)
     # n5 = n4 - row        f32   (row: a [64] periodic input) fused with n6
     # n6 = neg(n5)         f32
-    # outputs: a = n3, b = n6, c = n1 (an intermediate also read later), d = x
+    # outputs: a = n3, b = n6, c = n1 (an intermediate also read later), d = x, e = n4
     rows, d = 300, 64
     n = rows * d
     log(f"graph mixed n={n}")
     rng = np.random.default_rng(7)
     graph = Graph(inputs=["x", "y", "row"], execution_dtype=O.FLOAT32,
-                  outputs={"a": "n3", "b": "n6", "c": "n1", "d": "x"}, nodes=[
+                  outputs={"a": "n3", "b": "n6", "c": "n1", "d": "x", "e": "n4"}, nodes=[
         GraphNode("k", "math.constant", [], attributes={"value": 0.75}),
         GraphNode("n1", "math.exp", ["x"], output_type=O.FLOAT32),
         GraphNode("n2", "math.mul", ["n1", "y"], output_type=O.BFLOAT16),
@@ -150,7 +151,7 @@ def test_graph_call_mixed_nodes_workspace_and_outputs():
     b = Bufs()
     outs = {}
     views = {}
-    for key, dt in (("a", O.BFLOAT16), ("b", O.FLOAT32), ("c", O.FLOAT32), ("d", O.FLOAT32)):
+    for key, dt in (("a", O.BFLOAT16), ("b", O.FLOAT32), ("c", O.FLOAT32), ("d", O.FLOAT32), ("e", O.FLOAT16)):
         outs[key], views[key] = b.output(n, dt)
     inputs = {"x": b.input(x, O.FLOAT32), "y": b.input(y, O.BFLOAT16), "row": b.input(row, O.FLOAT16)}
     graph.call(inputs, views, stream())
@@ -165,6 +166,7 @@ def test_graph_call_mixed_nodes_workspace_and_outputs():
     assert ports == ["n1", "y"]
     n3 = O.encode(O.run(nodes, [n1, O.decode(y, O.BFLOAT16)], n), O.BFLOAT16)
     n4 = eval_node("math.max", [n1, np.array([0.75], np.float32)], O.FLOAT16, n)
+    compare_storage(to_host(outs["e"], np.uint16), n4, O.FLOAT16, 0, "output e (one-node max with a constant)")
     nodes, ports = fused_ast(graph.nodes[4])
     assert ports == ["n4", "row"]
     n6 = O.encode(O.run(nodes, [O.decode(n4, O.FLOAT16), O.decode(row, O.FLOAT16)], n, periods=[0, d]), O.FLOAT32)
