@@ -66,6 +66,58 @@ MFH_DEV mfh_u32 mfh_e5m2_bits(mfh_u32 code)
     return sign | ((e + 112u) << 23) | (m << 21);
 }
 
+// ---- f32 -> FP8 ---------------------------------------------------------------
+
+// NewF8E4M3FromFloat32 / NewF8E5M2FromFloat32 (dtype/fp8.go:77-136,190-249):
+// saturating round-to-nearest-even with the reference's exact case split,
+// whose results are kept as they are:
+//   * NaN -> 0x7f whatever its sign;
+//   * above the largest finite value (448 / 57344) and Inf -> 0x7e/0xfe
+//     (E4M3) or +-Inf 0x7c/0xfc (E5M2);
+//   * a value whose biased exponent reaches the top field value (E4M3
+//     [256, 448], E5M2 none below 57344) saturates the same way;
+//   * below the smallest normal the mantissa with its hidden bit is shifted
+//     right by (mantissa bits + 20 - e) resp. (21 - e) for biased e <= 0 and
+//     rounded; a result that reaches the hidden-bit position becomes the
+//     smallest normal (so E4M3 [2^-7, 2^-6) all give 0x08); biased e below
+//     -3 (E4M3) / -1 (E5M2) gives signed zero.
+// MB = mantissa bits, BIAS = exponent bias, EMAX = top exponent field value,
+// SAT = saturation code, MAXF = bits of the largest finite value.
+template <int MB, int BIAS, int EMAX, int MINSUB, mfh_u32 SAT, mfh_u32 MAXF>
+MFH_DEV mfh_u32 mfh_fp8_encode(float value)
+{
+    const mfh_u32 u = mfh_bits(value);
+    const mfh_u32 sign = (u >> 24) & 0x80u;
+    const mfh_u32 a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7fu;                 // NaN
+    if (a > MAXF) return sign | SAT;                   // Inf and above the largest finite value
+    if (a == 0u) return sign;
+    mfh_i32 e = (mfh_i32)(a >> 23) - 127 + BIAS;
+    const mfh_u32 mant = a & 0x7fffffu;
+    constexpr mfh_u32 drop = 23 - MB;                  // 20 (E4M3) or 21 (E5M2)
+    if (e <= 0) {
+        if (e < MINSUB) return sign;
+        const mfh_u32 full = mant | 0x800000u;
+        const mfh_u32 shift = drop - (mfh_u32)e;       // 20 - e / 21 - e, at most 24
+        const mfh_u32 t = full >> shift;
+        const mfh_u32 rest = full & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        const mfh_u32 r = t + ((rest > half) || (rest == half && (t & 1u)) ? 1u : 0u);
+        return sign | (r >= (1u << MB) ? (1u << MB) : r);
+    }
+    if (e >= EMAX) return sign | SAT;
+    mfh_u32 m = mant >> drop;
+    const mfh_u32 rest = mant & ((1u << drop) - 1u), half = 1u << (drop - 1u);
+    m += (rest > half) || (rest == half && (m & 1u)) ? 1u : 0u;
+    if (m >= (1u << MB)) {
+        m = 0u;
+        if (++e >= EMAX) return sign | SAT;
+    }
+    return sign | ((mfh_u32)e << MB) | m;
+}
+
+MFH_DEV mfh_u32 mfh_e4m3_encode(float v) { return mfh_fp8_encode<3, 7, 15, -3, 0x7eu, 0x43e00000u>(v); }
+MFH_DEV mfh_u32 mfh_e5m2_encode(float v) { return mfh_fp8_encode<2, 15, 31, -1, 0x7cu, 0x47600000u>(v); }
+
 // ---- BF16 -------------------------------------------------------------------
 
 MFH_DEV float mfh_bf16_to_f32(mfh_u32 h) { return mfh_f32(h << 16); }

@@ -242,6 +242,107 @@ __global__ __launch_bounds__(kBlock) void k_narrow_f32_vec(const u32x4* __restri
     }
 }
 
+// ---------------------------------------------------------------------------
+// Any numeric dtype -> FP8 (BytesToFloat8E4M3 / BytesToFloat8E5M2,
+// dtype/convert/convert.go:194-232: BytesToFloat32, then the saturating RNE
+// quantiser of codec.hpp)
+// ---------------------------------------------------------------------------
+
+template <int FMT>
+MFH_DEV mfh_u32 encode_fp8(float v)
+{
+    if constexpr (FMT == kF8E4M3) return mfh_e4m3_encode(v);
+    else return mfh_e5m2_encode(v);
+}
+
+// BytesToFloat32 of element i for every source dtype, FP8 and Int4 included.
+template <int IN>
+MFH_DEV float decode_any(const void* in, mfh_i64 i)
+{
+    if constexpr (IN == kF8E4M3) return mfh_f32(mfh_e4m3_bits(static_cast<const mfh_u8*>(in)[i]));
+    else if constexpr (IN == kF8E5M2) return mfh_f32(mfh_e5m2_bits(static_cast<const mfh_u8*>(in)[i]));
+    else if constexpr (IN == kInt4)
+        return (float)mfh_int4_at(static_cast<const mfh_u8*>(in)[i >> 1], (mfh_u32)(i & 1));
+    else return decode_at<IN>(in, i);
+}
+
+// Item = 16 elements -> one 16-byte store of codes.  f32 and 16-bit sources
+// are read with 16-byte loads; other sources element by element.
+template <int IN, int FMT>
+__global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ in, mfh_u8* __restrict__ out,
+                                                       mfh_i64 n, int vec_ok)
+{
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 nitems = vec_ok ? n / 16 : 0;
+    u32x4* dst = reinterpret_cast<u32x4*>(out);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
+        float f[16];
+        if constexpr (IN == kFloat32) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(in) + v * 4;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                u32x4 w = src[q];
+#pragma unroll
+                for (int k = 0; k < 4; k++) f[4 * q + k] = mfh_f32(w[k]);
+            }
+        } else if constexpr (IN == kBFloat16 || IN == kFloat16) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(in) + v * 2;
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                u32x4 w = src[q];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    f[8 * q + 2 * k] = dec16<IN>(w[k] & 0xffffu);
+                    f[8 * q + 2 * k + 1] = dec16<IN>(w[k] >> 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; k++) f[k] = decode_any<IN>(in, v * 16 + k);
+        }
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            o[q] = encode_fp8<FMT>(f[4 * q]) | (encode_fp8<FMT>(f[4 * q + 1]) << 8) |
+                   (encode_fp8<FMT>(f[4 * q + 2]) << 16) | (encode_fp8<FMT>(f[4 * q + 3]) << 24);
+        dst[v] = o;
+    }
+    for (mfh_i64 i = nitems * 16 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        out[i] = (mfh_u8)encode_fp8<FMT>(decode_any<IN>(in, i));
+}
+
+template <int FMT>
+int launch_encode_fp8(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
+{
+    const bool wide = in_dt == kFloat32 || in_dt == kBFloat16 || in_dt == kFloat16;
+    const int vec_ok = aligned16(out) && (!wide || aligned16(in)) && n >= 16;
+    const int64_t items = vec_ok ? n / 16 : n;
+    const unsigned grid = grid_for(items, dev, Kern::kConvert);
+    switch (in_dt) {
+#define MFH_ENCODE_CASE(DT) \
+    case DT: k_encode_fp8<DT, FMT><<<grid, kBlock, 0, stream>>>(in, out, n, vec_ok); break;
+        MFH_ENCODE_CASE(kFloat64)
+        MFH_ENCODE_CASE(kFloat32)
+        MFH_ENCODE_CASE(kFloat16)
+        MFH_ENCODE_CASE(kBFloat16)
+        MFH_ENCODE_CASE(kF8E4M3)
+        MFH_ENCODE_CASE(kF8E5M2)
+        MFH_ENCODE_CASE(kInt64)
+        MFH_ENCODE_CASE(kInt32)
+        MFH_ENCODE_CASE(kInt16)
+        MFH_ENCODE_CASE(kInt8)
+        MFH_ENCODE_CASE(kInt4)
+        MFH_ENCODE_CASE(kUint64)
+        MFH_ENCODE_CASE(kUint32)
+        MFH_ENCODE_CASE(kUint16)
+        MFH_ENCODE_CASE(kUint8)
+#undef MFH_ENCODE_CASE
+    default:
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+    }
+    return launch_status("k_encode_fp8");
+}
+
 bool is_out_dtype(int dt) { return dt == kFloat32 || dt == kBFloat16 || dt == kFloat16; }
 
 bool aligned(const void* p, unsigned bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
@@ -404,11 +505,17 @@ int mfh_convert(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype, 
     const Device* dev;
     MFH_TRY(bind_device(&dev));
     if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: negative count %lld", (long long)count);
-    if (!is_out_dtype(out_dtype))
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: output dtype %s is not f32/bf16/f16", dtype_name(out_dtype));
+    const bool to_fp8 = out_dtype == kF8E4M3 || out_dtype == kF8E5M2;
+    if (!is_out_dtype(out_dtype) && !to_fp8)
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: output dtype %s is not f32/bf16/f16/fp8",
+                    dtype_name(out_dtype));
     if (count == 0) return MFH_OK;
     if (!out || !in) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: NULL buffer");
     hipStream_t s = (hipStream_t)stream;
+    if (to_fp8)
+        return out_dtype == kF8E4M3
+                   ? launch_encode_fp8<kF8E4M3>(dev, static_cast<mfh_u8*>(out), in, in_dtype, count, s)
+                   : launch_encode_fp8<kF8E5M2>(dev, static_cast<mfh_u8*>(out), in, in_dtype, count, s);
     if (in_dtype == kF8E4M3 || in_dtype == kF8E5M2)
         return by_out<Fp8Launch>(out_dtype, dev, out, in, (int)in_dtype, count, 1.0f, s);
     if (in_dtype == kInt4)

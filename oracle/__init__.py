@@ -71,6 +71,8 @@ def _declare(L):
     L.orc_f32_to_e4m3.argtypes = [f32]
     L.orc_f32_to_e5m2.restype = c.c_uint8
     L.orc_f32_to_e5m2.argtypes = [f32]
+    L.orc_f32_to_fp8_buf.restype = None
+    L.orc_f32_to_fp8_buf.argtypes = [c.c_void_p, c.c_int64, c.c_int, c.c_void_p]
     L.orc_f32_to_bf16.restype = c.c_uint16
     L.orc_f32_to_bf16.argtypes = [f32]
     L.orc_bf16_to_f32.restype = f32
@@ -127,6 +129,14 @@ def f32_to_e4m3(v: float) -> int:
 
 def f32_to_e5m2(v: float) -> int:
     return lib().orc_f32_to_e5m2(v)
+
+
+def f32_to_fp8(values: np.ndarray, fmt: int) -> np.ndarray:
+    """BytesToFloat8E4M3 / BytesToFloat8E5M2 of f32 values (fmt F8E4M3/F8E5M2)."""
+    values = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    out = np.empty(values.size, dtype=np.uint8)
+    lib().orc_f32_to_fp8_buf(_ptr(values), values.size, fmt, _ptr(out))
+    return out
 
 
 def f32_bits_to_bf16(bits: int) -> int:

@@ -149,6 +149,11 @@ uint8_t orc_f32_to_e5m2(float value)
     return (uint8_t)(sign | (uint8_t)((uint8_t)exponent << 2) | (uint8_t)mantissa8);
 }
 
+void orc_f32_to_fp8_buf(const float* in, int64_t n, int fmt, uint8_t* out)
+{
+    for (int64_t i = 0; i < n; i++) out[i] = fmt == 5 ? orc_f32_to_e4m3(in[i]) : orc_f32_to_e5m2(in[i]);
+}
+
 /* ------------------------------------------------------------------------ */
 /* BF16.  dtype/bfloat16.go                                                  */
 /* ------------------------------------------------------------------------ */

@@ -36,6 +36,9 @@ float    orc_e4m3_to_f32(uint8_t code);
 float    orc_e5m2_to_f32(uint8_t code);
 uint8_t  orc_f32_to_e4m3(float value);
 uint8_t  orc_f32_to_e5m2(float value);
+/* BytesToFloat8E4M3 / BytesToFloat8E5M2 after BytesToFloat32
+ * (dtype/convert/convert.go:194-232): fmt 5 E4M3, 6 E5M2. */
+void     orc_f32_to_fp8_buf(const float* in, int64_t n, int fmt, uint8_t* out);
 uint16_t orc_f32_to_bf16(float value);
 float    orc_bf16_to_f32(uint16_t bits);
 float    orc_f16_to_f32(uint16_t bits);

@@ -98,6 +98,45 @@ def test_fp8_encode_round_trips_normal_codes():
     assert O.f32_to_e4m3(2.0 ** -7) == 0x08
 
 
+def nearest_even_code(x, table, mbits):
+    """Brute force: the code of the representable value nearest to x, ties to
+    the even mantissa; `table` maps positive finite codes to their values."""
+    codes = np.array(sorted(table))
+    vals = np.array([table[c] for c in codes])
+    d = np.abs(vals - x)
+    best = np.flatnonzero(d == d.min())
+    if best.size == 1:
+        return int(codes[best[0]])
+    even = [int(codes[b]) for b in best if (codes[b] & ((1 << mbits) - 1)) % 2 == 0]
+    return even[0]
+
+
+@pytest.mark.parametrize("fmt, lo, hi, mbits", [(O.F8E4M3, 2.0 ** -6, 248.0, 3), (O.F8E5M2, 2.0 ** -14, 57344.0, 2)])
+def test_fp8_encode_is_nearest_even_in_the_normal_range(fmt, lo, hi, mbits):
+    # Independent of the restated algorithm: inside the normal range the
+    # encoder must pick the nearest representable value, ties to even.  For
+    # E4M3 the range stops below 248, the midpoint into the top binade, which
+    # the reference saturates to 0x7e (448) instead of rounding to 256.
+    # Inputs: random values, every midpoint between neighbours and one f32 ulp
+    # either side of it.
+    dec = O.e4m3_to_f32 if fmt == O.F8E4M3 else O.e5m2_to_f32
+    table = {c: dec(c) for c in range(0x80) if math.isfinite(dec(c)) and dec(c) > 0}
+    table = {c: v for c, v in table.items() if lo <= v <= hi}
+    vals = sorted(table.values())
+    rng = np.random.default_rng(8)
+    xs = list(np.exp(rng.uniform(math.log(lo), math.log(hi), 3000)).astype(np.float32))
+    for a, b in zip(vals, vals[1:]):
+        m = np.float32((a + b) / 2)
+        xs += [m, np.nextafter(m, np.float32(0)), np.nextafter(m, np.float32(np.inf))]
+    xs = np.array([x for x in xs if lo <= x < hi], dtype=np.float32)
+    assert xs.size > 3000
+    got = O.f32_to_fp8(xs, fmt)
+    for x, g in zip(xs, got):
+        want = nearest_even_code(float(x), table, mbits)
+        assert g == want, (float(x), hex(g), hex(want))
+        assert O.f32_to_fp8(-np.array([x], np.float32), fmt)[0] == want | 0x80
+
+
 # --------------------------------------------------------------------------
 # Int4: closed form n - 16*(n >= 8), both nibbles, all bytes.
 # --------------------------------------------------------------------------
