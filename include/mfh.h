@@ -31,12 +31,12 @@ extern "C" {
 
 #define MFH_OK 0
 #define MFH_ERR_INVALID_ARGUMENT (-1)
-#define MFH_ERR_DTYPE_UNSUPPORTED (-2) /* tensor.ErrDTypeUnsupported, tensor/errors.go:16-19 */
-#define MFH_ERR_SHAPE_MISMATCH (-3)    /* tensor.ErrShapeMismatch, tensor/errors.go:26-29 */
+#define MFH_ERR_DTYPE_UNSUPPORTED (-2) /* tensor.ErrDTypeUnsupported, tensor/errors.go:18 */
+#define MFH_ERR_SHAPE_MISMATCH (-3)    /* tensor.ErrShapeMismatch, tensor/errors.go:28 */
 #define MFH_ERR_DEVICE (-4)            /* a HIP runtime call failed */
 #define MFH_ERR_COMPILE (-5)           /* hiprtc rejected a generated kernel */
 #define MFH_ERR_NOT_INITIALIZED (-6)   /* mfh_init was not called */
-#define MFH_ERR_CLOSED (-7)            /* tensor.ErrBackendClosed, tensor/errors.go:50-52 */
+#define MFH_ERR_CLOSED (-7)            /* tensor.ErrBackendClosed, tensor/errors.go:46 */
 
 /* ---- runtime: device, memory, streams ---------------------------------- */
 

@@ -161,3 +161,11 @@ def test_generated_activation_chain_uses_no_packed_fp32(tmp_path):
     k = M.FusedKernel(nodes, [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "act")
     asm = _device_asm(k.source, tmp_path)
     assert not re.search(r"v_pk_(fma|mul|add)_f32", asm)
+
+
+def test_backend_open_without_a_device_fails_loudly():
+    from manifesto_amd.backend import Backend
+    if M.lib().mfh_init(0) == 0:
+        pytest.skip("a GPU is present; the backend is covered by the GPU tests")
+    with pytest.raises(M.MFHError):
+        Backend(0)

@@ -1,0 +1,201 @@
+"""GPU tests of the HIP tensor backend (include/mfh_backend.h): the
+tensor.Backend / tensor.Tensor contract (tensor/backend.go:18-68,
+tensor/tensor.go:53-130) over device memory, the dequantising uploads
+checked bit for bit against the oracle (BytesToBFloat16 and the scaled
+dequant kernels' oracle), views, lifecycle errors, and axpyOntoResident
+(runtime/axpy.go:44-93) with the reference's cases (runtime/axpy_test.go:14-68).
+"""
+import numpy as np
+import pytest
+
+import manifesto_amd as M
+from manifesto_amd.backend import (Backend, ERR_LAYOUT_UNSUPPORTED, ERR_SHAPE_INVALID, ERR_TENSOR_CLOSED,
+                                   STATE_CLOSED, STATE_PENDING, STATE_READY)
+import oracle as O
+
+from gpu_util import log
+
+pytestmark = pytest.mark.gpu
+
+CHUNK = 16 << 20  # the backend's staging chunk; sizes below cross several
+
+
+@pytest.fixture(scope="module")
+def backend():
+    b = Backend(0)
+    yield b
+    b.release()
+
+
+def code(err):
+    return err.value.code
+
+
+def test_backend_contract(backend):
+    assert backend.location() == "hip"
+    assert backend.supported_dtypes() == [O.FLOAT32, O.FLOAT16, O.BFLOAT16, O.F8E4M3, O.F8E5M2, O.INT4]
+    assert backend.supported_layouts() == [0]
+    caps = backend.capabilities()
+    assert caps.max_bytes > (100 << 30) and caps.supports_async == 1 and caps.supports_sparse == 0
+    assert caps.native_alignment == 256 and caps.numa_nodes == 1
+    with pytest.raises(M.MFHError) as e:
+        backend.upload_sparse()
+    assert code(e) == ERR_LAYOUT_UNSUPPORTED
+
+
+@pytest.mark.parametrize("dims", [[0], [], [3], [2, 3, 4], [4096, 4097]])
+@pytest.mark.parametrize("dt, np_dt", [(O.FLOAT32, np.float32), (O.FLOAT16, np.uint16), (O.BFLOAT16, np.uint16)])
+def test_upload_download_round_trip(backend, dims, dt, np_dt):
+    n = int(np.prod(dims)) if dims else 1
+    rng = np.random.default_rng(n)
+    data = rng.integers(0, 2 ** 31, n, dtype=np.uint32).astype(np_dt) if np_dt != np.float32 else \
+        rng.normal(0, 1, n).astype(np.float32)
+    t = backend.upload(dims, dt, data.tobytes())
+    assert t.shape() == dims and t.len() == n and t.dtype() == dt and t.location() == "hip"
+    assert t.bytes() == data.nbytes and t.state() == STATE_READY
+    got_dt, raw = backend.download(t)
+    assert got_dt == dt and raw == data.tobytes()
+    assert t.raw_bytes() == (dt, data.tobytes())
+    t.release()
+
+
+@pytest.mark.parametrize("fmt", [O.F8E4M3, O.F8E5M2])
+def test_upload_fp8_is_stored_as_bfloat16(backend, fmt):
+    # BytesToBFloat16 on the device (dtype/convert/convert.go:155-171)
+    codes = np.tile(np.arange(256, dtype=np.uint8), 16)
+    t = backend.upload([16, 256], fmt, codes)
+    dt, raw = backend.download(t)
+    assert dt == O.BFLOAT16 and t.dtype() == O.BFLOAT16 and t.shape() == [16, 256]
+    assert np.frombuffer(raw, np.uint16).tolist() == O.bytes_to_bf16(fmt, codes).tolist()
+    # large enough to cross staging chunks
+    big = np.random.default_rng(fmt).integers(0, 256, 3 * CHUNK + 12345, dtype=np.uint8)
+    t = backend.upload([big.size], fmt, big)
+    dt, raw = backend.download(t)
+    np.testing.assert_array_equal(np.frombuffer(raw, np.uint16), O.bytes_to_bf16(fmt, big))
+
+
+def test_upload_int4_is_stored_as_bfloat16(backend):
+    packed = np.arange(256, dtype=np.uint8)
+    t = backend.upload([511], O.INT4, packed)  # odd count: the last byte's low nibble only
+    dt, raw = backend.download(t)
+    assert dt == O.BFLOAT16 and t.len() == 511
+    np.testing.assert_array_equal(np.frombuffer(raw, np.uint16), O.bytes_to_bf16(O.INT4, packed)[:511])
+    big = np.random.default_rng(5).integers(0, 256, 2 * CHUNK + 999, dtype=np.uint8)
+    t = backend.upload([big.size * 2], O.INT4, big)
+    dt, raw = backend.download(t)
+    np.testing.assert_array_equal(np.frombuffer(raw, np.uint16), O.bytes_to_bf16(O.INT4, big))
+
+
+@pytest.mark.parametrize("out_dt", [O.BFLOAT16, O.FLOAT16, O.FLOAT32])
+def test_scaled_fp8_upload(backend, out_dt):
+    codes = np.random.default_rng(2).integers(0, 256, 2 * CHUNK + 77, dtype=np.uint8)
+    t = backend.upload_fp8([codes.size], O.F8E4M3, codes, 0.0125, out_dt)
+    dt, raw = backend.download(t)
+    want = O.dequant_fp8(codes, O.F8E4M3, 0.0125, out_dt)
+    assert dt == out_dt
+    np.testing.assert_array_equal(np.frombuffer(raw, want.dtype).view(np.uint8), want.view(np.uint8))
+
+
+@pytest.mark.parametrize("group, scale_dt", [(128, O.FLOAT16), (64, O.BFLOAT16), (4096, O.FLOAT32)])
+def test_scaled_int4_upload(backend, group, scale_dt):
+    rows, cols = 2048, 8192 * 2  # 33.5M nibbles: more than one staging chunk
+    n = rows * cols
+    rng = np.random.default_rng(group)
+    packed = rng.integers(0, 256, n // 2, dtype=np.uint8)
+    s32 = rng.uniform(0.005, 0.02, n // group).astype(np.float32)
+    scales = O.encode(s32, scale_dt) if scale_dt != O.FLOAT32 else s32
+    t = backend.upload_int4([rows, cols], packed, scales, scale_dt, group, O.BFLOAT16)
+    dt, raw = backend.download(t)
+    want = O.dequant_int4(packed, n, scales, scale_dt, group, O.BFLOAT16)
+    assert dt == O.BFLOAT16
+    np.testing.assert_array_equal(np.frombuffer(raw, np.uint16), want)
+    log(f"int4 group {group}: {n} nibbles ok")
+
+
+def test_upload_errors(backend):
+    with pytest.raises(M.MFHError) as e:
+        backend.upload([3], O.FLOAT32, b"\0" * 11)
+    assert code(e) == -3
+    with pytest.raises(M.MFHError) as e:
+        backend.upload([2, -1], O.FLOAT32, b"")
+    assert code(e) == ERR_SHAPE_INVALID
+    with pytest.raises(M.MFHError) as e:
+        backend.upload([2], O.FLOAT64, b"\0" * 16)
+    assert code(e) == -2
+    with pytest.raises(M.MFHError) as e:
+        backend.upload([3], O.INT4, b"\0" * 1)  # 3 nibbles need 2 bytes
+    assert code(e) == -3
+
+
+def test_async_upload_and_sync(backend):
+    data = np.random.default_rng(9).normal(0, 1, 5 * CHUNK // 4 + 3).astype(np.float32)
+    src = data.copy()
+    t = backend.upload_async([data.size], O.FLOAT32, src)
+    src[:] = 0  # the source may be reused as soon as the call returns
+    assert t.state() in (STATE_PENDING, STATE_READY)
+    t.sync()
+    assert t.state() == STATE_READY
+    assert backend.download(t)[1] == data.tobytes()
+
+
+def test_views_and_lifecycle(backend):
+    data = np.arange(24, dtype=np.float32)
+    t = backend.upload([2, 3, 4], O.FLOAT32, data)
+    s = t.slice(5, 10)
+    assert s.shape() == [10] and backend.download(s)[1] == data[5:15].tobytes()
+    assert s.dispatch_pointer() == t.dispatch_pointer() + 20
+    r = t.reshape([6, 4])
+    assert r.shape() == [6, 4] and backend.download(r)[1] == data.tobytes()
+    with pytest.raises(M.MFHError) as e:
+        t.slice(20, 5)
+    assert code(e) == ERR_SHAPE_INVALID
+    with pytest.raises(M.MFHError) as e:
+        t.reshape([5, 5])
+    assert code(e) == -3
+    s.close()
+    s.close()  # idempotent
+    assert s.state() == STATE_CLOSED and backend.download(t)[1] == data.tobytes()  # a view's close frees nothing
+    t.close()
+    assert t.state() == STATE_CLOSED and r.state() == STATE_CLOSED and t.dispatch_pointer() == 0
+    with pytest.raises(M.MFHError) as e:
+        backend.download(r)  # closing the parent invalidates its views
+    assert code(e) == ERR_TENSOR_CLOSED
+
+
+def test_axpy_onto_resident(backend):
+    # runtime/axpy_test.go:26-52: bf16 y = [1,2,3], x = [4,5,6], alpha 0.5 -> [3,4.5,6]
+    y = backend.upload([3], O.BFLOAT16, O.f32_to_bf16(np.array([1, 2, 3], np.float32)))
+    x = backend.upload([3], O.BFLOAT16, O.f32_to_bf16(np.array([4, 5, 6], np.float32)))
+    assert backend.axpy_onto_resident(y, x, 0.5) is y
+    dt, raw = backend.download(y)
+    assert dt == O.BFLOAT16 and O.bytes_to_f32(O.BFLOAT16, np.frombuffer(raw, np.uint8)).tolist() == [3, 4.5, 6]
+    # f32 at size, against the oracle's unfused axpy
+    rng = np.random.default_rng(1)
+    yv, xv = rng.uniform(-1, 1, 1 << 22).astype(np.float32), rng.uniform(-1, 1, 1 << 22).astype(np.float32)
+    y = backend.upload([yv.size], O.FLOAT32, yv)
+    x = backend.upload([xv.size], O.FLOAT32, xv)
+    backend.axpy_onto_resident(y, x, -0.25)
+    y.sync()
+    np.testing.assert_array_equal(np.frombuffer(backend.download(y)[1], np.float32), O.axpy_f32(yv, xv, -0.25))
+    # the reference's checks and messages (runtime/axpy.go:72-82)
+    z = backend.upload([3], O.FLOAT32, np.zeros(3, np.float32))
+    with pytest.raises(M.MFHError, match="math.axpy: y dtype F32 does not match x dtype BF16"):
+        backend.axpy_onto_resident(z, backend.upload([3], O.BFLOAT16, np.zeros(3, np.uint16)), 1.0)
+    with pytest.raises(M.MFHError, match="math.axpy: y length 3 does not match x length 4"):
+        backend.axpy_onto_resident(z, backend.upload([4], O.FLOAT32, np.zeros(4, np.float32)), 1.0)
+
+
+def test_backend_close_invalidates_tensors():
+    b = Backend(0)
+    t = b.upload([4], O.FLOAT32, np.ones(4, np.float32))
+    b.close()
+    b.close()  # idempotent
+    assert t.state() == STATE_CLOSED
+    with pytest.raises(M.MFHError) as e:
+        t.sync()
+    assert code(e) == ERR_TENSOR_CLOSED
+    with pytest.raises(M.MFHError) as e:
+        b.upload([1], O.FLOAT32, np.ones(1, np.float32))
+    assert code(e) == -7
+    t.release()
+    b.release()
