@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "../../include/mfh_backend.h"
+#include "backend_internal.hpp"
 #include "common.hpp"
 
 namespace mfh {
@@ -188,19 +189,19 @@ int ensure_staging(BackendState& s)
     return MFH_OK;
 }
 
-// How an upload turns source bytes into stored elements.
-struct Plan {
-    int src = kInvalid;        // source dtype
-    int out = kInvalid;        // stored dtype
-    float scale = 1.0f;        // FP8
-    const void* scales = nullptr;  // Int4: device group scales
-    int scale_dt = kInvalid;
-    int64_t group = 0;
+struct MemorySource : Source {
+    const uint8_t* base;
+    explicit MemorySource(const void* p) : base(static_cast<const uint8_t*>(p)) {}
+    int read(void* dst, size_t offset, size_t len) override
+    {
+        std::memcpy(dst, base + offset, len);
+        return MFH_OK;
+    }
 };
 
 // Queues the upload of `n_src` source bytes holding `elements` elements into
 // `dst` (already allocated for the stored dtype) on the backend stream.
-int stream_in(BackendState& s, const Plan& p, const uint8_t* src, size_t n_src, int64_t elements, Storage& dst)
+int stream_in(BackendState& s, const Plan& p, Source& src, size_t n_src, int64_t elements, Storage& dst)
 {
     if (n_src == 0) return MFH_OK;
     MFH_TRY(ensure_staging(s));
@@ -219,7 +220,7 @@ int stream_in(BackendState& s, const Plan& p, const uint8_t* src, size_t n_src, 
         const int slot = c % kRing;
         const size_t len = std::min(chunk, n_src - done);
         MFH_TRY(check_hip(hipEventSynchronize(s.slot_free[slot]), "hipEventSynchronize"));
-        std::memcpy(s.pinned[slot], src + done, len);
+        MFH_TRY(src.read(s.pinned[slot], done, len));
         if (!convert) {
             MFH_TRY(check_hip(hipMemcpyAsync(static_cast<uint8_t*>(dst.ptr) + done, s.pinned[slot], len,
                                              hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(H2D)"));
@@ -253,8 +254,17 @@ int stream_in(BackendState& s, const Plan& p, const uint8_t* src, size_t n_src, 
     return MFH_OK;
 }
 
-int upload(mfh_backend* b, const int64_t* shape, int32_t rank, const Plan& plan, const void* bytes, size_t n_bytes,
-           bool wait, mfh_tensor** out)
+int wait_storage(Storage& st)
+{
+    if (st.pending && st.done) MFH_TRY(check_hip(hipEventSynchronize(st.done), "hipEventSynchronize"));
+    st.pending = false;
+    return MFH_OK;
+}
+
+}  // namespace
+
+int upload_from(mfh_backend* b, const int64_t* shape, int32_t rank, const Plan& plan, Source& source,
+                size_t n_bytes, bool wait, mfh_tensor** out)
 {
     if (!out) return fail(MFH_ERR_INVALID_ARGUMENT, "upload: tensor out-pointer is NULL");
     *out = nullptr;
@@ -269,11 +279,10 @@ int upload(mfh_backend* b, const int64_t* shape, int32_t rank, const Plan& plan,
     if ((int64_t)n_bytes != expected)
         return fail(MFH_ERR_SHAPE_MISMATCH, "tensor: shape mismatch: %zu bytes for %lld elements of %s (want %lld)",
                     n_bytes, (long long)t->elements, wire_name(plan.src), (long long)expected);
-    if (n_bytes > 0 && !bytes) return fail(MFH_ERR_INVALID_ARGUMENT, "upload: bytes are NULL");
     auto st = std::make_shared<Storage>();
     st->bytes = (size_t)t->elements * dtype_size(plan.out);
     if (st->bytes) MFH_TRY(check_hip(hipMalloc(&st->ptr, st->bytes), "hipMalloc"));
-    int rc = stream_in(s, plan, static_cast<const uint8_t*>(bytes), n_bytes, t->elements, *st);
+    int rc = stream_in(s, plan, source, n_bytes, t->elements, *st);
     if (rc == MFH_OK) rc = check_hip(hipEventCreateWithFlags(&st->done, hipEventDisableTiming), "hipEventCreate");
     if (rc == MFH_OK) rc = check_hip(hipEventRecord(st->done, s.stream), "hipEventRecord");
     if (rc == MFH_OK && wait) rc = check_hip(hipEventSynchronize(st->done), "hipEventSynchronize");
@@ -292,11 +301,17 @@ int upload(mfh_backend* b, const int64_t* shape, int32_t rank, const Plan& plan,
     return MFH_OK;
 }
 
-int wait_storage(Storage& st)
+namespace {
+
+int upload(mfh_backend* b, const int64_t* shape, int32_t rank, const Plan& plan, const void* bytes, size_t n_bytes,
+           bool wait, mfh_tensor** out)
 {
-    if (st.pending && st.done) MFH_TRY(check_hip(hipEventSynchronize(st.done), "hipEventSynchronize"));
-    st.pending = false;
-    return MFH_OK;
+    if (n_bytes > 0 && !bytes) {
+        if (out) *out = nullptr;
+        return fail(MFH_ERR_INVALID_ARGUMENT, "upload: bytes are NULL");
+    }
+    MemorySource src(bytes);
+    return upload_from(b, shape, rank, plan, src, n_bytes, wait, out);
 }
 
 }  // namespace

@@ -1,0 +1,39 @@
+// backend_internal.hpp — the upload pipeline of backend.cpp as used by the
+// other sources of the library (the SafeTensors loader).
+#ifndef MFH_BACKEND_INTERNAL_HPP
+#define MFH_BACKEND_INTERNAL_HPP
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/mfh_backend.h"
+#include "common.hpp"
+
+namespace mfh {
+
+// How an upload turns source bytes into stored elements.
+struct Plan {
+    int src = kInvalid;            // source dtype
+    int out = kInvalid;            // stored dtype
+    float scale = 1.0f;            // FP8
+    const void* scales = nullptr;  // Int4: device group scales
+    int scale_dt = kInvalid;
+    int64_t group = 0;
+};
+
+// Where upload bytes come from: read(dst, offset, len) fills `len` bytes of
+// the pinned staging chunk `dst` with source bytes [offset, offset + len).
+struct Source {
+    virtual ~Source() = default;
+    virtual int read(void* dst, size_t offset, size_t len) = 0;
+};
+
+// Checks the shape against `n_bytes` of plan.src, allocates the stored
+// tensor and streams the source through the backend's staging ring (waiting
+// for completion when `wait`).
+int upload_from(mfh_backend* backend, const int64_t* shape, int32_t rank, const Plan& plan, Source& source,
+                size_t n_bytes, bool wait, mfh_tensor** out);
+
+}  // namespace mfh
+
+#endif  // MFH_BACKEND_INTERNAL_HPP
