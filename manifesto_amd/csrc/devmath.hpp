@@ -39,7 +39,9 @@
 #define mfh_rintf(x) std::nearbyint((float)(x))
 #define mfh_rint(x) std::nearbyint((double)(x))
 #define mfh_ldexpf(x, k) std::ldexp((float)(x), (int)(k))
+#define mfh_ldexp(x, k) std::ldexp((double)(x), (int)(k))
 #define mfh_rcpf(x) (1.0f / (float)(x))
+#define mfh_rcp(x) (1.0 / (double)(x))
 #define mfh_tanh_f64(x) std::tanh((double)(x))
 #define mfh_exp_f64(x) std::exp((double)(x))
 #define mfh_log_f64(x) std::log((double)(x))
@@ -59,7 +61,9 @@ extern "C" __device__ double __ocml_log_f64(double);
 #define mfh_rintf(x) __builtin_rintf(x)
 #define mfh_rint(x) __builtin_rint(x)
 #define mfh_ldexpf(x, k) __builtin_amdgcn_ldexpf((x), (k))
+#define mfh_ldexp(x, k) __builtin_amdgcn_ldexp((x), (k))
 #define mfh_rcpf(x) __builtin_amdgcn_rcpf(x)
+#define mfh_rcp(x) __builtin_amdgcn_rcp(x)
 #define mfh_tanh_f64(x) __ocml_tanh_f64(x)
 #define mfh_exp_f64(x) __ocml_exp_f64(x)
 #define mfh_log_f64(x) __ocml_log_f64(x)
@@ -103,6 +107,21 @@ MFH_MATH float mfh_exp2_poly(float f)
     q = mfh_fmaf(q, f, 0.24022647738456726f);    // 0x3e75fdee
     q = mfh_fmaf(q, f, 0.6931471824645996f);     // 0x3f317218
     return mfh_fmaf(q, f, 1.0f);
+}
+
+// 2^f for |f| <= 1/2 in f64: degree 8, relative error below 2^-39.9 with
+// Horner rounding (the f64 fit of gen_exp_poly.py).
+MFH_MATH double mfh_exp2_poly_d(double f)
+{
+    double q = 0x1.6208e89aaa738p-20;
+    q = mfh_fma(q, f, 0x1.00daa1a549b84p-16);
+    q = mfh_fma(q, f, 0x1.430a636ccd334p-13);
+    q = mfh_fma(q, f, 0x1.5d87488d46abap-10);
+    q = mfh_fma(q, f, 0x1.3b2ab618fb075p-7);
+    q = mfh_fma(q, f, 0x1.c6b08dd4189f3p-5);
+    q = mfh_fma(q, f, 0x1.ebfbdff8ccfeap-3);
+    q = mfh_fma(q, f, 0x1.62e42fef863fep-1);
+    return mfh_fma(q, f, 1.0);
 }
 
 // e^a = p * 2^k, for a in [-200, 200].
@@ -171,15 +190,21 @@ MFH_MATH float mfh_gelu_ref(float v)
     return (float)(0.5 * d * (1.0 + th));
 }
 
-// sigmoid(v) = 1 / (1 + e^-v); below -87 (e^-v past the f32 range) and for
-// NaN the f64 form.  +Inf gives 1 by itself.
+// sigmoid(v) = 1 / (1 + 2^t), t = -v log2(e), all in f64: for v < 0 the
+// result is ~e^v and inherits the full relative error of E, which an f32
+// exponential (0.9 ulp) plus the final rounding would push past the 1-ulp
+// Sigmoid budget on a few inputs.  In f64 (2^f to 2^-39.9, reciprocal plus one
+// Newton step) the single rounding to f32 is the only error that matters.
+// Below -708 (and -Inf, NaN) the reference's form; +Inf gives 1 by itself.
 MFH_MATH float mfh_sigmoid(float v)
 {
-    int k;
-    float p = mfh_exp_core(-mfh_med3f(v, -87.0f, 104.0f), &k);
-    float s = mfh_div_one_plus(1.0f, p, k);
+    const double t = (double)mfh_med3f(v, -708.0f, 800.0f) * -MFH_LOG2E_D;
+    const double kd = mfh_rint(t);
+    const double den = 1.0 + mfh_ldexp(mfh_exp2_poly_d(t - kd), (int)kd);
+    const double r = mfh_rcp(den);
+    float s = (float)mfh_fma(r, mfh_fma(-den, r, 1.0), r);
     MFH_KEEP(s);
-    if (!(v >= -87.0f)) s = mfh_sigmoid_ref(v);
+    if (!(v >= -708.0f)) s = mfh_sigmoid_ref(v);
     return s;
 }
 

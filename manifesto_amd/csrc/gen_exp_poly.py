@@ -8,7 +8,9 @@ weighted least squares on Chebyshev nodes for relative error and rounded to
 f32.
 
 2^f on |f| <= 1/2 (the fraction left when the argument is already in log2
-units and reduced in f64) is fitted the same way.
+units and reduced in f64) is fitted the same way, once with f32 coefficients
+(degree 6) and once with f64 coefficients (degree 8, fitted in 50-digit
+arithmetic with mpmath).
 
 Run: python3 gen_exp_poly.py
 """
@@ -50,6 +52,34 @@ def fit_exp2(degree=6, half_width=0.5, nodes=4000):
     return [F32(c) for c in coef]
 
 
+def fit_exp2_f64(degree=8, half_width=0.5, nodes=600):
+    """Weighted least squares for 2^f - 1 = f q(f) in 50-digit arithmetic;
+    returns the coefficients rounded to f64 and the max relative error of
+    the f64 Horner evaluation on a grid."""
+    import mpmath as mp
+    mp.mp.dps = 50
+    xs = [half_width * mp.cos(mp.pi * (k + mp.mpf(0.5)) / nodes) for k in range(nodes)]
+    A = mp.matrix(nodes, degree)
+    b = mp.matrix(nodes, 1)
+    for i, x in enumerate(xs):
+        w = 1 / mp.power(2, x)
+        for j in range(degree):
+            A[i, j] = w * x ** (j + 1)
+        b[i] = w * (mp.power(2, x) - 1)
+    Q, R = mp.qr(A)
+    c = mp.lu_solve(R[:degree, :degree], (Q.T * b)[:degree, 0])
+    coef = [float(c[j]) for j in range(degree)]
+    worst = 0
+    for i in range(4001):
+        f = -half_width + 2 * half_width * i / 4000
+        acc = coef[-1]
+        for cj in reversed(coef[:-1]):
+            acc = acc * f + cj
+        acc = acc * f + 1.0
+        worst = max(worst, abs((mp.mpf(acc) - mp.power(2, mp.mpf(f))) / mp.power(2, mp.mpf(f))))
+    return coef, float(mp.log(worst, 2))
+
+
 def horner_f32(coef, r):
     """Evaluates 1 + r*(c1 + r*(c2 + ...)) with f32 fma rounding."""
     r64 = r.astype(np.float64)
@@ -80,6 +110,14 @@ def main():
     for j, c in enumerate(coef2, start=1):
         print(f"2^f c{j}", f32_hex(c), repr(float(c)))
     print("max error of 2^f in f32 ulps (incl. Horner rounding):", err.max())
+    try:
+        coef64, log2err = fit_exp2_f64()
+    except ImportError:
+        print("mpmath is not installed: f64 coefficients skipped")
+        return
+    for j, c in enumerate(coef64, start=1):
+        print(f"2^f f64 c{j}", float.hex(c))
+    print("log2 of the max relative error of 2^f in f64:", log2err)
 
 
 if __name__ == "__main__":
