@@ -28,40 +28,6 @@ namespace {
 constexpr size_t kChunk = 16u << 20;  // bytes of source data per staging chunk
 constexpr int kRing = 2;
 
-// DType.String (dtype/dtype.go:190-231): the names the reference prints in
-// its error messages.
-const char* wire_name(int dt)
-{
-    switch (dt) {
-    case kFloat64: return "F64";
-    case kFloat32: return "F32";
-    case kFloat16: return "F16";
-    case kBFloat16: return "BF16";
-    case kF8E4M3: return "F8E4M3";
-    case kF8E5M2: return "F8E5M2";
-    case kInt64: return "I64";
-    case kInt32: return "I32";
-    case kInt16: return "I16";
-    case kInt8: return "I8";
-    case kInt4: return "I4";
-    case kUint64: return "U64";
-    case kUint32: return "U32";
-    case kUint16: return "U16";
-    case kUint8: return "U8";
-    case kBool: return "BOOL";
-    default: return "INVALID";
-    }
-}
-
-// DType.BytesFor (dtype/dtype.go:81-101); -1 for dtypes without a size.
-int64_t bytes_for(int dt, int64_t elements)
-{
-    if (dt == kInt4) return (elements + 1) / 2;
-    if (dt == kBool) return (elements + 7) / 8;
-    int size = dtype_size(dt);
-    return size > 0 ? elements * size : -1;
-}
-
 bool stored_as_is(int dt) { return dt == kFloat32 || dt == kFloat16 || dt == kBFloat16; }
 bool dequantised(int dt) { return dt == kF8E4M3 || dt == kF8E5M2 || dt == kInt4; }
 
@@ -278,7 +244,7 @@ int upload_from(mfh_backend* b, const int64_t* shape, int32_t rank, const Plan& 
     if (expected < 0) return fail(MFH_ERR_DTYPE_UNSUPPORTED, "tensor: dtype not supported by backend");
     if ((int64_t)n_bytes != expected)
         return fail(MFH_ERR_SHAPE_MISMATCH, "tensor: shape mismatch: %zu bytes for %lld elements of %s (want %lld)",
-                    n_bytes, (long long)t->elements, wire_name(plan.src), (long long)expected);
+                    n_bytes, (long long)t->elements, dtype_string(plan.src), (long long)expected);
     auto st = std::make_shared<Storage>();
     st->bytes = (size_t)t->elements * dtype_size(plan.out);
     if (st->bytes) MFH_TRY(check_hip(hipMalloc(&st->ptr, st->bytes), "hipMalloc"));
@@ -367,7 +333,7 @@ int mfh_backend_upload(mfh_backend* backend, const int64_t* shape, int32_t rank,
 {
     if (!stored_as_is(source_dtype) && !dequantised(source_dtype)) {
         if (tensor) *tensor = nullptr;
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "tensor: dtype not supported by backend (%s)", wire_name(source_dtype));
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "tensor: dtype not supported by backend (%s)", dtype_string(source_dtype));
     }
     Plan p;
     p.src = source_dtype;
@@ -380,7 +346,7 @@ int mfh_backend_upload_async(mfh_backend* backend, const int64_t* shape, int32_t
 {
     if (!stored_as_is(source_dtype) && !dequantised(source_dtype)) {
         if (tensor) *tensor = nullptr;
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "tensor: dtype not supported by backend (%s)", wire_name(source_dtype));
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "tensor: dtype not supported by backend (%s)", dtype_string(source_dtype));
     }
     Plan p;
     p.src = source_dtype;
@@ -400,9 +366,9 @@ int mfh_backend_upload_fp8(mfh_backend* backend, const int64_t* shape, int32_t r
 {
     if (tensor) *tensor = nullptr;
     if (fp8_dtype != kF8E4M3 && fp8_dtype != kF8E5M2)
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_fp8: %s is not an FP8 dtype", wire_name(fp8_dtype));
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_fp8: %s is not an FP8 dtype", dtype_string(fp8_dtype));
     if (!stored_as_is(out_dtype))
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_fp8: output dtype %s is not F32/F16/BF16", wire_name(out_dtype));
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_fp8: output dtype %s is not F32/F16/BF16", dtype_string(out_dtype));
     Plan p;
     p.src = fp8_dtype;
     p.out = out_dtype;
@@ -418,9 +384,9 @@ int mfh_backend_upload_int4(mfh_backend* backend, const int64_t* shape, int32_t 
     const Device* dev;
     MFH_TRY(backend_ok(backend, &dev));
     if (scale_dtype != kFloat32 && scale_dtype != kFloat16 && scale_dtype != kBFloat16)
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_int4: scale dtype %s is not F32/F16/BF16", wire_name(scale_dtype));
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_int4: scale dtype %s is not F32/F16/BF16", dtype_string(scale_dtype));
     if (!stored_as_is(out_dtype))
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_int4: output dtype %s is not F32/F16/BF16", wire_name(out_dtype));
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "upload_int4: output dtype %s is not F32/F16/BF16", dtype_string(out_dtype));
     if (group <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "upload_int4: group must be positive, got %lld", (long long)group);
     std::vector<int64_t> dims;
     int64_t elements;
@@ -558,7 +524,7 @@ int mfh_tensor_slice(const mfh_tensor* t, int64_t start, int64_t length, mfh_ten
     *view = nullptr;
     MFH_TRY(tensor_ok(t));
     if (t->dtype == kInt4 || t->dtype == kBool)
-        return fail(MFH_ERR_INVALID_ARGUMENT, "slice: packed dtype %s", wire_name(t->dtype));
+        return fail(MFH_ERR_INVALID_ARGUMENT, "slice: packed dtype %s", dtype_string(t->dtype));
     if (start < 0 || length < 0 || start > t->elements || length > t->elements - start)
         return fail(MFH_ERR_SHAPE_INVALID, "tensor: invalid shape: slice [%lld, +%lld) out of range [0, %lld]",
                     (long long)start, (long long)length, (long long)t->elements);
@@ -629,13 +595,13 @@ int mfh_axpy_onto_resident(mfh_backend* backend, mfh_tensor* y, const mfh_tensor
     MFH_TRY(tensor_ok(x));
     // Location is "hip" for every tensor of this library (runtime/axpy.go:68-70).
     if (y->dtype != x->dtype)
-        return fail(MFH_ERR_INVALID_ARGUMENT, "math.axpy: y dtype %s does not match x dtype %s", wire_name(y->dtype),
-                    wire_name(x->dtype));
+        return fail(MFH_ERR_INVALID_ARGUMENT, "math.axpy: y dtype %s does not match x dtype %s", dtype_string(y->dtype),
+                    dtype_string(x->dtype));
     if (y->elements != x->elements)
         return fail(MFH_ERR_INVALID_ARGUMENT, "math.axpy: y length %lld does not match x length %lld",
                     (long long)y->elements, (long long)x->elements);
     if (!stored_as_is(y->dtype))
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "math.axpy: dtype %s has no device axpy", wire_name(y->dtype));
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "math.axpy: dtype %s has no device axpy", dtype_string(y->dtype));
     BackendState& s = *backend->state;
     std::lock_guard<std::mutex> lock(s.mu);
     // Order after uploads queued on other backends' streams.

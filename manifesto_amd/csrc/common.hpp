@@ -25,6 +25,12 @@ enum DType : uint8_t {
 int dtype_size(int dtype);
 // DType.Name (dtype/dtype.go:140-) for messages.
 const char* dtype_name(int dtype);
+// DType.String (dtype/dtype.go:190-231): the wire names ("F32", "BF16", ...)
+// the reference prints in its error messages.
+const char* dtype_string(int dtype);
+// DType.BytesFor (dtype/dtype.go:81-101): packed Int4 / Bool counts
+// included; -1 for a negative count or a dtype without a size.
+int64_t bytes_for(int dtype, int64_t elements);
 
 // Sets the calling thread's last error and returns `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

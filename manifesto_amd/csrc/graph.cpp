@@ -1,13 +1,14 @@
 // graph.cpp — the compile-and-dispatch layer around the HIP codegen target:
 // the manifest compute graph (ast.Graph), the optimizer's ConstantFold and
 // Fuse passes, codegen's AttachKernels with a HIP target, and CallGraph-style
-// execution of the lowered graph on one stream.
+// execution of the lowered graph on HIP streams.
 //
 // The passes restate the reference's Go semantics (file:line at each) so that
 // a C++ host gets the FusionASTs the Go compiler would hand to EmitHIP.
-// Execution runs the nodes in graph order; a value passed between nodes lives
-// in one per-graph device workspace whose offsets come from value lifetimes
-// (first-fit over a free list), so a steady-state call allocates nothing.
+// Execution launches the nodes in graph order on the streams ScheduleStreams
+// assigns (plan.cpp); a value passed between nodes lives in one per-graph
+// device workspace at offsets from the planner's interval colouring, so a
+// steady-state call allocates nothing.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -19,8 +20,10 @@
 #include <vector>
 
 #include "../../include/mfh_graph.h"
+#include "../../include/mfh_plan.h"
 #include "common.hpp"
 #include "fusion.hpp"
+#include "plan.hpp"
 
 namespace mfh {
 namespace {
@@ -196,6 +199,17 @@ struct mfh_graph {
     std::vector<float> ws_constants;  // the constants the workspace holds
     bool ws_constants_valid = false;
     uint32_t codegen_flags = 0;  // of the last AttachKernels; also used for unfused nodes
+    // stream mapping: StreamID k > 0 runs on aux[k - 1], StreamID 0 on the
+    // caller's stream; events[e] is SyncEvent e
+    int32_t max_streams = 1;
+    int32_t streams_used = 0;
+    std::vector<hipStream_t> aux;
+    std::vector<hipEvent_t> events;
+    std::vector<hipEvent_t> joins;  // per aux stream, back into the caller's
+    hipEvent_t fork = nullptr;
+    hipEvent_t done = nullptr;  // recorded after a call's last work
+    hipStream_t last_stream = nullptr;
+    bool called = false;
 };
 
 namespace mfh {
@@ -554,11 +568,14 @@ struct Slot {
     int64_t offset = 0;   // arena / constant offset in the workspace
     uint8_t dtype = kFloat32;
     int64_t count = 0;
-    int last_use = -1;
+    int producer = -1;          // step that writes it
+    std::vector<int> readers;   // steps that read it
+    bool pinned = false;        // read by the output copies after the last step
 };
 
 struct Step {
     HIPKernel* kernel = nullptr;
+    int node = -1;  // graph node index
     std::vector<int> operands;
     std::vector<mfh_operand> ops;
     int result = -1;
@@ -570,39 +587,14 @@ struct Copy {
     const mfh_value* to;
 };
 
-// First-fit placement of lifetimes in one region.
-struct Placer {
-    std::map<int64_t, int64_t> free;  // offset -> bytes
-    int64_t top = 0;
-    int64_t take(int64_t bytes)
-    {
-        for (auto it = free.begin(); it != free.end(); ++it) {
-            if (it->second < bytes) continue;
-            int64_t at = it->first, left = it->second - bytes;
-            free.erase(it);
-            if (left > 0) free.emplace(at + bytes, left);
-            return at;
-        }
-        int64_t at = top;
-        top += bytes;
-        return at;
-    }
-    void give(int64_t at, int64_t bytes)
-    {
-        auto it = free.emplace(at, bytes).first;
-        auto next = std::next(it);
-        if (next != free.end() && it->first + it->second == next->first) {
-            it->second += next->second;
-            free.erase(next);
-        }
-        if (it != free.begin()) {
-            auto prev = std::prev(it);
-            if (prev->first + prev->second == it->first) {
-                prev->second += it->second;
-                free.erase(it);
-            }
-        }
-    }
+// A call's values and launches, before placement and streams.
+struct Prepared {
+    std::vector<Slot> slots;
+    std::vector<Step> steps;
+    std::vector<Copy> copies;
+    std::vector<float> constants;
+    std::vector<int> node_slot;   // graph node -> the slot it defines
+    std::vector<int> input_slot;  // graph input -> its slot, -1 when unbound
 };
 
 int operand_mode(int64_t c, int64_t n, mfh_operand* op)
@@ -617,15 +609,14 @@ int operand_mode(int64_t c, int64_t n, mfh_operand* op)
     return MFH_OK;
 }
 
-int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
-               hipStream_t stream)
+// Binds inputs and outputs and lowers every node to a launch.  With
+// `shapes_only` the values' data pointers are not needed (planning).
+int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
+            bool shapes_only, Prepared* P)
 {
-    const Device* dev;
-    MFH_TRY(bind_device(&dev));
     if ((n_inputs > 0 && !inputs) || (n_outputs > 0 && !outputs) || n_inputs < 0 || n_outputs < 0)
         return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: bad value list");
-
-    std::vector<Slot> slots;
+    std::vector<Slot>& slots = P->slots;
     std::unordered_map<std::string, int> named;  // value name -> latest slot
     std::set<std::string> graph_inputs(g.inputs.begin(), g.inputs.end());
     for (int32_t i = 0; i < n_inputs; i++) {
@@ -636,7 +627,7 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         if (!hip_storage(v.dtype))
             return fail(MFH_ERR_DTYPE_UNSUPPORTED, "graph call: input \"%s\" is %s; values are Float32/Float16/BFloat16",
                         name.c_str(), dtype_name(v.dtype));
-        if (v.count < 0 || (v.count > 0 && !v.data))
+        if (v.count < 0 || (!shapes_only && v.count > 0 && !v.data))
             return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: input \"%s\" has no data", name.c_str());
         Slot s;
         s.kind = Slot::kInput;
@@ -645,6 +636,11 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         s.count = v.count;
         named[name] = (int)slots.size();
         slots.push_back(s);
+    }
+    P->input_slot.assign(g.inputs.size(), -1);
+    for (size_t k = 0; k < g.inputs.size(); k++) {
+        auto it = named.find(g.inputs[k]);
+        if (it != named.end()) P->input_slot[k] = it->second;
     }
     // Output bindings by value name.
     std::multimap<std::string, const mfh_value*> bound;
@@ -657,9 +653,7 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
     std::unordered_map<std::string, int> last_def;
     for (int i = 0; i < (int)g.nodes.size(); i++) last_def[g.nodes[i]->id] = i;
 
-    std::vector<float> constants;
-    std::vector<Step> steps;
-    std::vector<Copy> copies;
+    P->node_slot.assign(g.nodes.size(), -1);
     for (int i = 0; i < (int)g.nodes.size(); i++) {
         GraphNode& node = *g.nodes[i];
         if (node.op == kConstantOp) {
@@ -668,10 +662,10 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
                 return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: constant \"%s\" has no value", node.id.c_str());
             Slot s;
             s.kind = Slot::kConst;
-            s.offset = (int64_t)constants.size() * 4;
+            s.offset = (int64_t)P->constants.size() * 4;
             s.count = 1;
-            constants.push_back((float)it->second);  // fl32(Value), codegen/cpu.go:130-131
-            named[node.id] = (int)slots.size();
+            P->constants.push_back((float)it->second);  // fl32(Value), codegen/cpu.go:130-131
+            named[node.id] = P->node_slot[i] = (int)slots.size();
             slots.push_back(s);
             continue;
         }
@@ -702,8 +696,10 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
             return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\": op \"%s\" has no HIP lowering",
                         node.id.c_str(), node.op.c_str());
         }
+        const int t = (int)P->steps.size();
         Step st;
         st.kernel = kernel;
+        st.node = i;
         for (const std::string& name : node.inputs) {
             auto it = named.find(name);
             if (it == named.end())
@@ -725,12 +721,13 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
                             node.id.c_str(), node.inputs[k].c_str(), dtype_name(s.dtype),
                             dtype_name(kernel->declared[k]));
             st.ops.push_back(op);
-            s.last_use = (int)steps.size();  // index of the step being built
+            s.readers.push_back(t);
         }
         Slot out;
         out.dtype = kernel->out_dtype;
         out.count = st.count;
         out.kind = Slot::kArena;
+        out.producer = t;
         // The node that finally defines a bound output writes straight into
         // the caller's buffer when it matches.
         auto range = bound.equal_range(node.id);
@@ -742,9 +739,9 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
             }
         }
         st.result = (int)slots.size();
-        named[node.id] = st.result;
+        named[node.id] = P->node_slot[i] = st.result;
         slots.push_back(out);
-        steps.push_back(std::move(st));
+        P->steps.push_back(std::move(st));
     }
     // Bound outputs not written in place are copied at the end.
     for (const auto& kv : bound) {
@@ -761,32 +758,89 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         if (s.count > 0 && !b->data)
             return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: output \"%s\" has no data", b->name);
         if (s.kind == Slot::kBound && s.ptr == b->data) continue;
-        s.last_use = (int)steps.size() + 1;  // alive until the copies
-        copies.push_back(Copy{it->second, b});
+        s.pinned = true;
+        P->copies.push_back(Copy{it->second, b});
+    }
+    return MFH_OK;
+}
+
+// The launches as planning nodes: one per step, reading its operands' slots
+// and writing its result's.  Constants and graph inputs have no producer, so
+// they order nothing.
+Topology launch_topology(const Graph& g, const Prepared& P)
+{
+    Topology t;
+    t.ports.resize(P.slots.size());
+    for (const Step& st : P.steps) {
+        PlanNode n;
+        n.name = g.nodes[st.node]->id;
+        n.inputs.assign(st.operands.begin(), st.operands.end());
+        n.outputs.push_back(st.result);
+        t.nodes.push_back(std::move(n));
+    }
+    return t;
+}
+
+int graph_streams(Graph& g, int n_streams, int n_events)
+{
+    while ((int)g.aux.size() < n_streams - 1) {
+        hipStream_t s;
+        MFH_TRY(check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags(graph stream)"));
+        g.aux.push_back(s);
+        hipEvent_t e;
+        MFH_TRY(check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreateWithFlags"));
+        g.joins.push_back(e);
+    }
+    while ((int)g.events.size() < n_events) {
+        hipEvent_t e;
+        MFH_TRY(check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreateWithFlags"));
+        g.events.push_back(e);
+    }
+    if (!g.fork) MFH_TRY(check_hip(hipEventCreateWithFlags(&g.fork, hipEventDisableTiming), "hipEventCreateWithFlags"));
+    if (!g.done) MFH_TRY(check_hip(hipEventCreateWithFlags(&g.done, hipEventDisableTiming), "hipEventCreateWithFlags"));
+    return MFH_OK;
+}
+
+int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
+               hipStream_t stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    Prepared P;
+    MFH_TRY(prepare(g, inputs, n_inputs, outputs, n_outputs, false, &P));
+    std::vector<Slot>& slots = P.slots;
+    const int n_steps = (int)P.steps.size();
+
+    // Streams: ScheduleStreams over the launches (ir/stream_scheduler.go:56).
+    Topology topo = launch_topology(g, P);
+    MFH_TRY(schedule_streams(topo, g.max_streams));
+    int n_streams = 1, n_events = 0;
+    for (const PlanNode& n : topo.nodes) {
+        n_streams = std::max(n_streams, n.stream + 1);
+        for (const mfh_sync_event& e : n.barriers) n_events = std::max(n_events, e.event_id + 1);
     }
 
-    // Workspace layout: constants, then intermediates placed by lifetime.  A
-    // value is released after the last step that reads it (at once if none
-    // does); the result of a step is placed before its operands are released,
-    // so a kernel never writes over its own inputs.
-    const int n_steps = (int)steps.size();
-    const int64_t const_bytes = align_up((int64_t)constants.size() * 4);
-    std::vector<std::vector<int>> frees(n_steps);
-    for (int t = 0; t < n_steps; t++) {
-        const int r = steps[t].result;
-        if (slots[r].kind == Slot::kArena && slots[r].last_use < 0) slots[r].last_use = t;
+    // Workspace: constants, then the intermediates, placed so that a region
+    // is reused only after every launch touching its previous value is
+    // ordered before the new writer.  A step's result never shares memory
+    // with its operands, and a value copied out at the end is kept to the end.
+    const int64_t const_bytes = align_up((int64_t)P.constants.size() * 4);
+    std::vector<OrderedValue> values;
+    std::vector<int> value_slot;
+    for (int i = 0; i < (int)slots.size(); i++) {
+        const Slot& s = slots[i];
+        if (s.kind != Slot::kArena) continue;
+        OrderedValue v;
+        v.producer = s.producer;
+        v.users = s.readers;
+        if (s.pinned) v.users.push_back(kPinned);
+        v.size = std::max<int64_t>(1, s.count) * dtype_size(s.dtype);
+        values.push_back(std::move(v));
+        value_slot.push_back(i);
     }
-    for (int i = 0; i < (int)slots.size(); i++)
-        if (slots[i].kind == Slot::kArena && slots[i].last_use >= 0 && slots[i].last_use < n_steps)
-            frees[slots[i].last_use].push_back(i);
-    auto slot_bytes = [](const Slot& s) { return align_up(std::max<int64_t>(1, s.count) * dtype_size(s.dtype)); };
-    Placer placer;
-    for (int t = 0; t < n_steps; t++) {
-        Slot& r = slots[steps[t].result];
-        if (r.kind == Slot::kArena) r.offset = const_bytes + placer.take(slot_bytes(r));
-        for (int i : frees[t]) placer.give(slots[i].offset - const_bytes, slot_bytes(slots[i]));
-    }
-    const int64_t need = const_bytes + placer.top;
+    const int64_t arena = place_ordered(values, order_of(topo.nodes), kAlign);
+    for (size_t k = 0; k < values.size(); k++) slots[value_slot[k]].offset = const_bytes + values[k].offset;
+    const int64_t need = const_bytes + arena;
     if (need > g.ws_bytes) {
         if (g.ws) {
             // the previous workspace may still be read by queued work
@@ -799,32 +853,122 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         g.ws_bytes = need;
         g.ws_constants_valid = false;
     }
-    if (!constants.empty() && (!g.ws_constants_valid || g.ws_constants != constants)) {
-        g.ws_constants = constants;
-        MFH_TRY(check_hip(hipMemcpyAsync(g.ws, g.ws_constants.data(), constants.size() * 4, hipMemcpyHostToDevice,
+    MFH_TRY(graph_streams(g, n_streams, n_events));
+    // The workspace is shared by every call: work on a new caller stream
+    // waits for the previous call to finish with it.
+    if (g.called && g.last_stream != stream)
+        MFH_TRY(check_hip(hipStreamWaitEvent(stream, g.done, 0), "hipStreamWaitEvent(previous call)"));
+    if (!P.constants.empty() && (!g.ws_constants_valid || g.ws_constants != P.constants)) {
+        g.ws_constants = P.constants;
+        MFH_TRY(check_hip(hipMemcpyAsync(g.ws, g.ws_constants.data(), P.constants.size() * 4, hipMemcpyHostToDevice,
                                          stream), "hipMemcpyAsync(graph constants)"));
         g.ws_constants_valid = true;
+    }
+    // Fork: every other stream starts after the caller's queued work (the
+    // inputs, the constants).
+    if (n_streams > 1) {
+        MFH_TRY(check_hip(hipEventRecord(g.fork, stream), "hipEventRecord(fork)"));
+        for (int s = 1; s < n_streams; s++)
+            MFH_TRY(check_hip(hipStreamWaitEvent(g.aux[s - 1], g.fork, 0), "hipStreamWaitEvent(fork)"));
     }
     char* base = static_cast<char*>(g.ws);
     auto addr = [&](const Slot& s) -> void* {
         return s.kind == Slot::kInput || s.kind == Slot::kBound ? s.ptr : base + s.offset;
     };
+    auto on = [&](int32_t id) { return id == 0 ? stream : g.aux[id - 1]; };
     std::vector<const void*> ptrs;
-    for (const Step& st : steps) {
+    for (int t = 0; t < n_steps; t++) {
+        const Step& st = P.steps[t];
+        const PlanNode& pn = topo.nodes[t];
+        hipStream_t s = on(pn.stream);
+        for (const mfh_sync_event& e : pn.barriers)
+            if (e.wait) MFH_TRY(check_hip(hipStreamWaitEvent(s, g.events[e.event_id], 0), "hipStreamWaitEvent(barrier)"));
         const mfh_kernel* k = nullptr;
         MFH_TRY(st.kernel->variant(st.ops, &k));
         ptrs.clear();
         for (int o : st.operands) ptrs.push_back(addr(slots[o]));
-        MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, stream));
+        MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, s));
+        for (const mfh_sync_event& e : pn.barriers)
+            if (!e.wait) MFH_TRY(check_hip(hipEventRecord(g.events[e.event_id], s), "hipEventRecord(barrier)"));
     }
-    for (const Copy& c : copies) {
+    // Join: the caller's stream continues after every stream's last launch.
+    for (int s = 1; s < n_streams; s++) {
+        MFH_TRY(check_hip(hipEventRecord(g.joins[s - 1], g.aux[s - 1]), "hipEventRecord(join)"));
+        MFH_TRY(check_hip(hipStreamWaitEvent(stream, g.joins[s - 1], 0), "hipStreamWaitEvent(join)"));
+    }
+    for (const Copy& c : P.copies) {
         const Slot& s = slots[c.slot];
         const size_t bytes = (size_t)s.count * dtype_size(s.dtype);
         if (bytes)
             MFH_TRY(check_hip(hipMemcpyAsync(c.to->data, addr(s), bytes, hipMemcpyDeviceToDevice, stream),
                               "hipMemcpyAsync(graph output)"));
     }
+    MFH_TRY(check_hip(hipEventRecord(g.done, stream), "hipEventRecord(call done)"));
+    g.last_stream = stream;
+    g.called = true;
+    g.streams_used = n_streams;
     return MFH_OK;
+}
+
+// compiler.PlanGraph (compiler/plan.go:242-290): buildPlanningTopology
+// (:29-90), PlanWorkspace, attachGraphIOPorts (:179-228), ScheduleStreams.
+// The graph is taken in its own order (graph calls need it topological).
+int plan_graph(Graph& g, const mfh_value* inputs, int32_t n_inputs, int64_t align, int32_t max_streams, Topology* t)
+{
+    Prepared P;
+    MFH_TRY(prepare(g, inputs, n_inputs, nullptr, 0, true, &P));
+    auto port_for = [&](const Slot& s) {
+        PlanPort p;
+        p.dtype = s.kind == Slot::kConst ? kFloat32 : s.dtype;
+        p.dims = {s.count};
+        p.symbols = {""};
+        t->ports.push_back(p);
+        return (int32_t)t->ports.size() - 1;
+    };
+    std::map<std::string, int32_t> boundary, produced;
+    for (size_t k = 0; k < g.inputs.size(); k++) {
+        if (g.inputs[k].empty() || boundary.count(g.inputs[k])) continue;
+        const int slot = P.input_slot[k];
+        if (slot < 0) {
+            // an input the call leaves unbound has no shape to plan with
+            boundary[g.inputs[k]] = -1;
+            continue;
+        }
+        boundary[g.inputs[k]] = port_for(P.slots[slot]);
+    }
+    for (size_t i = 0; i < g.nodes.size(); i++) {
+        const GraphNode& node = *g.nodes[i];
+        PlanNode n;
+        n.name = node.id;
+        for (const std::string& name : node.inputs) {
+            auto p = produced.find(name);
+            if (p != produced.end()) {
+                n.inputs.push_back(p->second);
+                continue;
+            }
+            auto b = boundary.find(name);
+            n.inputs.push_back(b != boundary.end() ? b->second : -1);
+        }
+        const int32_t out = port_for(P.slots[P.node_slot[i]]);
+        n.outputs.push_back(out);
+        produced[node.id] = out;
+        t->nodes.push_back(std::move(n));
+    }
+    MFH_TRY(plan_workspace(*t, align));
+    for (const auto& kv : boundary) {
+        if (kv.second < 0 || !t->ports[kv.second].allocated)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "compiler: graph input \"%s\" has no workspace allocation", kv.first.c_str());
+        t->input_ports[kv.first] = t->ports[kv.second].offset;
+    }
+    for (const auto& kv : g.outputs) {
+        if (kv.first.empty()) continue;
+        auto p = produced.find(kv.second);
+        if (p == produced.end() || !t->ports[p->second].allocated)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "compiler: graph output \"%s\" producer \"%s\" has no workspace allocation",
+                        kv.first.c_str(), kv.second.c_str());
+        t->output_ports[kv.first] = t->ports[p->second].offset;
+    }
+    return schedule_streams(*t, max_streams);
 }
 
 }  // namespace
@@ -884,10 +1028,19 @@ int mfh_graph_release(mfh_graph* graph)
 {
     if (!graph) return MFH_OK;
     int rc = MFH_OK;
-    if (graph->ws) {
+    const bool device_state = graph->ws || graph->fork || graph->done || !graph->aux.empty() || !graph->events.empty();
+    if (device_state) {
         const Device* dev;
         rc = bind_device(&dev);
-        if (rc == MFH_OK) rc = check_hip(hipFree(graph->ws), "hipFree(graph workspace)");
+        if (rc == MFH_OK && graph->ws) rc = check_hip(hipFree(graph->ws), "hipFree(graph workspace)");
+        if (rc == MFH_OK) {
+            // hipFree waited for the device; the streams and events are idle
+            for (hipStream_t s : graph->aux) (void)hipStreamDestroy(s);
+            for (hipEvent_t e : graph->events) (void)hipEventDestroy(e);
+            for (hipEvent_t e : graph->joins) (void)hipEventDestroy(e);
+            if (graph->fork) (void)hipEventDestroy(graph->fork);
+            if (graph->done) (void)hipEventDestroy(graph->done);
+        }
     }
     delete graph;
     return rc;
@@ -1136,5 +1289,27 @@ int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, 
 }
 
 int64_t mfh_graph_workspace_bytes(const mfh_graph* graph) { return graph ? graph->ws_bytes : -1; }
+
+int mfh_graph_set_max_streams(mfh_graph* graph, int32_t max_streams)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_max_streams: graph is required");
+    if (max_streams < 1 || max_streams > 64)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_max_streams: %d streams; 1 to 64 are supported", (int)max_streams);
+    graph->max_streams = max_streams;
+    return MFH_OK;
+}
+
+int32_t mfh_graph_streams_used(const mfh_graph* graph) { return graph ? graph->streams_used : -1; }
+
+int mfh_graph_plan(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, int64_t align, int32_t max_streams,
+                   mfh_topology** topology)
+{
+    if (!graph || !topology) return fail(MFH_ERR_INVALID_ARGUMENT, "compiler: graph is required");
+    *topology = nullptr;
+    auto t = std::make_unique<mfh_topology>();
+    MFH_TRY(plan_graph(*graph, inputs, n_inputs, align, max_streams, t.get()));
+    *topology = t.release();
+    return MFH_OK;
+}
 
 }  // extern "C"

@@ -90,6 +90,51 @@ const char* dtype_name(int dtype)
     }
 }
 
+const char* dtype_string(int dt)
+{
+    switch (dt) {
+    case kInvalid: return "INVALID";
+    case kFloat64: return "F64";
+    case kFloat32: return "F32";
+    case kFloat16: return "F16";
+    case kBFloat16: return "BF16";
+    case kF8E4M3: return "F8E4M3";
+    case kF8E5M2: return "F8E5M2";
+    case kInt64: return "I64";
+    case kInt32: return "I32";
+    case kInt16: return "I16";
+    case kInt8: return "I8";
+    case kInt4: return "I4";
+    case kUint64: return "U64";
+    case kUint32: return "U32";
+    case kUint16: return "U16";
+    case kUint8: return "U8";
+    case kBool: return "BOOL";
+    case kComplex64: return "C64";
+    case kComplex128: return "C128";
+    default: {
+        thread_local char buf[24];
+        snprintf(buf, sizeof buf, "DTYPE(%d)", dt);
+        return buf;
+    }
+    }
+}
+
+int64_t bytes_for(int dt, int64_t elements)
+{
+    if (elements < 0) return -1;
+    switch (dt) {
+    case kInt4: return (elements + 1) / 2;
+    case kBool: return (elements + 7) / 8;
+    case kComplex64: return elements * 8;
+    case kComplex128: return elements * 16;
+    default: {
+        const int size = dtype_size(dt);
+        return size > 0 ? elements * size : -1;
+    }
+    }
+}
+
 int bind_device(const Device** out)
 {
     if (!g_ready.load(std::memory_order_acquire))
