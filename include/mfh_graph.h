@@ -177,6 +177,19 @@ int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, 
 /* Bytes of the graph's device workspace (0 before the first call). */
 int64_t mfh_graph_workspace_bytes(const mfh_graph* graph);
 
+/* Launch replay (no counterpart in the reference, whose CallGraph dispatches
+ * node by node): a call identical to an earlier one (same value names,
+ * pointers, dtypes and counts, same workspace and stream budget) is captured
+ * as a HIP graph on its second occurrence and replayed with one
+ * hipGraphLaunch from then on; the first occurrence runs as plain launches.
+ * Up to 8 distinct calls are kept per graph (least recently used dropped).
+ * Any change to the graph drops them.  A call made on a stream that is
+ * itself being captured runs as plain launches into that capture.  Enabled
+ * by default; mfh_graph_set_replay(graph, 0) turns it off.
+ * mfh_graph_replayed_calls counts the calls that ran as replays. */
+int mfh_graph_set_replay(mfh_graph* graph, int32_t enabled);
+int64_t mfh_graph_replayed_calls(const mfh_graph* graph);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,7 @@
 // every Add/Sub/Mul/Div rounds on its own as in Go, and cached by its text.
 #include <hip/hiprtc.h>
 
+#include <atomic>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -167,6 +168,9 @@ struct CodeObject {
 
 std::mutex g_cache_mu;
 std::unordered_map<std::string, std::shared_ptr<CodeObject>> g_cache;
+// Bumped whenever a loaded module is unloaded, so that holders of function
+// handles (captured graph calls) know theirs may be gone.
+std::atomic<uint64_t> g_module_generation{0};
 
 int compile_source(const std::string& source, const std::string& kernel_name, std::shared_ptr<CodeObject>* out)
 {
@@ -214,6 +218,7 @@ int load_function(CodeObject& obj, int device, hipFunction_t* fn)
         return MFH_OK;
     }
     if (obj.module) {
+        g_module_generation.fetch_add(1);
         (void)hipModuleUnload(obj.module);
         obj.module = nullptr;
         obj.function = nullptr;
@@ -449,9 +454,12 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
                      "hipModuleLaunchKernel");
 }
 
+uint64_t module_generation() { return g_module_generation.load(); }
+
 void release_kernel_cache()
 {
     std::lock_guard<std::mutex> lock(g_cache_mu);
+    g_module_generation.fetch_add(1);
     for (auto& kv : g_cache) {
         std::lock_guard<std::mutex> obj_lock(kv.second->mu);
         if (kv.second->module) (void)hipModuleUnload(kv.second->module);

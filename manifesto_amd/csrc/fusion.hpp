@@ -25,6 +25,9 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
              uint8_t out_dtype, const char* output_port, uint32_t flags, mfh_kernel** out);
 int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
             hipStream_t stream);
+// Changes whenever a loaded kernel module is unloaded (shutdown, device
+// change); function handles taken before a change may be dangling.
+uint64_t module_generation();
 
 }  // namespace mfh
 

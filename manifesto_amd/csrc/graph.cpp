@@ -185,6 +185,15 @@ struct GraphNode {
     std::shared_ptr<HIPKernel> solo;     // one-node kernel of an unfused elementwise node
 };
 
+// One call seen before: its key and, once captured, its executable graph.
+struct Replay {
+    std::string key;
+    hipGraphExec_t exec = nullptr;
+    int streams = 1;
+    uint64_t tick = 0;
+};
+constexpr int kMaxReplays = 8;
+
 }  // namespace
 }  // namespace mfh
 
@@ -210,6 +219,15 @@ struct mfh_graph {
     hipEvent_t done = nullptr;  // recorded after a call's last work
     hipStream_t last_stream = nullptr;
     bool called = false;
+    // calls replayed as HIP graphs, keyed by everything their launches
+    // depend on; cleared by any change to the graph
+    bool replay = true;
+    bool replay_broken = false;
+    std::vector<mfh::Replay> replays;
+    uint64_t replay_clock = 0;
+    uint64_t replay_generation = 0;
+    int64_t replayed = 0;
+    hipStream_t capture = nullptr;
 };
 
 namespace mfh {
@@ -801,15 +819,116 @@ int graph_streams(Graph& g, int n_streams, int n_events)
     return MFH_OK;
 }
 
+// The launches of one call on `ls` and the graph's other streams: fork from
+// `ls`, every node with its waits and signals, join back into `ls`, then the
+// output copies.  With `ls` capturing, this records the call as a graph.
+int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipStream_t ls)
+{
+    std::vector<Slot>& slots = P.slots;
+    if (n_streams > 1) {
+        MFH_TRY(check_hip(hipEventRecord(g.fork, ls), "hipEventRecord(fork)"));
+        for (int s = 1; s < n_streams; s++)
+            MFH_TRY(check_hip(hipStreamWaitEvent(g.aux[s - 1], g.fork, 0), "hipStreamWaitEvent(fork)"));
+    }
+    char* base = static_cast<char*>(g.ws);
+    auto addr = [&](const Slot& s) -> void* {
+        return s.kind == Slot::kInput || s.kind == Slot::kBound ? s.ptr : base + s.offset;
+    };
+    auto on = [&](int32_t id) { return id == 0 ? ls : g.aux[id - 1]; };
+    std::vector<const void*> ptrs;
+    for (size_t t = 0; t < P.steps.size(); t++) {
+        const Step& st = P.steps[t];
+        const PlanNode& pn = topo.nodes[t];
+        hipStream_t s = on(pn.stream);
+        for (const mfh_sync_event& e : pn.barriers)
+            if (e.wait) MFH_TRY(check_hip(hipStreamWaitEvent(s, g.events[e.event_id], 0), "hipStreamWaitEvent(barrier)"));
+        const mfh_kernel* k = nullptr;
+        MFH_TRY(st.kernel->variant(st.ops, &k));
+        ptrs.clear();
+        for (int o : st.operands) ptrs.push_back(addr(slots[o]));
+        MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, s));
+        for (const mfh_sync_event& e : pn.barriers)
+            if (!e.wait) MFH_TRY(check_hip(hipEventRecord(g.events[e.event_id], s), "hipEventRecord(barrier)"));
+    }
+    for (int s = 1; s < n_streams; s++) {
+        MFH_TRY(check_hip(hipEventRecord(g.joins[s - 1], g.aux[s - 1]), "hipEventRecord(join)"));
+        MFH_TRY(check_hip(hipStreamWaitEvent(ls, g.joins[s - 1], 0), "hipStreamWaitEvent(join)"));
+    }
+    for (const Copy& c : P.copies) {
+        const Slot& s = slots[c.slot];
+        const size_t bytes = (size_t)s.count * dtype_size(s.dtype);
+        if (bytes)
+            MFH_TRY(check_hip(hipMemcpyAsync(c.to->data, addr(s), bytes, hipMemcpyDeviceToDevice, ls),
+                              "hipMemcpyAsync(graph output)"));
+    }
+    return MFH_OK;
+}
+
+// Everything a call's launches depend on: value names, pointers, dtypes and
+// counts, the workspace, the stream budget.
+std::string call_key(const Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
+                     int32_t n_outputs)
+{
+    std::string key;
+    char buf[96];
+    auto add = [&](const mfh_value& v) {
+        key += v.name ? v.name : "";
+        snprintf(buf, sizeof buf, "|%p|%u|%lld;", v.data, (unsigned)v.dtype, (long long)v.count);
+        key += buf;
+    };
+    for (int32_t i = 0; i < n_inputs; i++) add(inputs[i]);
+    key += "->";
+    for (int32_t i = 0; i < n_outputs; i++) add(outputs[i]);
+    snprintf(buf, sizeof buf, "ws=%p/%lld;s=%d", g.ws, (long long)g.ws_bytes, (int)g.max_streams);
+    return key + buf;
+}
+
+// Waits for the last call, then drops every captured call.
+void drop_replays(Graph& g)
+{
+    bool any = false;
+    for (const Replay& r : g.replays) any = any || r.exec;
+    if (any && g.done) (void)hipEventSynchronize(g.done);
+    for (Replay& r : g.replays)
+        if (r.exec) (void)hipGraphExecDestroy(r.exec);
+    g.replays.clear();
+}
+
 int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
                hipStream_t stream)
 {
     const Device* dev;
     MFH_TRY(bind_device(&dev));
+    if (!g.replays.empty() && g.replay_generation != module_generation()) drop_replays(g);
+
+    // A call the caller is capturing runs as plain launches into their graph.
+    hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
+    MFH_TRY(check_hip(hipStreamIsCapturing(stream, &capturing), "hipStreamIsCapturing"));
+    const bool replayable = g.replay && !g.replay_broken && capturing == hipStreamCaptureStatusNone;
+    std::string key;
+    Replay* seen = nullptr;
+    if (replayable) {
+        key = call_key(g, inputs, n_inputs, outputs, n_outputs);
+        for (Replay& r : g.replays)
+            if (r.key == key) seen = &r;
+        if (seen && seen->exec) {
+            // the same call again: replay its graph
+            if (g.called && g.last_stream != stream)
+                MFH_TRY(check_hip(hipStreamWaitEvent(stream, g.done, 0), "hipStreamWaitEvent(previous call)"));
+            MFH_TRY(check_hip(hipGraphLaunch(seen->exec, stream), "hipGraphLaunch(graph call)"));
+            seen->tick = ++g.replay_clock;
+            g.replayed++;
+            g.streams_used = seen->streams;
+            MFH_TRY(check_hip(hipEventRecord(g.done, stream), "hipEventRecord(call done)"));
+            g.last_stream = stream;
+            g.called = true;
+            return MFH_OK;
+        }
+    }
+
     Prepared P;
     MFH_TRY(prepare(g, inputs, n_inputs, outputs, n_outputs, false, &P));
     std::vector<Slot>& slots = P.slots;
-    const int n_steps = (int)P.steps.size();
 
     // Streams: ScheduleStreams over the launches (ir/stream_scheduler.go:56).
     Topology topo = launch_topology(g, P);
@@ -841,7 +960,15 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
     const int64_t arena = place_ordered(values, order_of(topo.nodes), kAlign);
     for (size_t k = 0; k < values.size(); k++) slots[value_slot[k]].offset = const_bytes + values[k].offset;
     const int64_t need = const_bytes + arena;
+    const bool captured = capturing != hipStreamCaptureStatusNone;
+    if (need > g.ws_bytes && captured)
+        return fail(MFH_ERR_INVALID_ARGUMENT,
+                    "graph call: the workspace must grow to %lld bytes while the caller's stream is being captured; "
+                    "make the same call once before capturing", (long long)need);
     if (need > g.ws_bytes) {
+        // captured calls address the old workspace
+        drop_replays(g);
+        seen = nullptr;
         if (g.ws) {
             // the previous workspace may still be read by queued work
             MFH_TRY(check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize"));
@@ -852,61 +979,77 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         MFH_TRY(check_hip(hipMalloc(&g.ws, (size_t)need), "hipMalloc(graph workspace)"));
         g.ws_bytes = need;
         g.ws_constants_valid = false;
+        // this call is remembered under the new workspace
+        if (replayable) key = call_key(g, inputs, n_inputs, outputs, n_outputs);
     }
     MFH_TRY(graph_streams(g, n_streams, n_events));
     // The workspace is shared by every call: work on a new caller stream
-    // waits for the previous call to finish with it.
-    if (g.called && g.last_stream != stream)
+    // waits for the previous call to finish with it.  (A capturing caller
+    // orders its capture itself.)
+    if (!captured && g.called && g.last_stream != stream)
         MFH_TRY(check_hip(hipStreamWaitEvent(stream, g.done, 0), "hipStreamWaitEvent(previous call)"));
-    if (!P.constants.empty() && (!g.ws_constants_valid || g.ws_constants != P.constants)) {
+    const bool new_constants = !P.constants.empty() && (!g.ws_constants_valid || g.ws_constants != P.constants);
+    if (new_constants && captured)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: the graph's constants must be uploaded while the caller's "
+                    "stream is being captured; make the same call once before capturing");
+    if (new_constants) {
         g.ws_constants = P.constants;
         MFH_TRY(check_hip(hipMemcpyAsync(g.ws, g.ws_constants.data(), P.constants.size() * 4, hipMemcpyHostToDevice,
                                          stream), "hipMemcpyAsync(graph constants)"));
         g.ws_constants_valid = true;
     }
-    // Fork: every other stream starts after the caller's queued work (the
-    // inputs, the constants).
-    if (n_streams > 1) {
-        MFH_TRY(check_hip(hipEventRecord(g.fork, stream), "hipEventRecord(fork)"));
-        for (int s = 1; s < n_streams; s++)
-            MFH_TRY(check_hip(hipStreamWaitEvent(g.aux[s - 1], g.fork, 0), "hipStreamWaitEvent(fork)"));
+
+    // The second identical call is captured once and replayed from then on;
+    // the first runs as plain launches (and loads every kernel it needs).
+    bool launched = false;
+    if (replayable && seen) {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        if (!g.capture) MFH_TRY(check_hip(hipStreamCreateWithFlags(&g.capture, hipStreamNonBlocking), "hipStreamCreateWithFlags"));
+        if (hipStreamBeginCapture(g.capture, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+            const int rc = launch_all(g, P, topo, n_streams, g.capture);
+            const hipError_t end = hipStreamEndCapture(g.capture, &graph);
+            if (rc == MFH_OK && end == hipSuccess && graph &&
+                hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess)
+                exec = nullptr;
+        }
+        if (graph) (void)hipGraphDestroy(graph);
+        if (exec) {
+            seen->exec = exec;
+            seen->streams = n_streams;
+            seen->tick = ++g.replay_clock;
+            MFH_TRY(check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch(graph call)"));
+            launched = true;
+        } else {
+            // capture is not available here: this call and later ones run as
+            // plain launches
+            (void)hipGetLastError();
+            g.replay_broken = true;
+        }
     }
-    char* base = static_cast<char*>(g.ws);
-    auto addr = [&](const Slot& s) -> void* {
-        return s.kind == Slot::kInput || s.kind == Slot::kBound ? s.ptr : base + s.offset;
-    };
-    auto on = [&](int32_t id) { return id == 0 ? stream : g.aux[id - 1]; };
-    std::vector<const void*> ptrs;
-    for (int t = 0; t < n_steps; t++) {
-        const Step& st = P.steps[t];
-        const PlanNode& pn = topo.nodes[t];
-        hipStream_t s = on(pn.stream);
-        for (const mfh_sync_event& e : pn.barriers)
-            if (e.wait) MFH_TRY(check_hip(hipStreamWaitEvent(s, g.events[e.event_id], 0), "hipStreamWaitEvent(barrier)"));
-        const mfh_kernel* k = nullptr;
-        MFH_TRY(st.kernel->variant(st.ops, &k));
-        ptrs.clear();
-        for (int o : st.operands) ptrs.push_back(addr(slots[o]));
-        MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, s));
-        for (const mfh_sync_event& e : pn.barriers)
-            if (!e.wait) MFH_TRY(check_hip(hipEventRecord(g.events[e.event_id], s), "hipEventRecord(barrier)"));
-    }
-    // Join: the caller's stream continues after every stream's last launch.
-    for (int s = 1; s < n_streams; s++) {
-        MFH_TRY(check_hip(hipEventRecord(g.joins[s - 1], g.aux[s - 1]), "hipEventRecord(join)"));
-        MFH_TRY(check_hip(hipStreamWaitEvent(stream, g.joins[s - 1], 0), "hipStreamWaitEvent(join)"));
-    }
-    for (const Copy& c : P.copies) {
-        const Slot& s = slots[c.slot];
-        const size_t bytes = (size_t)s.count * dtype_size(s.dtype);
-        if (bytes)
-            MFH_TRY(check_hip(hipMemcpyAsync(c.to->data, addr(s), bytes, hipMemcpyDeviceToDevice, stream),
-                              "hipMemcpyAsync(graph output)"));
+    if (!launched) MFH_TRY(launch_all(g, P, topo, n_streams, stream));
+    g.streams_used = n_streams;
+    if (captured) return MFH_OK;
+    if (replayable && !seen) {
+        if ((int)g.replays.size() >= kMaxReplays) {
+            // forget the least recently used call
+            auto old = std::min_element(g.replays.begin(), g.replays.end(),
+                                        [](const Replay& a, const Replay& b) { return a.tick < b.tick; });
+            if (old->exec) {
+                (void)hipEventSynchronize(g.done);
+                (void)hipGraphExecDestroy(old->exec);
+            }
+            g.replays.erase(old);
+        }
+        Replay r;
+        r.key = key;
+        r.tick = ++g.replay_clock;
+        g.replays.push_back(std::move(r));
+        g.replay_generation = module_generation();
     }
     MFH_TRY(check_hip(hipEventRecord(g.done, stream), "hipEventRecord(call done)"));
     g.last_stream = stream;
     g.called = true;
-    g.streams_used = n_streams;
     return MFH_OK;
 }
 
@@ -1028,8 +1171,10 @@ int mfh_graph_release(mfh_graph* graph)
 {
     if (!graph) return MFH_OK;
     int rc = MFH_OK;
-    const bool device_state = graph->ws || graph->fork || graph->done || !graph->aux.empty() || !graph->events.empty();
+    const bool device_state = graph->ws || graph->fork || graph->done || !graph->aux.empty() || !graph->events.empty() ||
+                              graph->capture || !graph->replays.empty();
     if (device_state) {
+        drop_replays(*graph);
         const Device* dev;
         rc = bind_device(&dev);
         if (rc == MFH_OK && graph->ws) rc = check_hip(hipFree(graph->ws), "hipFree(graph workspace)");
@@ -1038,6 +1183,7 @@ int mfh_graph_release(mfh_graph* graph)
             for (hipStream_t s : graph->aux) (void)hipStreamDestroy(s);
             for (hipEvent_t e : graph->events) (void)hipEventDestroy(e);
             for (hipEvent_t e : graph->joins) (void)hipEventDestroy(e);
+            if (graph->capture) (void)hipStreamDestroy(graph->capture);
             if (graph->fork) (void)hipEventDestroy(graph->fork);
             if (graph->done) (void)hipEventDestroy(graph->done);
         }
@@ -1048,6 +1194,7 @@ int mfh_graph_release(mfh_graph* graph)
 
 int mfh_graph_add_input(mfh_graph* graph, const char* name)
 {
+    if (graph) drop_replays(*graph);
     if (!graph || !name) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_input: graph and name are required");
     graph->inputs.push_back(name);
     return MFH_OK;
@@ -1055,6 +1202,7 @@ int mfh_graph_add_input(mfh_graph* graph, const char* name)
 
 int mfh_graph_set_output(mfh_graph* graph, const char* key, const char* value)
 {
+    if (graph) drop_replays(*graph);
     if (!graph || !key || !value)
         return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_output: graph, key and value are required");
     for (auto& kv : graph->outputs)
@@ -1068,6 +1216,7 @@ int mfh_graph_set_output(mfh_graph* graph, const char* key, const char* value)
 
 int mfh_graph_add_node(mfh_graph* graph, const char* id, const char* op, const char* const* inputs, int32_t n_inputs)
 {
+    if (graph) drop_replays(*graph);
     if (!graph || !id || !op) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_node: graph, id and op are required");
     if (n_inputs < 0 || (n_inputs > 0 && !inputs))
         return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_node: bad input list");
@@ -1084,6 +1233,7 @@ int mfh_graph_add_node(mfh_graph* graph, const char* id, const char* op, const c
 
 int mfh_graph_set_attribute(mfh_graph* graph, int32_t node, const char* key, double value)
 {
+    if (graph) drop_replays(*graph);
     GraphNode* n = node_at(graph, node);
     if (!n) return bad_node("mfh_graph_set_attribute", node);
     if (!key) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_attribute: key is NULL");
@@ -1094,6 +1244,7 @@ int mfh_graph_set_attribute(mfh_graph* graph, int32_t node, const char* key, dou
 int mfh_graph_set_types(mfh_graph* graph, int32_t node, const uint8_t* input_types, int32_t n_input_types,
                         uint8_t output_type)
 {
+    if (graph) drop_replays(*graph);
     GraphNode* n = node_at(graph, node);
     if (!n) return bad_node("mfh_graph_set_types", node);
     if (n_input_types < 0 || (n_input_types > 0 && !input_types))
@@ -1107,6 +1258,7 @@ int mfh_graph_set_fusion(mfh_graph* graph, int32_t node, const mfh_ast_node* nod
                          int32_t n_nodes, const char* const* input_ports, int32_t n_input_ports,
                          const char* output_port, uint8_t dtype)
 {
+    if (graph) drop_replays(*graph);
     GraphNode* n = node_at(graph, node);
     if (!n) return bad_node("mfh_graph_set_fusion", node);
     if (!nodes || n_nodes <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: root is required");
@@ -1242,18 +1394,21 @@ int32_t mfh_optimizer_elementwise_ops(const char** ops, int32_t cap)
 
 int mfh_optimizer_constant_fold(mfh_graph* graph, int32_t* nodes_folded)
 {
+    if (graph) drop_replays(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
     return constant_fold(*graph, nodes_folded);
 }
 
 int mfh_optimizer_fuse(mfh_graph* graph, mfh_fusion_stats* stats)
 {
+    if (graph) drop_replays(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
     return fuse(*graph, stats);
 }
 
 int mfh_optimizer_run(mfh_graph* graph, uint32_t options, int32_t* nodes_folded, mfh_fusion_stats* stats)
 {
+    if (graph) drop_replays(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
     if (nodes_folded) *nodes_folded = 0;
     if (stats) *stats = mfh_fusion_stats{0, 0, 0};
@@ -1265,6 +1420,7 @@ int mfh_optimizer_run(mfh_graph* graph, uint32_t options, int32_t* nodes_folded,
 int mfh_codegen_attach_kernels(mfh_graph* graph, const int32_t* targets, int32_t n_targets, uint32_t flags,
                                int32_t* attached)
 {
+    if (graph) drop_replays(*graph);
     if (attached) *attached = 0;
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen: graph is required");
     return attach_kernels(*graph, targets, n_targets, flags, attached);
@@ -1292,6 +1448,7 @@ int64_t mfh_graph_workspace_bytes(const mfh_graph* graph) { return graph ? graph
 
 int mfh_graph_set_max_streams(mfh_graph* graph, int32_t max_streams)
 {
+    if (graph) drop_replays(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_max_streams: graph is required");
     if (max_streams < 1 || max_streams > 64)
         return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_max_streams: %d streams; 1 to 64 are supported", (int)max_streams);
@@ -1300,6 +1457,17 @@ int mfh_graph_set_max_streams(mfh_graph* graph, int32_t max_streams)
 }
 
 int32_t mfh_graph_streams_used(const mfh_graph* graph) { return graph ? graph->streams_used : -1; }
+
+int mfh_graph_set_replay(mfh_graph* graph, int32_t enabled)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_replay: graph is required");
+    drop_replays(*graph);
+    graph->replay = enabled != 0;
+    graph->replay_broken = false;
+    return MFH_OK;
+}
+
+int64_t mfh_graph_replayed_calls(const mfh_graph* graph) { return graph ? graph->replayed : -1; }
 
 int mfh_graph_plan(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, int64_t align, int32_t max_streams,
                    mfh_topology** topology)

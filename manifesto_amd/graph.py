@@ -99,6 +99,8 @@ def _L():
             "mfh_graph_kernel": (c.c_int, [vp, i32, i32, c.POINTER(vp)]),
             "mfh_graph_call": (c.c_int, [vp, c.POINTER(Value), i32, c.POINTER(Value), i32, vp]),
             "mfh_graph_workspace_bytes": (i64, [vp]),
+            "mfh_graph_set_replay": (c.c_int, [vp, i32]),
+            "mfh_graph_replayed_calls": (i64, [vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -288,6 +290,14 @@ class Graph:
 
     def workspace_bytes(self) -> int:
         return _L().mfh_graph_workspace_bytes(self._h)
+
+    def set_replay(self, enabled: bool) -> None:
+        """Replays of repeated identical calls as captured HIP graphs (on by
+        default)."""
+        check(_L().mfh_graph_set_replay(self._h, int(enabled)))
+
+    def replayed_calls(self) -> int:
+        return _L().mfh_graph_replayed_calls(self._h)
 
     def call(self, inputs: dict, outputs: dict, stream: int = 0) -> None:
         """runtime.Backend.CallGraph on the device: `inputs` maps input names

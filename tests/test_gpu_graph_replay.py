@@ -1,0 +1,189 @@
+"""GPU tests of graph-call replay: a call identical to an earlier one is
+captured as a HIP graph on its second occurrence and replayed afterwards.
+
+Every call's outputs are checked against numpy float32 evaluations of the same
+exact ops (one IEEE f32 rounding each), with the inputs rewritten by eager
+torch work and a synchronisation between calls, so a replay that reads stale
+inputs, skips a node or misses a changed constant shows up as a wrong value.
+"""
+import numpy as np
+import pytest
+
+import manifesto_amd as M
+from manifesto_amd import graph as G
+from manifesto_amd import plan as P
+from manifesto_amd.abi import check
+from manifesto_amd.graph import Graph, GraphNode
+
+from gpu_util import log, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+F32 = M.FLOAT32
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    M.init(0)
+
+
+def chain_graph(fuse=True):
+    # k = 0.75; a = x * k; b = a + y; c = relu(b); d = -c; e = max(d, x)
+    g = Graph(inputs=["x", "y"], outputs={"e": "e", "c": "c"}, execution_dtype=F32, nodes=[
+        GraphNode("k", "math.constant", [], attributes={"value": 0.75}),
+        GraphNode("a", "math.mul", ["x", "k"]), GraphNode("b", "math.add", ["a", "y"]),
+        GraphNode("c", "activation.relu", ["b"]), GraphNode("d", "math.neg", ["c"]),
+        GraphNode("e", "math.max", ["d", "x"])])
+    if fuse:
+        G.run(g)
+        G.attach_kernels(g)
+    return g
+
+
+def chain_expected(x, y, k=0.75):
+    # the evaluator's rules: relu v < 0 ? 0 : v, max l > r ? l : r (codegen/cpu.go)
+    b = x * np.float32(k) + y
+    c = np.where(b < 0, np.float32(0), b)
+    d = -c
+    return {"e": np.where(d > x, d, x), "c": c}
+
+
+class Buffers:
+    def __init__(self, n, keys):
+        torch = torch_mod()
+        self.n = n
+        self.x = torch.empty(n, device="cuda")
+        self.y = torch.empty(n, device="cuda")
+        self.out = {k: torch.empty(n, device="cuda") for k in keys}
+
+    def fill(self, rng):
+        torch = torch_mod()
+        x = rng.normal(0, 1, self.n).astype(np.float32)
+        y = rng.normal(0, 1, self.n).astype(np.float32)
+        self.x.copy_(torch.from_numpy(x))  # eager work between calls
+        self.y.copy_(torch.from_numpy(y))
+        for t in self.out.values():
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        return x, y
+
+    def call(self, graph, stream=None):
+        torch = torch_mod()
+        s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        graph.call({"x": self.x, "y": self.y}, self.out, s)
+
+    def check(self, want, what):
+        torch = torch_mod()
+        torch.cuda.synchronize()
+        for k, t in self.out.items():
+            got = t.cpu().numpy()
+            bad = np.flatnonzero(got.view(np.uint32) != want[k].view(np.uint32))
+            assert bad.size == 0, f"{what} output {k}: {bad.size} mismatches, first at {bad[:4]}"
+
+
+def test_replays_follow_new_input_contents():
+    rng = np.random.default_rng(21)
+    g = chain_graph()
+    b = Buffers((1 << 20) + 5, ["e", "c"])
+    for call in range(6):
+        log(f"graph replay call {call}")
+        x, y = b.fill(rng)
+        b.call(g)
+        b.check(chain_expected(x, y), f"call {call}")
+    # call 0 launches, call 1 is captured, calls 2-5 replay
+    assert g.replayed_calls() == 4
+
+
+def test_replays_dropped_when_the_graph_changes():
+    rng = np.random.default_rng(22)
+    g = chain_graph()
+    b = Buffers(4099, ["e", "c"])
+    for _ in range(3):
+        x, y = b.fill(rng)
+        b.call(g)
+        b.check(chain_expected(x, y), "before the change")
+    assert g.replayed_calls() == 1
+    # change the constant (node 0): the next calls must use 1.5
+    assert g.nodes[0].op == G.CONSTANT_OP
+    check(G._L().mfh_graph_set_attribute(g._h, 0, b"value", 1.5))
+    for call in range(4):
+        x, y = b.fill(rng)
+        b.call(g)
+        b.check(chain_expected(x, y, 1.5), f"after the change, call {call}")
+    assert g.replayed_calls() == 3
+
+
+def test_replays_per_buffer_set():
+    rng = np.random.default_rng(23)
+    g = chain_graph()
+    sets = [Buffers(3 << 16, ["e", "c"]), Buffers(3 << 16, ["e", "c"])]
+    for call in range(6):
+        b = sets[call % 2]
+        x, y = b.fill(rng)
+        b.call(g)
+        b.check(chain_expected(x, y), f"set {call % 2} call {call}")
+    assert g.replayed_calls() == 2  # the third call of each set
+
+
+def test_replay_off():
+    rng = np.random.default_rng(24)
+    g = chain_graph()
+    g.set_replay(False)
+    b = Buffers(1000, ["e", "c"])
+    for call in range(4):
+        x, y = b.fill(rng)
+        b.call(g)
+        b.check(chain_expected(x, y), f"call {call}")
+    assert g.replayed_calls() == 0
+
+
+def test_multi_stream_replay():
+    rng = np.random.default_rng(25)
+    nodes = [GraphNode("a1", "math.neg", ["x"]), GraphNode("a2", "math.abs", ["a1"]),
+             GraphNode("b1", "math.abs", ["y"]), GraphNode("b2", "math.max", ["b1", "a1"]),
+             GraphNode("c1", "math.mul", ["x", "y"]), GraphNode("d", "math.add", ["a2", "b2"]),
+             GraphNode("e", "math.sub", ["d", "c1"])]
+    g = Graph(inputs=["x", "y"], outputs={"e": "e", "b2": "b2"}, execution_dtype=F32, nodes=nodes)
+    P.set_max_streams(g, 4)
+    b = Buffers((1 << 21) + 1, ["e", "b2"])
+    for call in range(5):
+        log(f"multi-stream replay call {call}")
+        x, y = b.fill(rng)
+        b.call(g)
+        a1 = -x
+        b1 = np.abs(y)
+        b2 = np.where(b1 > a1, b1, a1)
+        b.check({"b2": b2, "e": (np.abs(a1) + b2) - x * y}, f"call {call}")
+    assert P.streams_used(g) == 3
+    assert g.replayed_calls() == 3
+
+
+def test_call_inside_a_caller_capture():
+    torch = torch_mod()
+    rng = np.random.default_rng(26)
+    g = chain_graph()
+    b = Buffers(1 << 18, ["e", "c"])
+    x, y = b.fill(rng)
+    b.call(g)  # sizes the workspace and uploads the constants outside the capture
+    b.check(chain_expected(x, y), "warm-up")
+    tg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(tg):
+        b.call(g, torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        log(f"caller capture replay {rep}")
+        x, y = b.fill(rng)
+        tg.replay()
+        b.check(chain_expected(x, y), f"torch graph replay {rep}")
+    # unfused, the graph keeps a, b and d in its workspace: a larger call
+    # inside a capture would have to grow it, which is refused
+    g = chain_graph(fuse=False)
+    x, y = b.fill(rng)
+    b.call(g)
+    b.check(chain_expected(x, y), "unfused warm-up")
+    assert g.workspace_bytes() > 256
+    big = Buffers(1 << 20, ["e", "c"])
+    big.fill(rng)
+    tg2 = torch.cuda.CUDAGraph()
+    with pytest.raises(M.MFHError, match="must grow"):
+        with torch.cuda.graph(tg2):
+            big.call(g, torch.cuda.current_stream().cuda_stream)
