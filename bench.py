@@ -319,7 +319,8 @@ def load_traffic():
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("fp8_e4m3_to_bf16", {}).get("traffic_bytes_per_dispatch")
+        doc = json.load(f)
+    return doc.get("kernels", doc).get("fp8_e4m3_to_bf16", {}).get("traffic_bytes_per_dispatch")
 
 
 def main():

@@ -4,9 +4,10 @@
 // 16-byte output vector; item i of every thread sits next to item i of its
 // neighbours, so each store instruction of a wave writes 1 KiB contiguously
 // and each load instruction reads a contiguous span.  Threads take U items
-// per grid-stride step (loads first, then converts and stores).  A scalar
-// loop finishes the elements after the last whole item, and does all of them
-// when a pointer is not aligned for the vector path.
+// per step (loads first, then converts and stores): FP8 in one-shot chunks
+// per workgroup, the others in grid-stride loops.  A scalar loop finishes the
+// elements after the last whole item, and does all of them when a pointer is
+// not aligned for the vector path.
 //
 // FP8: the output for a code depends only on (code, format, scale), so each
 // workgroup first builds the 256-entry table in LDS with the exact rules of
@@ -46,48 +47,64 @@ MFH_DEV void store_one(void* out, mfh_i64 i, mfh_u32 enc)
 // ---------------------------------------------------------------------------
 
 // Item = 8 codes (16-bit output) or 4 codes (f32 output) -> one 16-byte store.
+// A block takes chunks of kBlock * U consecutive items (thread t holds items
+// t, t + kBlock, ...), so each store instruction of a wave writes 1 KiB
+// contiguously.  The grid normally has one block per chunk ("one-shot": no
+// block outlives its chunk, so the blocks sweep memory in dispatch order) and
+// loops only when there are more chunks than the largest grid.  A block
+// issues its first chunk's loads before building the table, so the load
+// latency covers the build; stores write through to memory (mfh_store_wt)
+// and leave no dirty L2 lines for the end-of-kernel writeback.  Measured at
+// [4096, 14336] on MI355X: +3% over a grid-stride loop at 6 blocks per CU.
 template <int OUT, int U>
 __global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict__ in,
                                                         void* __restrict__ out, mfh_i64 n,
                                                         float scale, int fmt, int vec_ok)
 {
     __shared__ mfh_u32 lut[256];
-    const mfh_u32 t = threadIdx.x;
-    {
-        mfh_u32 bits = fmt == kF8E4M3 ? mfh_e4m3_bits(t) : mfh_e5m2_bits(t);
-        lut[t] = encode_one<OUT>(mfh_scale_mul(mfh_f32(bits), scale));
-    }
-    __syncthreads();
-
     constexpr int kCodes = OUT == kFloat32 ? 4 : 8;
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    constexpr mfh_i64 kChunk = (mfh_i64)kBlock * U;
+    const mfh_u32 t = threadIdx.x;
     const mfh_i64 nitems = vec_ok ? n / kCodes : 0;
-    u32x4* dst = reinterpret_cast<u32x4*>(out);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + t; v < nitems; v += stride * U) {
-        u32x2 w[U];
+    const mfh_i64 nchunks = (nitems + kChunk - 1) / kChunk;
+    u32x2 w[U];
+    auto load = [&](mfh_i64 c) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            mfh_i64 i = v + u * stride;
+            const mfh_i64 i = c * kChunk + u * kBlock + t;
             if (i < nitems) {
                 if constexpr (kCodes == 8) w[u] = reinterpret_cast<const u32x2*>(in)[i];
                 else w[u] = u32x2{reinterpret_cast<const mfh_u32*>(in)[i], 0u};
             }
         }
+    };
+    mfh_i64 c = blockIdx.x;
+    if (c < nchunks) load(c);
+    {
+        mfh_u32 bits = fmt == kF8E4M3 ? mfh_e4m3_bits(t) : mfh_e5m2_bits(t);
+        lut[t] = encode_one<OUT>(mfh_scale_mul(mfh_f32(bits), scale));
+    }
+    __syncthreads();
+    for (; c < nchunks; c += gridDim.x) {
+        if (c != (mfh_i64)blockIdx.x) load(c);
+        const mfh_i64 first = c * kChunk;
+        const StreamOut dst(reinterpret_cast<u32x4*>(out) + first, nitems - first);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            mfh_i64 i = v + u * stride;
-            if (i >= nitems) break;
-            mfh_u32 x = w[u][0], y = w[u][1];
+            const int j = u * kBlock + (int)t;
+            if (first + j >= nitems) break;
+            const mfh_u32 x = w[u][0], y = w[u][1];
             if constexpr (OUT == kFloat32) {
-                dst[i] = u32x4{lut[x & 0xffu], lut[(x >> 8) & 0xffu], lut[(x >> 16) & 0xffu], lut[x >> 24]};
+                dst.store(j, u32x4{lut[x & 0xffu], lut[(x >> 8) & 0xffu], lut[(x >> 16) & 0xffu], lut[x >> 24]});
             } else {
-                dst[i] = u32x4{lut[x & 0xffu] | (lut[(x >> 8) & 0xffu] << 16),
-                               lut[(x >> 16) & 0xffu] | (lut[x >> 24] << 16),
-                               lut[y & 0xffu] | (lut[(y >> 8) & 0xffu] << 16),
-                               lut[(y >> 16) & 0xffu] | (lut[y >> 24] << 16)};
+                dst.store(j, u32x4{lut[x & 0xffu] | (lut[(x >> 8) & 0xffu] << 16),
+                                   lut[(x >> 16) & 0xffu] | (lut[x >> 24] << 16),
+                                   lut[y & 0xffu] | (lut[(y >> 8) & 0xffu] << 16),
+                                   lut[(y >> 16) & 0xffu] | (lut[y >> 24] << 16)});
             }
         }
     }
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
     for (mfh_i64 i = nitems * kCodes + (mfh_i64)blockIdx.x * kBlock + t; i < n; i += stride)
         store_one<OUT>(out, i, lut[in[i]]);
 }

@@ -33,6 +33,8 @@ namespace mfh {
 namespace {
 
 constexpr int kBlockThreads = 256;
+// Blocks per CU that make every grid one-shot (capped by the work itself).
+constexpr int kOneShotBlocksPerCu = 1 << 16;
 
 const char* io_suffix(int dtype)
 {
@@ -300,24 +302,14 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     for (int k = 0; k < n_inputs; k++)
         if (inputs[k].mode == MFH_OPERAND_PERIODIC && inputs[k].period % vec != 0) periods_vectorizable = false;
 
-    // Launch shape from the chain's VALU cost per element (instruction slots,
-    // quarter-rate ops counted four times): a memory-bound chain wants two
-    // items per thread and few workgroups (writes in flight, not occupancy);
-    // a VALU-bound one wants one item and high occupancy to cover latency.
-    // Measured on MI355X with the SwiGLU (~35 slots) and f16 gelu (~45) chains.
-    int cost = 0;
-    for (const mfh_ast_node& nd : list) {
-        switch (nd.type) {
-        case kNodeGelu: cost += 40; break;
-        case kNodeSilu: case kNodeSigmoid: cost += 30; break;
-        case kNodeExp: case kNodeLog: case kNodeTanh: cost += 60; break;
-        case kNodeDiv: case kNodeSqrt: cost += 10; break;
-        default: cost += 1; break;
-        }
-    }
-    const bool heavy = cost > 8;
-    const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : (heavy ? 1 : 2);
-    const int auto_bpc = cost > 38 ? 24 : 4;
+    // Launch shape: one item per thread and a one-shot grid (one block per
+    // 256 items, so each block streams one chunk and exits and the blocks
+    // sweep memory in dispatch order).  Measured on MI355X against
+    // grid-stride loops at 4-24 blocks per CU: +11% on the SwiGLU chain and
+    // +9% on the f16 gelu chain; a no-compute 2:1 read:write stream gains
+    // 17% the same way.  mfh_set_launch_config("fused", ...) overrides both.
+    const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : 1;
+    const int auto_bpc = kOneShotBlocksPerCu;
 
     const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
     // Element loop: every operand decoded to f32.  Vector loop: f16 operands
@@ -441,7 +433,7 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
     int64_t items = nvec > 0 ? (nvec + kernel->unroll - 1) / kernel->unroll : count;
     int64_t need = (items + kBlockThreads - 1) / kBlockThreads;
     int bpc = blocks_per_cu(Kern::kFused) > 0 ? blocks_per_cu(Kern::kFused) : kernel->auto_bpc;
-    int64_t cap = (int64_t)dev->compute_units * bpc;
+    int64_t cap = std::min<int64_t>((int64_t)dev->compute_units * bpc, (int64_t(1) << 32) / kBlockThreads - 1);
     unsigned grid = (unsigned)std::max<int64_t>(1, std::min(need, cap));
     std::vector<const void*> ptrs(inputs, inputs + n_inputs);
     std::vector<void*> args;

@@ -21,6 +21,8 @@ typedef mfh_u32 u32x4 __attribute__((ext_vector_type(4)));
 typedef mfh_u32 u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBlock = 256;  // 4 wave64 per workgroup
+// A dispatch counts its work-items in 32 bits: grids stay below 2^32 / kBlock.
+constexpr int64_t kMaxGrid = (int64_t(1) << 32) / kBlock - 1;
 
 // Grid for `items` work items of `per_thread` items each, capped at
 // compute_units * blocks_per_cu(k); threads loop over the rest.
@@ -28,11 +30,32 @@ inline unsigned grid_for(int64_t items, const Device* dev, Kern k, int per_threa
 {
     int64_t threads = (items + per_thread - 1) / per_thread;
     int64_t need = (threads + kBlock - 1) / kBlock;
-    int64_t cap = (int64_t)dev->compute_units * blocks_per_cu(k);
+    int64_t cap = std::min<int64_t>((int64_t)dev->compute_units * blocks_per_cu(k), kMaxGrid);
     return (unsigned)std::max<int64_t>(1, std::min(need, cap));
 }
 
 int launch_status(const char* what);
+
+// 16-byte stores of a chunk that write through to memory: buffer stores with
+// the sc1 (system scope) cache policy, addressed from the chunk's first item
+// (the base is uniform across the block, so the descriptor lives in SGPRs).
+// The descriptor's record count is the chunk's remaining bytes, so the
+// hardware drops anything past the end of the output.
+struct StreamOut {
+    __amdgpu_buffer_rsrc_t rsrc;
+    __device__ StreamOut(u32x4* base, int64_t items_left)
+        : rsrc(__builtin_amdgcn_make_buffer_rsrc(
+              base, 0, (int)std::min<int64_t>(items_left * 16, 0x7fffffff), kBufferConfig))
+    {
+    }
+    __device__ void store(int item, u32x4 v) const
+    {
+        __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, item * 16, 0, kCachePolicySc1);
+    }
+    // Word 3 of a raw (untyped) gfx9 buffer descriptor.
+    static constexpr int kBufferConfig = 0x00020000;
+    static constexpr int kCachePolicySc1 = 16;
+};
 
 }  // namespace mfh
 

@@ -156,12 +156,16 @@ struct LaunchCfg {
     std::atomic<int> bpc;
     std::atomic<int> unroll;  // 0: the kernel family chooses (fused: by chain cost)
 };
-// Defaults measured on MI355X (256 CUs): the write-heavy streams run best
-// with a few MB of stores in flight, well below full occupancy.  0 for the
-// fused family means "per kernel": each generated kernel carries a shape
-// chosen from its estimated VALU cost (see fusion.cpp).
+// Large enough that every thread runs exactly one step at any size that
+// fits in HBM (the grid is also capped by the work itself): "one-shot"
+// grids, whose blocks each stream one chunk and exit.
+constexpr int kMaxBlocksPerCu = 1 << 16;
+// Defaults measured on MI355X (256 CUs).  FP8 runs one-shot (two items per
+// thread); the Int4 and axpy grid-stride loops run best with a few MB of
+// stores in flight, well below full occupancy.  0 for the fused family means
+// "per kernel": each generated kernel carries its shape (see fusion.cpp).
 LaunchCfg g_cfg[(int)Kern::kCount] = {
-    {"fp8", {6}, {1}}, {"int4", {6}, {1}}, {"axpy", {2}, {1}},
+    {"fp8", {kMaxBlocksPerCu}, {2}}, {"int4", {6}, {1}}, {"axpy", {2}, {1}},
     {"axpy16", {2}, {1}}, {"convert", {4}, {1}}, {"fused", {0}, {0}},
 };
 std::once_flag g_cfg_env_once;
@@ -175,7 +179,7 @@ void read_cfg_env()
         const char* bpc = std::getenv(("MFH_BPC_" + upper).c_str());
         if (!bpc) bpc = all;
         const char* un = std::getenv(("MFH_UNROLL_" + upper).c_str());
-        if (bpc && atoi(bpc) > 0 && atoi(bpc) <= 64) c.bpc = atoi(bpc);
+        if (bpc && atoi(bpc) > 0 && atoi(bpc) <= kMaxBlocksPerCu) c.bpc = atoi(bpc);
         if (un && (atoi(un) == 1 || atoi(un) == 2 || atoi(un) == 4)) c.unroll = atoi(un);
     }
 }
@@ -261,7 +265,8 @@ int mfh_set_launch_config(const char* kernel, int32_t blocks_per_cu, int32_t ite
 {
     LaunchCfg* c = find_cfg(kernel);
     if (!c) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: unknown kernel family \"%s\"", kernel ? kernel : "(null)");
-    if (blocks_per_cu > 64) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: blocks_per_cu %d > 64", blocks_per_cu);
+    if (blocks_per_cu > kMaxBlocksPerCu)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: blocks_per_cu %d > %d", blocks_per_cu, kMaxBlocksPerCu);
     if (items_per_thread > 0 && items_per_thread != 1 && items_per_thread != 2 && items_per_thread != 4)
         return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: items_per_thread must be 1, 2 or 4");
     if (blocks_per_cu > 0) c->bpc = blocks_per_cu;

@@ -79,7 +79,7 @@ def test_emit_hip_broadcast_operands():
 def test_emit_hip_item_width_follows_the_widest_operand():
     relu_add = flatten((N_RELU, (N_ADD, ("in", 0), ("in", 1))))
     k16 = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT16, M.OPERAND_FULL, 0)], M.BFLOAT16, "a")
-    assert "mfh_ld8_bf16(p0" in k16.source and "8 elements per item, 2 item(s)" in k16.source
+    assert "mfh_ld8_bf16(p0" in k16.source and "8 elements per item, 1 item(s)" in k16.source
     k32 = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_FULL, 0)], M.BFLOAT16, "b")
     assert "mfh_ld4_bf16(p0" in k32.source and "mfh_ld4_f32(p1" in k32.source and "mfh_st4_bf16(pout" in k32.source
     # a scalar f32 operand does not narrow the item
