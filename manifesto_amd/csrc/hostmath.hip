@@ -2,7 +2,8 @@
 // scalar broadcast and linspace (runtime/executor_math.go).
 //
 // axpy moves 12 bytes per f32 element (read x, read y, write y) and does two
-// flops, so it is an HBM stream: 16-byte vectors in a grid-stride loop.  The
+// flops, so it is an HBM stream: 16-byte vectors in a grid-stride loop, with
+// non-temporal stores (y is streamed out, not re-read).  The
 // product is rounded before the add (the library is built with
 // -ffp-contract=off), as the Go loop at runtime/axpy.go:115-117 computes it.
 #include "launch.hpp"
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, cons
             u32x4 o;
 #pragma unroll
             for (int k = 0; k < 4; k++) o[k] = mfh_bits(axpy_step(mfh_f32(b[u][k]), mfh_f32(a[u][k]), alpha));
-            yv[i] = o;
+            store_nt(&yv[i], o);
         }
     }
     for (mfh_i64 i = nvec * 4 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(kBlock) void k_axpy16(mfh_u16* __restrict__ y, cons
                 float hi = axpy_step(dec16<DT>(b[u][k] >> 16), dec16<DT>(a[u][k] >> 16), alpha);
                 o[k] = enc16x2<DT>(lo, hi);
             }
-            yv[i] = o;
+            store_nt(&yv[i], o);
         }
     }
     for (mfh_i64 i = nvec * 8 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
