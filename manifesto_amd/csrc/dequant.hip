@@ -242,7 +242,7 @@ __global__ __launch_bounds__(kBlock) void k_convert16_vec(const void* __restrict
             store_nt(&dst[v], u32x4{mfh_bits(dec16<IN>(w[0] & 0xffffu)), mfh_bits(dec16<IN>(w[0] >> 16)),
                                     mfh_bits(dec16<IN>(w[1] & 0xffffu)), mfh_bits(dec16<IN>(w[1] >> 16))});
         } else {
-            u32x4 w = reinterpret_cast<const u32x4*>(in)[v];
+            u32x4 w = load_nt(reinterpret_cast<const u32x4*>(in) + v);
             u32x4 o;
 #pragma unroll
             for (int k = 0; k < 4; k++) o[k] = encode_pair<OUT>(dec16<IN>(w[k] & 0xffffu), dec16<IN>(w[k] >> 16));
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(kBlock) void k_narrow_f32_vec(const u32x4* __restri
 {
     const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
     for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
-        u32x4 a = in[v];
+        u32x4 a = load_nt(in + v);
         store_nt(&out[v], u32x2{encode_pair<OUT>(mfh_f32(a[0]), mfh_f32(a[1])),
                                 encode_pair<OUT>(mfh_f32(a[2]), mfh_f32(a[3]))});
     }
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ 
             const u32x4* src = reinterpret_cast<const u32x4*>(in) + v * 4;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                u32x4 w = src[q];
+                u32x4 w = load_nt(src + q);
 #pragma unroll
                 for (int k = 0; k < 4; k++) f[4 * q + k] = mfh_f32(w[k]);
             }
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ 
             const u32x4* src = reinterpret_cast<const u32x4*>(in) + v * 2;
 #pragma unroll
             for (int q = 0; q < 2; q++) {
-                u32x4 w = src[q];
+                u32x4 w = load_nt(src + q);
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     f[8 * q + 2 * k] = dec16<IN>(w[k] & 0xffffu);

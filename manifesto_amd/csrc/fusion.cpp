@@ -310,6 +310,12 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // 17% the same way.  mfh_set_launch_config("fused", ...) overrides both.
     const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
+    // Non-temporal loads for the streamed (full-length) operands when the
+    // kernel reads at least as many bytes per element as it writes.
+    int read_bytes = 0;
+    for (int k = 0; k < n_inputs; k++)
+        if (inputs[k].mode == MFH_OPERAND_FULL) read_bytes += inputs[k].dtype == kFloat32 ? 4 : 2;
+    const bool stream_loads = read_bytes >= (out_dtype == kFloat32 ? 4 : 2);
 
     const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
     // Element loop: every operand decoded to f32.  Vector loop: f16 operands
@@ -331,7 +337,8 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     src.reserve(sizeof(kPrelude) + 4096);
     src += kPrelude;
     src += "\n// EmitHIP: fusion '" + identifier + "'" + (precise ? " (precise transcendentals)" : "") +
-           ", " + V + " elements per item, " + U + " item(s) per thread per step\n";
+           ", " + V + " elements per item, " + U + " item(s) per thread per step" +
+           (stream_loads ? ", streamed loads" : "") + "\n";
     src += "extern \"C\" __global__ __launch_bounds__(256) void " + kernel_name + "(\n";
     for (int k = 0; k < n_inputs; k++) src += "    const void* __restrict__ p" + std::to_string(k) + ",\n";
     src += "    void* __restrict__ pout, mfh_i64 n, mfh_i64 nvec)\n{\n";
@@ -354,11 +361,12 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     for (int k = 0; k < n_inputs; k++) {
         if (inputs[k].mode == MFH_OPERAND_SCALAR) continue;
         std::string ks = std::to_string(k);
+        const std::string nt = stream_loads && inputs[k].mode == MFH_OPERAND_FULL ? "<1>" : "";
         if (packed16[k])
-            src += "                mfh_ldw" + V + "_f16(p" + ks + ", " + operand_index(inputs[k], "e0") + ", w" + ks +
-                   "[u]);\n";
+            src += "                mfh_ldw" + V + "_f16" + nt + "(p" + ks + ", " + operand_index(inputs[k], "e0") +
+                   ", w" + ks + "[u]);\n";
         else
-            src += "                mfh_ld" + V + "_" + io_suffix(inputs[k].dtype) + "(p" + ks + ", " +
+            src += "                mfh_ld" + V + "_" + io_suffix(inputs[k].dtype) + nt + "(p" + ks + ", " +
                    operand_index(inputs[k], "e0") + ", a" + ks + "[u]);\n";
     }
     src += "            }\n        }\n";

@@ -15,11 +15,23 @@
 typedef mfh_u32 mfh_u32x4 __attribute__((ext_vector_type(4)));
 typedef mfh_u32 mfh_u32x2 __attribute__((ext_vector_type(2)));
 
+// Vector loads take NT = 1 for a streamed operand of a kernel that reads at
+// least as many bytes as it writes (non-temporal loads measured +4% on a 1:1
+// stream and +8% on 2:1, but -10% on 1:2); operands re-read across the grid
+// (periodic rows such as a bias) keep NT = 0.
+template <int NT, typename T>
+MFH_DEV T mfh_vld(const void* p)
+{
+    if constexpr (NT) return __builtin_nontemporal_load(static_cast<const T*>(p));
+    else return *static_cast<const T*>(p);
+}
+
 // ---- 8-element items (16-bit operands) ----
 
+template <int NT = 0>
 MFH_DEV void mfh_ld8_bf16(const void* p, mfh_i64 e, float* a)
 {
-    mfh_u32x4 x = *reinterpret_cast<const mfh_u32x4*>(static_cast<const mfh_u16*>(p) + e);
+    mfh_u32x4 x = mfh_vld<NT, mfh_u32x4>(static_cast<const mfh_u16*>(p) + e);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         a[2 * k] = mfh_f32(x[k] << 16);
@@ -27,9 +39,10 @@ MFH_DEV void mfh_ld8_bf16(const void* p, mfh_i64 e, float* a)
     }
 }
 
+template <int NT = 0>
 MFH_DEV void mfh_ld8_f16(const void* p, mfh_i64 e, float* a)
 {
-    mfh_u32x4 x = *reinterpret_cast<const mfh_u32x4*>(static_cast<const mfh_u16*>(p) + e);
+    mfh_u32x4 x = mfh_vld<NT, mfh_u32x4>(static_cast<const mfh_u16*>(p) + e);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         a[2 * k] = mfh_f16_to_f32(x[k] & 0xffffu);
@@ -53,16 +66,18 @@ MFH_DEV void mfh_st8_f16(void* p, mfh_i64 e, const float* r)
 
 // ---- 4-element items (some operand is f32) ----
 
+template <int NT = 0>
 MFH_DEV void mfh_ld4_f32(const void* p, mfh_i64 e, float* a)
 {
-    mfh_u32x4 x = *reinterpret_cast<const mfh_u32x4*>(static_cast<const float*>(p) + e);
+    mfh_u32x4 x = mfh_vld<NT, mfh_u32x4>(static_cast<const float*>(p) + e);
 #pragma unroll
     for (int k = 0; k < 4; k++) a[k] = mfh_f32(x[k]);
 }
 
+template <int NT = 0>
 MFH_DEV void mfh_ld4_bf16(const void* p, mfh_i64 e, float* a)
 {
-    mfh_u32x2 x = *reinterpret_cast<const mfh_u32x2*>(static_cast<const mfh_u16*>(p) + e);
+    mfh_u32x2 x = mfh_vld<NT, mfh_u32x2>(static_cast<const mfh_u16*>(p) + e);
 #pragma unroll
     for (int k = 0; k < 2; k++) {
         a[2 * k] = mfh_f32(x[k] << 16);
@@ -70,9 +85,10 @@ MFH_DEV void mfh_ld4_bf16(const void* p, mfh_i64 e, float* a)
     }
 }
 
+template <int NT = 0>
 MFH_DEV void mfh_ld4_f16(const void* p, mfh_i64 e, float* a)
 {
-    mfh_u32x2 x = *reinterpret_cast<const mfh_u32x2*>(static_cast<const mfh_u16*>(p) + e);
+    mfh_u32x2 x = mfh_vld<NT, mfh_u32x2>(static_cast<const mfh_u16*>(p) + e);
 #pragma unroll
     for (int k = 0; k < 2; k++) {
         a[2 * k] = mfh_f16_to_f32(x[k] & 0xffffu);
@@ -107,16 +123,18 @@ MFH_DEV void mfh_st4_f16(void* p, mfh_i64 e, const float* r)
 // same f32 sum as converting first and adding, in one instruction instead of
 // two or three.
 
+template <int NT = 0>
 MFH_DEV void mfh_ldw8_f16(const void* p, mfh_i64 e, mfh_u32* w)
 {
-    mfh_u32x4 x = *reinterpret_cast<const mfh_u32x4*>(static_cast<const mfh_u16*>(p) + e);
+    mfh_u32x4 x = mfh_vld<NT, mfh_u32x4>(static_cast<const mfh_u16*>(p) + e);
 #pragma unroll
     for (int k = 0; k < 4; k++) w[k] = x[k];
 }
 
+template <int NT = 0>
 MFH_DEV void mfh_ldw4_f16(const void* p, mfh_i64 e, mfh_u32* w)
 {
-    mfh_u32x2 x = *reinterpret_cast<const mfh_u32x2*>(static_cast<const mfh_u16*>(p) + e);
+    mfh_u32x2 x = mfh_vld<NT, mfh_u32x2>(static_cast<const mfh_u16*>(p) + e);
     w[0] = x[0];
     w[1] = x[1];
 }

@@ -2,8 +2,8 @@
 // scalar broadcast and linspace (runtime/executor_math.go).
 //
 // axpy moves 12 bytes per f32 element (read x, read y, write y) and does two
-// flops, so it is an HBM stream: 16-byte vectors in a grid-stride loop, with
-// non-temporal stores (y is streamed out, not re-read).  The
+// flops, so it is an HBM stream: 16-byte vectors, one-shot grid by default, with
+// non-temporal loads and stores (each byte is touched once).  The
 // product is rounded before the add (the library is built with
 // -ffp-contract=off), as the Go loop at runtime/axpy.go:115-117 computes it.
 #include "launch.hpp"
@@ -44,8 +44,8 @@ __global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, cons
         for (int u = 0; u < U; u++) {
             mfh_i64 i = v + u * stride;
             if (i < nvec) {
-                a[u] = xv[i];
-                b[u] = yv[i];
+                a[u] = load_nt(&xv[i]);
+                b[u] = load_nt(&yv[i]);
             }
         }
 #pragma unroll
@@ -78,8 +78,8 @@ __global__ __launch_bounds__(kBlock) void k_axpy16(mfh_u16* __restrict__ y, cons
         for (int u = 0; u < U; u++) {
             mfh_i64 i = v + u * stride;
             if (i < nvec) {
-                a[u] = xv[i];
-                b[u] = yv[i];
+                a[u] = load_nt(&xv[i]);
+                b[u] = load_nt(&yv[i]);
             }
         }
 #pragma unroll

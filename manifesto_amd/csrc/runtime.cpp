@@ -160,13 +160,13 @@ struct LaunchCfg {
 // fits in HBM (the grid is also capped by the work itself): "one-shot"
 // grids, whose blocks each stream one chunk and exit.
 constexpr int kMaxBlocksPerCu = 1 << 16;
-// Defaults measured on MI355X (256 CUs).  FP8 and Int4 run one-shot with two
-// items per thread; the axpy grid-stride loop runs best with a few MB of
-// stores in flight, well below full occupancy.  0 for the fused family means
-// "per kernel": each generated kernel carries its shape (see fusion.cpp).
+// Defaults measured on MI355X (256 CUs) with streaming loads and stores:
+// every family runs one-shot, FP8 and Int4 with two items per thread, axpy
+// and the casts with one.  0 for the fused family means "per kernel": each
+// generated kernel carries its shape (see fusion.cpp).
 LaunchCfg g_cfg[(int)Kern::kCount] = {
-    {"fp8", {kMaxBlocksPerCu}, {2}}, {"int4", {kMaxBlocksPerCu}, {2}}, {"axpy", {2}, {1}},
-    {"axpy16", {2}, {1}}, {"convert", {4}, {1}}, {"fused", {0}, {0}},
+    {"fp8", {kMaxBlocksPerCu}, {2}}, {"int4", {kMaxBlocksPerCu}, {2}}, {"axpy", {kMaxBlocksPerCu}, {1}},
+    {"axpy16", {kMaxBlocksPerCu}, {1}}, {"convert", {kMaxBlocksPerCu}, {1}}, {"fused", {0}, {0}},
 };
 std::once_flag g_cfg_env_once;
 

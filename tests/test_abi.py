@@ -53,7 +53,9 @@ def test_emit_hip_swiglu_source_shape():
     src = k.source
     assert k.kernel_name == "fused_mlp_swiglu_out"  # like metalKernelName (codegen/metal.go:281-290)
     assert f'void {k.kernel_name}(' in src
-    assert "mfh_ld8_bf16(p0, e0, a0[u])" in src and "mfh_ld8_bf16(p1, e0, a1[u])" in src
+    # reads 4 B per element, writes 2: streamed (non-temporal) loads
+    assert "mfh_ld8_bf16<1>(p0, e0, a0[u])" in src and "mfh_ld8_bf16<1>(p1, e0, a1[u])" in src
+    assert "streamed loads" in src
     assert "mfh_silu(x0)" in src and "mfh_st8_bf16(pout, it * 8, r)" in src
     assert src.count("for (mfh_i64 i = nvec * 8 + tid; i < n; i += stride)") == 1
 
@@ -66,7 +68,8 @@ def test_emit_hip_broadcast_operands():
     k = M.FusedKernel(nodes, ops, M.FLOAT16, "chain")
     src = k.source
     # f16 operands stay packed in the vector loop; adds take them directly
-    assert "mfh_ldw8_f16(p1, (e0 % 4096LL), w1[u])" in src
+    # the periodic bias is re-read across the grid: a cached load; x streams
+    assert "mfh_ldw8_f16(p1, (e0 % 4096LL), w1[u])" in src and "mfh_ldw8_f16<1>(p0, e0, w0[u])" in src
     assert "mfh_add_hh(w0[u][j >> 1], j & 1, w1[u][j >> 1], j & 1)" in src
     assert "mfh_add_fh(t2, w3[u][j >> 1], j & 1)" in src
     assert "const float x1 = mfh_ld1_f16(p1, (i % 4096LL));" in src  # element loop decodes
@@ -79,12 +82,15 @@ def test_emit_hip_broadcast_operands():
 def test_emit_hip_item_width_follows_the_widest_operand():
     relu_add = flatten((N_RELU, (N_ADD, ("in", 0), ("in", 1))))
     k16 = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT16, M.OPERAND_FULL, 0)], M.BFLOAT16, "a")
-    assert "mfh_ld8_bf16(p0" in k16.source and "8 elements per item, 1 item(s)" in k16.source
+    assert "mfh_ld8_bf16<1>(p0" in k16.source and "8 elements per item, 1 item(s)" in k16.source
     k32 = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_FULL, 0)], M.BFLOAT16, "b")
-    assert "mfh_ld4_bf16(p0" in k32.source and "mfh_ld4_f32(p1" in k32.source and "mfh_st4_bf16(pout" in k32.source
+    assert "mfh_ld4_bf16<1>(p0" in k32.source and "mfh_ld4_f32<1>(p1" in k32.source and "mfh_st4_bf16(pout" in k32.source
     # a scalar f32 operand does not narrow the item
     ks = M.FusedKernel(relu_add, [(M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_SCALAR, 0)], M.BFLOAT16, "c")
-    assert "mfh_ld8_bf16(p0" in ks.source
+    assert "mfh_ld8_bf16<1>(p0" in ks.source
+    # a kernel that writes more than it reads keeps cached loads
+    widen = M.FusedKernel(flatten((N_RELU, ("in", 0))), [(M.BFLOAT16, M.OPERAND_FULL, 0)], M.FLOAT32, "w")
+    assert "mfh_ld4_bf16(p0" in widen.source and "streamed loads" not in widen.source
 
 
 def test_emit_hip_constants_are_rounded_to_f32():

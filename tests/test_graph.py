@@ -499,7 +499,7 @@ def test_attach_kernels_uses_port_types():
     G.run(graph)
     assert G.attach_kernels(graph, flags=M.FUSION_PRECISE) == 1
     src = graph.nodes[1].attributes[G.KERNEL_ATTRIBUTE].For(G.TARGET_HIP).source()
-    assert "mfh_ldw4_f16(p0" in src and "mfh_ld4_f32(p2" in src and "mfh_st4_f16(pout" in src
+    assert "mfh_ldw4_f16<1>(p0" in src and "mfh_ld4_f32<1>(p2" in src and "mfh_st4_f16(pout" in src
     assert "precise transcendentals" in src
 
 
