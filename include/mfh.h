@@ -78,11 +78,14 @@ int mfh_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int mfh_stream_sync(void* stream);
 
 /* Launch shape of one family of streaming kernels: workgroups per compute
- * unit for its grid-stride loop and work items per thread per step (1, 2 or
- * 4).  `kernel` is "fp8", "int4", "axpy", "axpy16", "convert" or "fused"; a
- * value <= 0 keeps the current setting.  Defaults are measured on MI355X and
- * can also be set with MFH_BPC_<KERNEL> / MFH_UNROLL_<KERNEL>.  A deployment
- * knob with no counterpart in the reference; results do not depend on it. */
+ * unit (the grid is also capped by the work itself, so a large value gives a
+ * one-shot grid, one workgroup per chunk) and work items per thread per step
+ * (1, 2 or 4).  `kernel` is "fp8", "int4", "axpy", "axpy16", "convert" or
+ * "fused"; 0 keeps the current setting and -1 restores the default.  Defaults
+ * are measured on MI355X and can also be set with MFH_BPC_<KERNEL> /
+ * MFH_UNROLL_<KERNEL>.  For "fused" the items per thread apply to kernels
+ * compiled afterwards.  A deployment knob with no counterpart in the
+ * reference; results do not depend on it. */
 int mfh_set_launch_config(const char* kernel, int32_t blocks_per_cu, int32_t items_per_thread);
 int mfh_get_launch_config(const char* kernel, int32_t* blocks_per_cu, int32_t* items_per_thread);
 

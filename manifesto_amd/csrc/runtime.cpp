@@ -154,7 +154,8 @@ namespace {
 struct LaunchCfg {
     const char* name;
     std::atomic<int> bpc;
-    std::atomic<int> unroll;  // 0: the kernel family chooses (fused: by chain cost)
+    std::atomic<int> unroll;  // 0: the kernel family chooses (fused: per kernel)
+    int default_bpc = 0, default_unroll = 0;  // filled from the initial values
 };
 // Large enough that every thread runs exactly one step at any size that
 // fits in HBM (the grid is also capped by the work itself): "one-shot"
@@ -172,6 +173,10 @@ std::once_flag g_cfg_env_once;
 
 void read_cfg_env()
 {
+    for (auto& c : g_cfg) {
+        c.default_bpc = c.bpc.load();
+        c.default_unroll = c.unroll.load();
+    }
     const char* all = std::getenv("MFH_BLOCKS_PER_CU");
     for (auto& c : g_cfg) {
         std::string upper(c.name);
@@ -265,12 +270,16 @@ int mfh_set_launch_config(const char* kernel, int32_t blocks_per_cu, int32_t ite
 {
     LaunchCfg* c = find_cfg(kernel);
     if (!c) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: unknown kernel family \"%s\"", kernel ? kernel : "(null)");
-    if (blocks_per_cu > kMaxBlocksPerCu)
-        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: blocks_per_cu %d > %d", blocks_per_cu, kMaxBlocksPerCu);
-    if (items_per_thread > 0 && items_per_thread != 1 && items_per_thread != 2 && items_per_thread != 4)
-        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: items_per_thread must be 1, 2 or 4");
+    if (blocks_per_cu > kMaxBlocksPerCu || blocks_per_cu < -1)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: blocks_per_cu %d is not in -1..%d", blocks_per_cu,
+                    kMaxBlocksPerCu);
+    if (items_per_thread < -1 || (items_per_thread > 0 && items_per_thread != 1 && items_per_thread != 2 &&
+                                  items_per_thread != 4))
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_config: items_per_thread must be 1, 2 or 4 (or 0, -1)");
     if (blocks_per_cu > 0) c->bpc = blocks_per_cu;
+    else if (blocks_per_cu == -1) c->bpc = c->default_bpc;
     if (items_per_thread > 0) c->unroll = items_per_thread;
+    else if (items_per_thread == -1) c->unroll = c->default_unroll;
     return MFH_OK;
 }
 

@@ -175,3 +175,19 @@ def test_backend_open_without_a_device_fails_loudly():
         pytest.skip("a GPU is present; the backend is covered by the GPU tests")
     with pytest.raises(M.MFHError):
         Backend(0)
+
+
+def test_launch_config_set_keep_and_restore():
+    default = M.get_launch_config("fp8")
+    M.set_launch_config("fp8", 7, 4)
+    assert M.get_launch_config("fp8") == (7, 4)
+    M.set_launch_config("fp8", 0, 0)  # 0 keeps
+    assert M.get_launch_config("fp8") == (7, 4)
+    M.set_launch_config("fp8", -1, -1)  # -1 restores the default
+    assert M.get_launch_config("fp8") == default
+    with pytest.raises(M.MFHError):
+        M.set_launch_config("fp8", -2, 0)
+    with pytest.raises(M.MFHError):
+        M.set_launch_config("fp8", 0, 3)
+    with pytest.raises(M.MFHError):
+        M.set_launch_config("nope", 1, 1)
