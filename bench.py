@@ -9,7 +9,8 @@ timed steps are replayed from a captured HIP graph so the clock sees kernel
 time, not Python launch overhead.  The other BASELINE configs (axpy, SwiGLU,
 the f16 gelu chain, Int4) are measured the same way and listed under
 "configs".  The CPU baseline is the oracle (a C restatement of the Go loops,
--O2 -ffp-contract=off) timed on this host, single-threaded.
+-O2 -ffp-contract=off) timed on this host, single-threaded as the Go loops
+run; "cpu_baseline_all_cores" splits the same sample over the host's threads.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only N]
 """
@@ -85,8 +86,10 @@ class Axpy(Workload):
         x = rng.uniform(-1, 1, self.n).astype(np.float32)
         y = rng.uniform(-1, 1, self.n).astype(np.float32)
         O = self.O
-        return self.n, lambda: O.lib().orc_axpy_f32(y.ctypes.data, x.ctypes.data, self.n, 0.75), \
-            "the full N=2^24 f32 axpy (runtime/axpy.go:115-117 loop)"
+
+        def part(lo, hi):
+            O.lib().orc_axpy_f32(y.ctypes.data + 4 * lo, x.ctypes.data + 4 * lo, hi - lo, 0.75)
+        return self.n, 1, part, "the full N=2^24 f32 axpy (runtime/axpy.go:115-117 loop)"
 
 
 class Fp8(Workload):
@@ -110,9 +113,11 @@ class Fp8(Workload):
         codes = rng.integers(0, 256, self.n, dtype=np.uint8)
         out = np.empty(self.n, dtype=np.uint16)
         O = self.O
-        return self.n, lambda: O.lib().orc_dequant_fp8(codes.ctypes.data, self.n, O.F8E4M3, 0.0125,
-                                                       O.BFLOAT16, out.ctypes.data), \
-            "the full [4096,14336] tensor: BytesToFloat32 pass + scale + RNE narrowing pass"
+
+        def part(lo, hi):
+            O.lib().orc_dequant_fp8(codes.ctypes.data + lo, hi - lo, O.F8E4M3, 0.0125, O.BFLOAT16,
+                                    out.ctypes.data + 2 * lo)
+        return self.n, 1, part, "the full [4096,14336] tensor: BytesToFloat32 pass + scale + RNE narrowing pass"
 
 
 class SwiGLU(Workload):
@@ -146,10 +151,10 @@ class SwiGLU(Workload):
         u = O.f32_to_bf16(rng.standard_normal(m, dtype=np.float32))
         nodes = self.nodes
 
-        def run():  # shape.cast to f32, CPUKernel.Run, narrow to bf16
-            out = O.run(nodes, [O.decode(g, O.BFLOAT16), O.decode(u, O.BFLOAT16)], m)
+        def part(lo, hi):  # shape.cast to f32, CPUKernel.Run, narrow to bf16
+            out = O.run(nodes, [O.decode(g[lo:hi], O.BFLOAT16), O.decode(u[lo:hi], O.BFLOAT16)], hi - lo)
             O.f32_to_bf16(out)
-        return m, run, "2^22 elements of the same chain: bf16->f32 casts, CPUKernel.Run, f32->bf16"
+        return m, 1, part, "2^22 elements of the same chain: bf16->f32 casts, CPUKernel.Run, f32->bf16"
 
 
 class GeluChain(Workload):
@@ -191,10 +196,11 @@ class GeluChain(Workload):
         s = np.array([1.1], np.float32)
         nodes = self.nodes
 
-        def run():
-            out = O.run(nodes, [O.decode(x, O.FLOAT16), b, s, O.decode(r, O.FLOAT16)], m, [0, 4096, 1, 0])
+        def part(lo, hi):  # lo is a multiple of the 4096-element bias period
+            out = O.run(nodes, [O.decode(x[lo:hi], O.FLOAT16), b, s, O.decode(r[lo:hi], O.FLOAT16)], hi - lo,
+                        [0, 4096, 1, 0])
             O.f32_to_f16(out)
-        return m, run, "2^22 elements of the same chain: f16->f32 casts, CPUKernel.Run, f32->f16"
+        return m, 4096, part, "2^22 elements of the same chain: f16->f32 casts, CPUKernel.Run, f32->f16"
 
 
 class Int4(Workload):
@@ -222,9 +228,11 @@ class Int4(Workload):
         packed = rng.integers(0, 256, self.n // 2, dtype=np.uint8)
         scales = O.f32_to_f16(rng.uniform(0.005, 0.02, self.n // 128).astype(np.float32))
         out = np.empty(self.n, dtype=np.uint16)
-        return self.n, lambda: O.lib().orc_dequant_int4(packed.ctypes.data, self.n, scales.ctypes.data,
-                                                        O.FLOAT16, 128, O.BFLOAT16, out.ctypes.data), \
-            "the full [14336,4096] tensor: f64 nibble decode pass + scale + RNE narrowing pass"
+
+        def part(lo, hi):  # lo is a multiple of the 128-element group
+            O.lib().orc_dequant_int4(packed.ctypes.data + lo // 2, hi - lo, scales.ctypes.data + 2 * (lo // 128),
+                                     O.FLOAT16, 128, O.BFLOAT16, out.ctypes.data + 2 * lo)
+        return self.n, 128, part, "the full [14336,4096] tensor: f64 nibble decode pass + scale + RNE narrowing pass"
 
 
 WORKLOADS = [Axpy, Fp8, SwiGLU, GeluChain, Int4]
@@ -273,8 +281,43 @@ def time_gpu(w, steps, warmup, use_graph=True):
     return ms, n, wall
 
 
-def time_cpu(w, budget_s=3.0):
-    m, fn, what = w.cpu_sample()
+def cpu_threads():
+    """Host threads for the all-core baseline: this process's CPU affinity,
+    capped by OMP_NUM_THREADS when set (16 on the GPU boxes)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_cpu(w, budget_s=3.0, threads=1):
+    """Times the oracle's restatement of the reference loop over the sample:
+    one thread (the reference's loops are serial) or `threads` threads over
+    disjoint ranges of it (ctypes releases the GIL around each C call)."""
+    import concurrent.futures as cf
+    m, unit, part, what = w.cpu_sample()
+    if threads <= 1:
+        ranges = [(0, m)]
+    else:
+        step = -(-m // threads // unit) * unit
+        ranges = [(lo, min(m, lo + step)) for lo in range(0, m, step)]
+    pool = cf.ThreadPoolExecutor(max_workers=len(ranges)) if len(ranges) > 1 else None
+
+    def fn():
+        if pool is None:
+            part(0, m)
+        else:
+            list(pool.map(lambda r: part(*r), ranges))
     fn()  # warm
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -283,11 +326,19 @@ def time_cpu(w, budget_s=3.0):
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
+    if pool is not None:
+        pool.shutdown()
     sec = el / reps
     per_elem = w.bytes_per_step / w.n
-    return {"value": round(m * per_elem / sec / 1e9, 3), "unit": "GB/s",
-            "elements_per_s": round(m / sec, 1), "cores": 1, "kind": "port",
-            "sample": f"{what}; {reps} repetition(s), {el:.1f} s; GOMAXPROCS-equivalent 1 (serial loops)"}
+    out = {"value": round(m * per_elem / sec / 1e9, 3), "unit": "GB/s",
+           "elements_per_s": round(m / sec, 1), "cores": len(ranges), "kind": "port"}
+    if len(ranges) == 1:
+        out["sample"] = f"{what}; {reps} repetition(s), {el:.1f} s; GOMAXPROCS-equivalent 1 (serial loops)"
+    else:
+        out["sample"] = (f"{what}, split into {len(ranges)} contiguous ranges on {len(ranges)} threads; "
+                         f"{reps} repetition(s), {el:.1f} s")
+        out["cpu_model"] = cpu_model()
+    return out
 
 
 def profile_run(torch, M, O, reps):
@@ -365,6 +416,7 @@ def main():
         if not args.no_cpu:
             r["cpu_baseline"] = time_cpu(w)
             r["speedup_vs_cpu"] = round(gbs / r["cpu_baseline"]["value"], 1)
+            r["cpu_baseline_all_cores"] = time_cpu(w, budget_s=2.0, threads=cpu_threads())
         log(json.dumps(r))
         results[cls.cfg] = r
         del w
@@ -382,6 +434,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": load_traffic(), "kernel": head["kernel"]},
         "cpu_baseline": head.get("cpu_baseline"),
+        "cpu_baseline_all_cores": head.get("cpu_baseline_all_cores"),
         "elements_per_s": head["elements_per_s"],
         "configs": [results[k] for k in sorted(results)],
     }
