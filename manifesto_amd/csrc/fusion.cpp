@@ -255,7 +255,7 @@ struct mfh_kernel {
     std::vector<mfh_operand> inputs;
     uint8_t out_dtype = mfh::kFloat32;
     int vec = 8;     // elements per work item
-    int unroll = 1;  // work items per thread per grid-stride step
+    int unroll = 1;  // work items per thread per step
     int auto_bpc = 4;  // workgroups per CU unless the launch config sets one
     bool periods_vectorizable = true;
     std::shared_ptr<mfh::CodeObject> code;
