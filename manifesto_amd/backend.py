@@ -208,15 +208,21 @@ class Backend:
                                            ctypes.byref(h)))
         return Tensor(self, h)
 
-    def download(self, tensor: Tensor):
-        """Backend.Download: (storage dtype, bytes)."""
+    def download(self, tensor: Tensor, out=None):
+        """Backend.Download: (storage dtype, bytes).  The bytes are a
+        bytearray the call fills (or `out`, a writable buffer of at least the
+        tensor's size, reused as is)."""
         L = _L()
         n = max(0, tensor.len()) * max(1, _size(tensor.dtype()))
-        out = bytearray(n)
-        ptr = (ctypes.c_char * max(1, n)).from_buffer(out) if n else None
+        if out is None:
+            out = bytearray(n)
+        view = memoryview(out).cast("B")
+        if view.nbytes < n:
+            raise ValueError(f"download: buffer holds {view.nbytes} bytes, need {n}")
+        ptr = (ctypes.c_char * max(1, view.nbytes)).from_buffer(view) if n else None
         dt, got = ctypes.c_uint8(), ctypes.c_size_t()
-        check(L.mfh_backend_download(self._h, tensor._h, ctypes.byref(dt), ptr, n, ctypes.byref(got)))
-        return dt.value, bytes(out[:got.value])
+        check(L.mfh_backend_download(self._h, tensor._h, ctypes.byref(dt), ptr, view.nbytes, ctypes.byref(got)))
+        return dt.value, out if got.value == view.nbytes else view[:got.value]
 
     def axpy_onto_resident(self, y: Tensor, x: Tensor, alpha: float) -> Tensor:
         check(_L().mfh_axpy_onto_resident(self._h, y._h, x._h, alpha))
