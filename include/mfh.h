@@ -190,9 +190,11 @@ int mfh_fusion_compile(const mfh_ast_node* nodes, int32_t n_nodes, const mfh_ope
                        uint32_t flags, mfh_kernel** kernel);
 
 /* HIPKernel.Source / KernelName / Identifier, like MetalKernel
- * (codegen/metal.go:38-56).  The strings live until mfh_fusion_release. */
+ * (codegen/metal.go:35-56): the identifier is the output port ("anon" when
+ * none was given).  The strings live until mfh_fusion_release. */
 const char* mfh_fusion_source(const mfh_kernel* kernel);
 const char* mfh_fusion_kernel_name(const mfh_kernel* kernel);
+const char* mfh_fusion_identifier(const mfh_kernel* kernel);
 int32_t mfh_fusion_num_inputs(const mfh_kernel* kernel);
 
 /* Runs the kernel over `count` elements: CPUKernel.Run (codegen/cpu.go:59-90)

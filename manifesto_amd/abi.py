@@ -85,6 +85,7 @@ def _declare(L):
                                           c.c_char_p, c.c_uint32, c.POINTER(vp)]),
         "mfh_fusion_source": (c.c_char_p, [vp]),
         "mfh_fusion_kernel_name": (c.c_char_p, [vp]),
+        "mfh_fusion_identifier": (c.c_char_p, [vp]),
         "mfh_fusion_num_inputs": (i32, [vp]),
         "mfh_fusion_launch": (c.c_int, [vp, c.POINTER(vp), i32, vp, i64, vp]),
         "mfh_fusion_release": (c.c_int, [vp]),
@@ -192,6 +193,10 @@ class FusedKernel:
     @property
     def kernel_name(self) -> str:
         return lib().mfh_fusion_kernel_name(self._h).decode()
+
+    @property
+    def identifier(self) -> str:
+        return lib().mfh_fusion_identifier(self._h).decode()
 
     def launch(self, inputs, out: int, count: int, stream: int = 0) -> None:
         ptrs = (ctypes.c_void_p * max(1, len(inputs)))(*inputs)

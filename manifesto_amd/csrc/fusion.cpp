@@ -483,6 +483,7 @@ int mfh_fusion_compile(const mfh_ast_node* nodes, int32_t n_nodes, const mfh_ope
 
 const char* mfh_fusion_source(const mfh_kernel* kernel) { return kernel ? kernel->source.c_str() : nullptr; }
 const char* mfh_fusion_kernel_name(const mfh_kernel* kernel) { return kernel ? kernel->kernel_name.c_str() : nullptr; }
+const char* mfh_fusion_identifier(const mfh_kernel* kernel) { return kernel ? kernel->identifier.c_str() : nullptr; }
 int32_t mfh_fusion_num_inputs(const mfh_kernel* kernel) { return kernel ? (int32_t)kernel->inputs.size() : -1; }
 
 int mfh_fusion_launch(const mfh_kernel* kernel, const void* const* inputs, int32_t n_inputs, void* out,

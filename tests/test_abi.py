@@ -52,6 +52,7 @@ def test_emit_hip_swiglu_source_shape():
     k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "mlp.swiglu-out")
     src = k.source
     assert k.kernel_name == "fused_mlp_swiglu_out"  # like metalKernelName (codegen/metal.go:281-290)
+    assert k.identifier == "mlp.swiglu-out"  # Identifier() is the output port (codegen/metal.go:143)
     assert f'void {k.kernel_name}(' in src
     # reads 4 B per element, writes 2: streamed (non-temporal) loads
     assert "mfh_ld8_bf16<1>(p0, e0, a0[u])" in src and "mfh_ld8_bf16<1>(p1, e0, a1[u])" in src
