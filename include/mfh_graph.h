@@ -170,7 +170,10 @@ typedef struct {
  * node's OutputType, else the graph's ExecutionDType, else Float32.
  * Intermediates live in one device workspace per graph, laid out by value
  * lifetime and kept across calls.  Every bound output receives its value; an
- * output with no binding is computed and dropped. */
+ * output with no binding is computed and dropped.  Calls on one graph must
+ * not overlap in host threads (they share its workspace, streams and replay
+ * cache); different graphs may be called from different threads.  Work
+ * queued on different caller streams is ordered by the graph itself. */
 int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
                    int32_t n_outputs, void* stream);
 
