@@ -387,7 +387,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards with no exchange step; see DESIGN.md)", file=sys.stderr)
+              "(every config shards into contiguous per-GPU ranges with no exchange step, so "
+              "one GPU's share at its real shape is what this bench measures)", file=sys.stderr)
         sys.exit(2)
 
     import torch
