@@ -51,6 +51,7 @@
 #define mfh_is_nan_or_inf_class(v) (std::isnan(v) || std::isinf(v))
 inline unsigned mfh_fbits(float f) { unsigned u; __builtin_memcpy(&u, &f, 4); return u; }
 inline float mfh_fromfbits(unsigned u) { float f; __builtin_memcpy(&f, &u, 4); return f; }
+inline int mfh_low_int(double d) { unsigned long long u; __builtin_memcpy(&u, &d, 8); return (int)(unsigned)u; }
 #else
 extern "C" __device__ double __ocml_tanh_f64(double);
 extern "C" __device__ double __ocml_exp_f64(double);
@@ -75,6 +76,7 @@ extern "C" __device__ double __ocml_log_f64(double);
 #define mfh_med3f(x, lo, hi) __builtin_amdgcn_fmed3f((x), (lo), (hi))
 __device__ inline unsigned mfh_fbits(float f) { return __builtin_bit_cast(unsigned, f); }
 __device__ inline float mfh_fromfbits(unsigned u) { return __builtin_bit_cast(float, u); }
+__device__ inline int mfh_low_int(double d) { return (int)(unsigned)__builtin_bit_cast(unsigned long long, d); }
 #endif
 
 #define MFH_LOG2E_F 1.44269502162933349609375f         // 0x3fb8aa3b
@@ -190,59 +192,82 @@ MFH_MATH float mfh_gelu_ref(float v)
     return (float)(0.5 * d * (1.0 + th));
 }
 
+// Each fast activation comes in two parts: mfh_<name>_fast(v, rare) is
+// branch-free and sets `rare` for the inputs it does not cover, and
+// mfh_<name>(v) returns the reference form for those and the fast value for
+// all others.  Generated kernels call the fast forms for every element of an
+// item and then recompute the flagged elements through mfh_<name>, so the
+// results are the same and the item's main body has no branch.
+//
+// Ranges are reduced by the round-to-integer constant C = 1.5 * 2^52:
+// fma(a, b, C) = C + rint(a b) for |a b| < 2^51, whose low word is that
+// integer as an int32, and fma(a, b, -(that - C)) is the remainder rounded
+// once; three f64 operations where rint, a subtraction and an integer
+// conversion took four (f64 runs at half the f32 rate on gfx950).
+#define MFH_ROUND_INT_D 6755399441055744.0  // 1.5 * 2^52
+
 // sigmoid(v) = 1 / (1 + 2^t), t = -v log2(e), all in f64: for v < 0 the
 // result is ~e^v and inherits the full relative error of E, which an f32
 // exponential (0.9 ulp) plus the final rounding would push past the 1-ulp
 // Sigmoid budget on a few inputs.  In f64 (2^f to 2^-39.9, reciprocal plus one
 // Newton step) the single rounding to f32 is the only error that matters.
 // Below -708 (and -Inf, NaN) the reference's form; +Inf gives 1 by itself.
-MFH_MATH float mfh_sigmoid(float v)
+MFH_MATH float mfh_sigmoid_fast(float v, bool& rare)
 {
-    const double t = (double)mfh_med3f(v, -708.0f, 800.0f) * -MFH_LOG2E_D;
-    const double kd = mfh_rint(t);
-    const double den = 1.0 + mfh_ldexp(mfh_exp2_poly_d(t - kd), (int)kd);
+    const double x = (double)mfh_med3f(v, -708.0f, 800.0f);
+    const double tk = mfh_fma(x, -MFH_LOG2E_D, MFH_ROUND_INT_D);
+    const double kd = tk - MFH_ROUND_INT_D;
+    const double den = 1.0 + mfh_ldexp(mfh_exp2_poly_d(mfh_fma(x, -MFH_LOG2E_D, -kd)), mfh_low_int(tk));
     const double r = mfh_rcp(den);
-    float s = (float)mfh_fma(r, mfh_fma(-den, r, 1.0), r);
-    MFH_KEEP(s);
-    if (!(v >= -708.0f)) s = mfh_sigmoid_ref(v);
-    return s;
+    rare |= !(v >= -708.0f);
+    return (float)mfh_fma(r, mfh_fma(-den, r, 1.0), r);
 }
 
 // silu(v) = v / (1 + e^-v); below -87 (and -Inf, NaN) the f64 form, where the
-// result underflows to denormals and -0.  +Inf gives +Inf.
-MFH_MATH float mfh_silu(float v)
+// result underflows to denormals and -0, and +Inf, which the f64 form maps to
+// +Inf (every v that the clamp to [-87, FLT_MAX] changes).
+MFH_MATH float mfh_silu_fast(float v, bool& rare)
 {
     int k;
-    float p = mfh_exp_core(-mfh_med3f(v, -87.0f, 104.0f), &k);
-    float s = mfh_div_one_plus(v, p, k);
-    MFH_KEEP(s);
-    s = v == __builtin_inff() ? v : s;
-    if (!(v >= -87.0f)) s = mfh_silu_ref(v);
-    return s;
+    const float p = mfh_exp_core(-mfh_med3f(v, -87.0f, 104.0f), &k);
+    rare |= mfh_med3f(v, -87.0f, 3.40282347e38f) != v;
+    return mfh_div_one_plus(v, p, k);
 }
 
 // Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
-// t = -2 inner log2(e) = d (KA + KB d^2) formed in f64 (the cubic needs more
-// than f32's 24 bits where E is large), reduced in f64 (t = k + f exactly) and
-// 2^f evaluated in f32.  Within 2 f32 ulps of the reference over every f32
-// input.  Above v = 14 the reference's tanh is exactly 1 in f64 and
-// gelu(v) = v, which the clamped d reproduces.  Below v = -4.9 (inner < -9.3)
-// the reference's 1 + tanh cancels in f64, so that rare range (and NaN) runs
-// the reference form itself.
+// t = -2 inner log2(e) = d w, w = KA + KB d^2, formed and reduced in f64 (the
+// cubic needs more than f32's 24 bits where E is large) and 2^f evaluated in
+// f32.  Within 2 f32 ulps of the reference over every f32 input.  Above
+// v = 14 the reference's tanh is exactly 1 in f64 and gelu(v) = v, which the
+// clamped d reproduces.  Below v = -4.9 (inner < -9.3) the reference's
+// 1 + tanh cancels in f64, so that rare range, +Inf and NaN (every v that the
+// clamp to [-4.9, FLT_MAX] changes) take the reference form itself.
 #define MFH_GELU_KA (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_LOG2E_D)
 #define MFH_GELU_KB (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_GELU_A_D * MFH_LOG2E_D)
-MFH_MATH float mfh_gelu(float v)
+MFH_MATH float mfh_gelu_fast(float v, bool& rare)
 {
-    double d = (double)mfh_med3f(v, -5.0f, 14.0f);
-    double t = d * mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA);
-    double kd = mfh_rint(t);
-    float p = mfh_exp2_poly((float)(t - kd));
-    float s = mfh_div_one_plus_short(v, p, (int)kd);
-    MFH_KEEP(s);
-    s = v == __builtin_inff() ? v : s;
-    if (!(v >= -4.9f)) s = mfh_gelu_ref(v);
-    return s;
+    const double d = (double)mfh_med3f(v, -5.0f, 14.0f);
+    const double w = mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA);
+    const double tk = mfh_fma(w, d, MFH_ROUND_INT_D);
+    const double kd = tk - MFH_ROUND_INT_D;
+    const float p = mfh_exp2_poly((float)mfh_fma(w, d, -kd));
+    rare |= mfh_med3f(v, -4.9f, 3.40282347e38f) != v;
+    return mfh_div_one_plus_short(v, p, mfh_low_int(tk));
 }
+
+#define MFH_FAST_OR_REF(name)               \
+    MFH_MATH float mfh_##name(float v)       \
+    {                                       \
+        bool rare = false;                  \
+        float s = mfh_##name##_fast(v, rare); \
+        MFH_KEEP(s);                        \
+        if (rare) s = mfh_##name##_ref(v);  \
+        return s;                           \
+    }
+MFH_FAST_OR_REF(sigmoid)
+MFH_FAST_OR_REF(silu)
+MFH_FAST_OR_REF(gelu)
+#undef MFH_FAST_OR_REF
 
 MFH_MATH float mfh_exp_ref(float v) { return (float)mfh_exp_f64((double)v); }
 MFH_MATH float mfh_log_ref(float v) { return (float)mfh_log_f64((double)v); }

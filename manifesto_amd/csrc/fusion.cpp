@@ -80,6 +80,11 @@ struct Emitter {
     // Vector loop only: inputs held as packed f16 words w<k>[u][j >> 1]
     // (empty in the element loop).
     std::vector<bool> packed16 = {};
+    // Vector loop only: Sigmoid, Silu and Gelu call their branch-free fast
+    // forms, which OR each element's rare-range flag into the item's bool
+    // `q`; `deferred` is set once such a call has been emitted.
+    bool defer_rare = false;
+    bool deferred = false;
 
     std::string fresh() { return "t" + std::to_string(tmp++); }
 
@@ -88,6 +93,15 @@ struct Emitter {
         std::string name = fresh();
         body += "        const float " + name + " = " + expr + ";\n";
         return name;
+    }
+
+    std::string activation(const char* name, const std::string& a)
+    {
+        const std::string fn = std::string("mfh_") + name;
+        if (precise) return let(fn + "_ref(" + a + ")");
+        if (!defer_rare) return let(fn + "(" + a + ")");
+        deferred = true;
+        return let(fn + "_fast(" + a + ", q)");
     }
 
     // Returns the name holding node idx's value for the current element.
@@ -131,10 +145,10 @@ struct Emitter {
         case kNodeExp: return let("mfh_exp_ref(" + a + ")");
         case kNodeLog: return let("mfh_log_ref(" + a + ")");
         case kNodeReLU: return let("(" + a + " < 0.0f) ? 0.0f : " + a);
-        case kNodeSigmoid: return let((precise ? "mfh_sigmoid_ref(" : "mfh_sigmoid(") + a + ")");
+        case kNodeSigmoid: return activation("sigmoid", a);
         case kNodeTanh: return let("mfh_tanh_ref(" + a + ")");
-        case kNodeSilu: return let((precise ? "mfh_silu_ref(" : "mfh_silu(") + a + ")");
-        case kNodeGelu: return let((precise ? "mfh_gelu_ref(" : "mfh_gelu(") + a + ")");
+        case kNodeSilu: return activation("silu", a);
+        case kNodeGelu: return activation("gelu", a);
         case kNodeLeakyReLU: {
             std::string scaled = let("0.01f * " + a);
             return let("(" + a + " >= 0.0f) ? " + a + " : " + scaled);
@@ -302,13 +316,21 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     for (int k = 0; k < n_inputs; k++)
         if (inputs[k].mode == MFH_OPERAND_PERIODIC && inputs[k].period % vec != 0) periods_vectorizable = false;
 
-    // Launch shape: one item per thread and a one-shot grid (one block per
-    // 256 items, so each block streams one chunk and exits and the blocks
-    // sweep memory in dispatch order).  Measured on MI355X against
-    // grid-stride loops at 4-24 blocks per CU: +11% on the SwiGLU chain and
-    // +9% on the f16 gelu chain; a no-compute 2:1 read:write stream gains
-    // 17% the same way.  mfh_set_launch_config("fused", ...) overrides both.
-    const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : 1;
+    const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
+    // Launch shape: a one-shot grid (one block per 256 x unroll items, so each
+    // block streams one chunk and exits and the blocks sweep memory in
+    // dispatch order).  Measured on MI355X against grid-stride loops at 4-24
+    // blocks per CU: +11% on the SwiGLU chain and +9% on the f16 gelu chain;
+    // a no-compute 2:1 read:write stream gains 17% the same way.  One item per
+    // thread, except where the fast element math mixes f32 with f64 work
+    // (Gelu, Sigmoid): two items per thread give the gelu chain +5% and the
+    // sigmoid chain 0-3%, while SwiGLU, Silu and add/mul chains lose 2-4% and
+    // the precise (f64 library) forms gain nothing.
+    // mfh_set_launch_config("fused", ...) overrides both.
+    bool f64_fast = false;
+    for (const mfh_ast_node& node : list)
+        if (!precise && (node.type == kNodeGelu || node.type == kNodeSigmoid)) f64_fast = true;
+    const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : f64_fast ? 2 : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
     // Non-temporal loads for the streamed (full-length) operands when the
     // kernel reads at least as many bytes per element as it writes.
@@ -317,7 +339,6 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
         if (inputs[k].mode == MFH_OPERAND_FULL) read_bytes += inputs[k].dtype == kFloat32 ? 4 : 2;
     const bool stream_loads = read_bytes >= (out_dtype == kFloat32 ? 4 : 2);
 
-    const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
     // Element loop: every operand decoded to f32.  Vector loop: f16 operands
     // stay packed words so that adds can take them directly.
     Emitter em{list, c0, c1, precise, "", 0};
@@ -325,8 +346,12 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     std::vector<bool> packed16(n_inputs, false);
     for (int k = 0; k < n_inputs; k++)
         packed16[k] = inputs[k].mode != MFH_OPERAND_SCALAR && inputs[k].dtype == kFloat16;
-    Emitter emv{list, c0, c1, precise, "", 0, packed16};
+    Emitter emv{list, c0, c1, precise, "", 0, packed16, true};
     std::string vresult = emv.emit(0);
+    // With fast activations, elements in a rare range are recomputed after
+    // the item's main body by the same expression with the per-element forms.
+    Emitter emr{list, c0, c1, precise, "", 0, packed16};
+    const std::string rresult = emv.deferred ? emr.emit(0) : "";
 
     std::string identifier = output_port && *output_port ? output_port : "anon";
     std::string kernel_name = "fused_" + sanitize(output_port ? output_port : "");
@@ -372,16 +397,26 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     src += "            }\n        }\n";
     src += "#pragma unroll\n        for (int u = 0; u < " + U + "; u++) {\n";
     src += "            const mfh_i64 it = v + u * stride;\n            if (it >= nvec) break;\n";
-    src += "            float r[" + V + "];\n#pragma unroll\n            for (int j = 0; j < " + V + "; j++) {\n";
+    std::string operands;
     for (int k = 0; k < n_inputs; k++) {
         std::string ks = std::to_string(k);
         std::string value = inputs[k].mode == MFH_OPERAND_SCALAR ? "s" + ks
                             : packed16[k] ? "mfh_h2f(w" + ks + "[u][j >> 1], j & 1)"
                                           : "a" + ks + "[u][j]";
-        src += "        const float x" + ks + " = " + value + ";\n";
+        operands += "        const float x" + ks + " = " + value + ";\n";
     }
-    src += emv.body;
+    src += "            float r[" + V + "];\n";
+    if (emv.deferred) src += "            bool q = false;\n";
+    src += "#pragma unroll\n            for (int j = 0; j < " + V + "; j++) {\n";
+    src += operands + emv.body;
     src += "                r[j] = " + vresult + ";\n            }\n";
+    if (emv.deferred) {
+        // an item with an element in a rare range: every element again with
+        // the per-element forms (the same value for the others)
+        src += "            if (q) {\n#pragma unroll\n                for (int j = 0; j < " + V + "; j++) {\n";
+        src += operands + emr.body;
+        src += "                    r[j] = " + rresult + ";\n                }\n            }\n";
+    }
     src += "            mfh_st" + V + "_" + osfx + "(pout, it * " + V + ", r);\n        }\n    }\n";
     // scalar tail (and the whole range when the vector path is off)
     src += "    for (mfh_i64 i = nvec * " + V + " + tid; i < n; i += stride) {\n";

@@ -57,8 +57,13 @@ def test_emit_hip_swiglu_source_shape():
     # reads 4 B per element, writes 2: streamed (non-temporal) loads
     assert "mfh_ld8_bf16<1>(p0, e0, a0[u])" in src and "mfh_ld8_bf16<1>(p1, e0, a1[u])" in src
     assert "streamed loads" in src
-    assert "mfh_silu(x0)" in src and "mfh_st8_bf16(pout, it * 8, r)" in src
+    assert "mfh_st8_bf16(pout, it * 8, r)" in src
     assert src.count("for (mfh_i64 i = nvec * 8 + tid; i < n; i += stride)") == 1
+    # the vector loop runs the branch-free fast form with a per-item rare flag
+    # and recomputes flagged items with the per-element form; the scalar tail
+    # uses the per-element form directly
+    assert "mfh_silu_fast(x0, q)" in src and "if (q) {" in src and src.count("mfh_silu(x0)") == 2
+    assert "8 elements per item, 1 item(s) per thread" in src  # f32-only math: one item per thread
 
 
 def test_emit_hip_broadcast_operands():
@@ -75,9 +80,12 @@ def test_emit_hip_broadcast_operands():
     assert "mfh_add_fh(t2, w3[u][j >> 1], j & 1)" in src
     assert "const float x1 = mfh_ld1_f16(p1, (i % 4096LL));" in src  # element loop decodes
     assert "const float s2 = mfh_ld1_f32(p2, 0);" in src
-    assert "mfh_gelu(" in src
+    assert "mfh_gelu_fast(t1, q)" in src and "mfh_gelu(t1)" in src
+    # gelu mixes f32 with f64 work: two items per thread by default
+    assert "8 elements per item, 2 item(s) per thread" in src
     precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)
-    assert "mfh_gelu_ref(" in precise.source
+    assert "mfh_gelu_ref(" in precise.source and "_fast(" not in precise.source.split("EmitHIP")[1]
+    assert "if (q)" not in precise.source and "1 item(s) per thread" in precise.source
 
 
 def test_emit_hip_item_width_follows_the_widest_operand():
