@@ -6,7 +6,8 @@ achieved HBM GB/s (algorithmic bytes / kernel time) and as a fraction of the
 MI355X's 8 TB/s.  One step = one kernel launch over one resident batch.  Buffer
 sets are rotated so the footprint exceeds the 256 MB Infinity Cache, and the
 timed steps are replayed from a captured HIP graph so the clock sees kernel
-time, not Python launch overhead.  The other BASELINE configs (axpy, SwiGLU,
+time, not Python launch overhead; the W warm-up steps replay the same graph
+first, so the timed replay runs at the settled clock of sustained load.  The other BASELINE configs (axpy, SwiGLU,
 the f16 gelu chain, Int4) are measured the same way and listed under
 "configs".  The CPU baseline is the oracle (a C restatement of the Go loops,
 -O2 -ffp-contract=off) timed on this host, single-threaded as the Go loops
@@ -238,14 +239,25 @@ class Int4(Workload):
 WORKLOADS = [Axpy, Fp8, SwiGLU, GeluChain, Int4]
 
 
+def warm_steps(w, args):
+    """Untimed launches time_gpu makes before the timed region."""
+    if args.no_graph:
+        return max(args.warmup, len(w.sets))
+    return len(w.sets) + max(1, -(-args.warmup // args.steps)) * args.steps
+
+
 def time_gpu(w, steps, warmup, use_graph=True):
     """Runs `warmup` untimed steps, then times exactly `steps` steps (each one
     launch over the next rotated buffer set) between two events on the
     launch stream.  With use_graph the `steps` launches are captured into one
-    HIP graph that is replayed once untimed and once timed, so the timed
-    region holds back-to-back kernels with no host launch gaps."""
+    HIP graph, the warm-up runs as ceil(warmup / steps) untimed replays of it
+    (at least one) and one more replay is timed, so the timed region holds
+    back-to-back kernels with no host launch gaps and follows the same load.
+    Under sustained load the board sits at its power cap and the clock
+    settles over the first tens of milliseconds; a warm-up of a few replays
+    times the settled state."""
     torch = w.torch
-    for i in range(max(warmup, len(w.sets))):
+    for i in range(len(w.sets) if use_graph else max(warmup, len(w.sets))):
         w.step(i)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -257,7 +269,8 @@ def time_gpu(w, steps, warmup, use_graph=True):
                 for i in range(steps):
                     w.step(i)
         torch.cuda.synchronize()
-        graph.replay()  # warm
+        for _ in range(max(1, -(-warmup // steps))):
+            graph.replay()
         torch.cuda.synchronize()
         s = torch.cuda.current_stream()
         t0 = time.perf_counter()
@@ -378,7 +391,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", type=int, default=0, help="measure only this BASELINE config")
@@ -413,7 +426,8 @@ def main():
         r = {"config": cls.cfg, "workload": w.name, "kernel": w.kernel, "ms_per_step": round(ms, 5),
              "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
              "elements_per_s": round(w.n / (ms * 1e-3), 1), "bytes_per_step": w.bytes_per_step,
-             "steps_timed": n, "rotated_sets": len(w.sets), "wall_s": round(wall, 4)}
+             "steps_timed": n, "warmup_steps_run": warm_steps(w, args), "rotated_sets": len(w.sets),
+             "wall_s": round(wall, 4)}
         if not args.no_cpu:
             r["cpu_baseline"] = time_cpu(w)
             r["speedup_vs_cpu"] = round(gbs / r["cpu_baseline"]["value"], 1)
@@ -431,7 +445,7 @@ def main():
         "data": "synthetic (seeded torch RNG on device; uniform bytes over all 256 codes)",
         "config": {"workload": "BASELINE config 2: fp8_e4m3 -> bf16 dequant [4096,14336], scale 0.0125",
                    "elements": Fp8.n, "algorithmic_bytes_per_step": Fp8.bytes_per_step,
-                   "timing": "HIP events on the launch stream around one replay of a graph of K launches over rotated buffer sets"},
+                   "timing": "HIP events on the launch stream around one replay of a graph of K launches over rotated buffer sets, after ceil(W/K) untimed replays of the same graph"},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": load_traffic(), "kernel": head["kernel"]},
         "cpu_baseline": head.get("cpu_baseline"),
