@@ -89,6 +89,17 @@ int mfh_stream_sync(void* stream);
 int mfh_set_launch_config(const char* kernel, int32_t blocks_per_cu, int32_t items_per_thread);
 int mfh_get_launch_config(const char* kernel, int32_t* blocks_per_cu, int32_t* items_per_thread);
 
+/* Threads per workgroup of a kernel family, the third part of its launch
+ * shape.  "fused" takes any power of two from 64 to 1024 and applies it to
+ * kernels compiled afterwards (default 64, one wave: measured fastest on
+ * MI355X for the streaming chains); the other families are compiled for 256
+ * and accept only that.  0 keeps the current setting and -1 restores the
+ * default; also settable with MFH_THREADS_<KERNEL>.  mfh_get_launch_threads
+ * reports 0 for "fused" while each kernel uses its default.  No counterpart
+ * in the reference; results do not depend on it. */
+int mfh_set_launch_threads(const char* kernel, int32_t threads);
+int mfh_get_launch_threads(const char* kernel, int32_t* threads);
+
 /* ---- runtime host math -------------------------------------------------- */
 
 /* y <- y + alpha*x in place over `count` elements of storage dtype `dtype`

@@ -17,7 +17,7 @@ from .abi import (  # noqa: F401
     OPERAND_FULL, OPERAND_PERIODIC, OPERAND_SCALAR, FUSION_PRECISE,
     AstNode, Operand, FusedKernel,
     axpy, dequant_fp8, dequant_int4, convert, scalar_broadcast, linspace,
-    take_sticky_error, stream_sync, set_launch_config, get_launch_config,
+    take_sticky_error, stream_sync, set_launch_config, get_launch_config, set_launch_threads, get_launch_threads,
 )
 
 __all__ = [name for name in dir() if not name.startswith("_")]

@@ -75,6 +75,8 @@ def _declare(L):
         "mfh_stream_sync": (c.c_int, [vp]),
         "mfh_set_launch_config": (c.c_int, [c.c_char_p, i32, i32]),
         "mfh_get_launch_config": (c.c_int, [c.c_char_p, c.POINTER(i32), c.POINTER(i32)]),
+        "mfh_set_launch_threads": (c.c_int, [c.c_char_p, i32]),
+        "mfh_get_launch_threads": (c.c_int, [c.c_char_p, c.POINTER(i32)]),
         "mfh_axpy": (None, [vp, vp, i64, f32, u8, vp]),
         "mfh_scalar_broadcast": (c.c_int, [vp, u8, vp, u8, i64, f32, i32, vp]),
         "mfh_linspace": (c.c_int, [vp, u8, i64, f32, f32, i32, vp]),
@@ -127,6 +129,17 @@ def get_launch_config(kernel: str):
     bpc, ipt = ctypes.c_int32(), ctypes.c_int32()
     check(lib().mfh_get_launch_config(kernel.encode(), ctypes.byref(bpc), ctypes.byref(ipt)))
     return bpc.value, ipt.value
+
+
+def set_launch_threads(kernel: str, threads: int) -> None:
+    """Threads per workgroup of a kernel family (0 keeps, -1 restores the default)."""
+    check(lib().mfh_set_launch_threads(kernel.encode(), threads))
+
+
+def get_launch_threads(kernel: str) -> int:
+    t = ctypes.c_int32()
+    check(lib().mfh_get_launch_threads(kernel.encode(), ctypes.byref(t)))
+    return t.value
 
 
 # ---- runtime math / conversion wrappers ------------------------------------

@@ -58,6 +58,9 @@ enum class Kern { kFp8, kInt4, kAxpy, kAxpy16, kConvert, kFused, kCount };
 // INT4, AXPY, AXPY16, CONVERT, FUSED) change them.
 int blocks_per_cu(Kern k);
 int items_per_thread(Kern k);
+// Threads per workgroup (MFH_THREADS_<NAME>, mfh_set_launch_threads); 0 for
+// the fused family means each generated kernel's default.
+int threads_per_block(Kern k);
 
 }  // namespace mfh
 

@@ -32,7 +32,12 @@ namespace mfh {
 
 namespace {
 
-constexpr int kBlockThreads = 256;
+// Threads per workgroup of a generated kernel unless the launch config sets
+// a size: one wave.  Measured on MI355X at the BASELINE sizes (one-shot grids,
+// same kernels otherwise): the SwiGLU chain +3% and the f16 gelu chain +1%
+// against 256-thread workgroups (128 threads: +1% and -4%); a no-compute
+// 2:1 read:write stream +2-4% with 64 or 128.
+constexpr int kFusedThreads = 64;
 // Blocks per CU that make every grid one-shot (capped by the work itself).
 constexpr int kOneShotBlocksPerCu = 1 << 16;
 
@@ -270,6 +275,7 @@ struct mfh_kernel {
     uint8_t out_dtype = mfh::kFloat32;
     int vec = 8;     // elements per work item
     int unroll = 1;  // work items per thread per step
+    int block = mfh::kFusedThreads;  // threads per workgroup
     int auto_bpc = 4;  // workgroups per CU unless the launch config sets one
     bool periods_vectorizable = true;
     std::shared_ptr<mfh::CodeObject> code;
@@ -317,7 +323,7 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
         if (inputs[k].mode == MFH_OPERAND_PERIODIC && inputs[k].period % vec != 0) periods_vectorizable = false;
 
     const bool precise = (flags & MFH_FUSION_PRECISE) != 0;
-    // Launch shape: a one-shot grid (one block per 256 x unroll items, so each
+    // Launch shape: a one-shot grid (one block per `block` x unroll items, so each
     // block streams one chunk and exits and the blocks sweep memory in
     // dispatch order).  Measured on MI355X against grid-stride loops at 4-24
     // blocks per CU: +11% on the SwiGLU chain and +9% on the f16 gelu chain;
@@ -325,13 +331,15 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // thread, except where the fast element math mixes f32 with f64 work
     // (Gelu, Sigmoid): two items per thread give the gelu chain +5% and the
     // sigmoid chain 0-3%, while SwiGLU, Silu and add/mul chains lose 2-4% and
-    // the precise (f64 library) forms gain nothing.
-    // mfh_set_launch_config("fused", ...) overrides both.
+    // the precise (f64 library) forms gain nothing.  Workgroups of one wave
+    // (kFusedThreads).  mfh_set_launch_config("fused", ...) and
+    // mfh_set_launch_threads("fused", ...) override these.
     bool f64_fast = false;
     for (const mfh_ast_node& node : list)
         if (!precise && (node.type == kNodeGelu || node.type == kNodeSigmoid)) f64_fast = true;
     const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : f64_fast ? 2 : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
+    const int block = threads_per_block(Kern::kFused) > 0 ? threads_per_block(Kern::kFused) : kFusedThreads;
     // Non-temporal loads for the streamed (full-length) operands when the
     // kernel reads at least as many bytes per element as it writes.
     int read_bytes = 0;
@@ -356,7 +364,7 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     std::string identifier = output_port && *output_port ? output_port : "anon";
     std::string kernel_name = "fused_" + sanitize(output_port ? output_port : "");
     const char* osfx = io_suffix(out_dtype);
-    const std::string V = std::to_string(vec), U = std::to_string(unroll);
+    const std::string V = std::to_string(vec), U = std::to_string(unroll), B = std::to_string(block);
 
     std::string src;
     src.reserve(sizeof(kPrelude) + 4096);
@@ -364,11 +372,11 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     src += "\n// EmitHIP: fusion '" + identifier + "'" + (precise ? " (precise transcendentals)" : "") +
            ", " + V + " elements per item, " + U + " item(s) per thread per step" +
            (stream_loads ? ", streamed loads" : "") + "\n";
-    src += "extern \"C\" __global__ __launch_bounds__(256) void " + kernel_name + "(\n";
+    src += "extern \"C\" __global__ __launch_bounds__(" + B + ") void " + kernel_name + "(\n";
     for (int k = 0; k < n_inputs; k++) src += "    const void* __restrict__ p" + std::to_string(k) + ",\n";
     src += "    void* __restrict__ pout, mfh_i64 n, mfh_i64 nvec)\n{\n";
-    src += "    const mfh_i64 stride = (mfh_i64)gridDim.x * 256;\n";
-    src += "    const mfh_i64 tid = (mfh_i64)blockIdx.x * 256 + threadIdx.x;\n";
+    src += "    const mfh_i64 stride = (mfh_i64)gridDim.x * " + B + ";\n";
+    src += "    const mfh_i64 tid = (mfh_i64)blockIdx.x * " + B + " + threadIdx.x;\n";
     for (int k = 0; k < n_inputs; k++)
         if (inputs[k].mode == MFH_OPERAND_SCALAR)
             src += "    const float s" + std::to_string(k) + " = mfh_ld1_" + io_suffix(inputs[k].dtype) + "(p" +
@@ -439,6 +447,7 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     kernel->out_dtype = out_dtype;
     kernel->vec = vec;
     kernel->unroll = unroll;
+    kernel->block = block;
     kernel->auto_bpc = auto_bpc;
     kernel->periods_vectorizable = periods_vectorizable;
     MFH_TRY(compile_source(kernel->source, kernel_name, &kernel->code));
@@ -474,9 +483,9 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
     MFH_TRY(load_function(*kernel->code, dev->ordinal, &fn));
     int64_t nvec = vec_ok ? count / kernel->vec : 0;
     int64_t items = nvec > 0 ? (nvec + kernel->unroll - 1) / kernel->unroll : count;
-    int64_t need = (items + kBlockThreads - 1) / kBlockThreads;
+    int64_t need = (items + kernel->block - 1) / kernel->block;
     int bpc = blocks_per_cu(Kern::kFused) > 0 ? blocks_per_cu(Kern::kFused) : kernel->auto_bpc;
-    int64_t cap = std::min<int64_t>((int64_t)dev->compute_units * bpc, (int64_t(1) << 32) / kBlockThreads - 1);
+    int64_t cap = std::min<int64_t>((int64_t)dev->compute_units * bpc, (int64_t(1) << 32) / kernel->block - 1);
     unsigned grid = (unsigned)std::max<int64_t>(1, std::min(need, cap));
     std::vector<const void*> ptrs(inputs, inputs + n_inputs);
     std::vector<void*> args;
@@ -485,7 +494,7 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
     args.push_back(&out);
     args.push_back(&count);
     args.push_back(&nvec);
-    return check_hip(hipModuleLaunchKernel(fn, grid, 1, 1, kBlockThreads, 1, 1, 0, stream, args.data(), nullptr),
+    return check_hip(hipModuleLaunchKernel(fn, grid, 1, 1, kernel->block, 1, 1, 0, stream, args.data(), nullptr),
                      "hipModuleLaunchKernel");
 }
 

@@ -155,7 +155,8 @@ struct LaunchCfg {
     const char* name;
     std::atomic<int> bpc;
     std::atomic<int> unroll;  // 0: the kernel family chooses (fused: per kernel)
-    int default_bpc = 0, default_unroll = 0;  // filled from the initial values
+    std::atomic<int> threads;  // threads per workgroup; 0: the family's default
+    int default_bpc = 0, default_unroll = 0, default_threads = 0;  // filled from the initial values
 };
 // Large enough that every thread runs exactly one step at any size that
 // fits in HBM (the grid is also capped by the work itself): "one-shot"
@@ -164,11 +165,23 @@ constexpr int kMaxBlocksPerCu = 1 << 16;
 // Defaults measured on MI355X (256 CUs) with streaming loads and stores:
 // every family runs one-shot, FP8 and Int4 with two items per thread, axpy
 // and the casts with one.  0 for the fused family means "per kernel": each
-// generated kernel carries its shape (see fusion.cpp).
+// generated kernel carries its shape (see fusion.cpp).  The ahead-of-time
+// families are compiled for 256-thread workgroups; generated kernels take
+// their workgroup size at compile time (default 64, fusion.cpp).
 LaunchCfg g_cfg[(int)Kern::kCount] = {
-    {"fp8", {kMaxBlocksPerCu}, {2}}, {"int4", {kMaxBlocksPerCu}, {2}}, {"axpy", {kMaxBlocksPerCu}, {1}},
-    {"axpy16", {kMaxBlocksPerCu}, {1}}, {"convert", {kMaxBlocksPerCu}, {1}}, {"fused", {0}, {0}},
+    {"fp8", {kMaxBlocksPerCu}, {2}, {256}}, {"int4", {kMaxBlocksPerCu}, {2}, {256}},
+    {"axpy", {kMaxBlocksPerCu}, {1}, {256}}, {"axpy16", {kMaxBlocksPerCu}, {1}, {256}},
+    {"convert", {kMaxBlocksPerCu}, {1}, {256}}, {"fused", {0}, {0}, {0}},
 };
+
+// Workgroup sizes a family can run: the ahead-of-time kernels only the one
+// they are compiled for, generated kernels any power of two from one wave
+// (64 threads) to 1024.
+bool threads_supported(const LaunchCfg& c, int threads)
+{
+    if (c.default_threads != 0) return threads == c.default_threads;
+    return threads >= 64 && threads <= 1024 && (threads & (threads - 1)) == 0;
+}
 std::once_flag g_cfg_env_once;
 
 void read_cfg_env()
@@ -176,6 +189,7 @@ void read_cfg_env()
     for (auto& c : g_cfg) {
         c.default_bpc = c.bpc.load();
         c.default_unroll = c.unroll.load();
+        c.default_threads = c.threads.load();
     }
     const char* all = std::getenv("MFH_BLOCKS_PER_CU");
     for (auto& c : g_cfg) {
@@ -186,6 +200,8 @@ void read_cfg_env()
         const char* un = std::getenv(("MFH_UNROLL_" + upper).c_str());
         if (bpc && atoi(bpc) > 0 && atoi(bpc) <= kMaxBlocksPerCu) c.bpc = atoi(bpc);
         if (un && (atoi(un) == 1 || atoi(un) == 2 || atoi(un) == 4)) c.unroll = atoi(un);
+        const char* th = std::getenv(("MFH_THREADS_" + upper).c_str());
+        if (th && threads_supported(c, atoi(th))) c.threads = atoi(th);
     }
 }
 
@@ -209,6 +225,12 @@ int items_per_thread(Kern k)
 {
     std::call_once(g_cfg_env_once, read_cfg_env);
     return g_cfg[(int)k].unroll.load(std::memory_order_relaxed);
+}
+
+int threads_per_block(Kern k)
+{
+    std::call_once(g_cfg_env_once, read_cfg_env);
+    return g_cfg[(int)k].threads.load(std::memory_order_relaxed);
 }
 
 }  // namespace mfh
@@ -289,6 +311,33 @@ int mfh_get_launch_config(const char* kernel, int32_t* blocks_per_cu, int32_t* i
     if (!c) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_get_launch_config: unknown kernel family \"%s\"", kernel ? kernel : "(null)");
     if (blocks_per_cu) *blocks_per_cu = c->bpc;
     if (items_per_thread) *items_per_thread = c->unroll;
+    return MFH_OK;
+}
+
+int mfh_set_launch_threads(const char* kernel, int32_t threads)
+{
+    LaunchCfg* c = find_cfg(kernel);
+    if (!c) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_threads: unknown kernel family \"%s\"", kernel ? kernel : "(null)");
+    if (threads == 0) return MFH_OK;
+    if (threads == -1) {
+        c->threads = c->default_threads;
+        return MFH_OK;
+    }
+    if (!threads_supported(*c, threads)) {
+        if (c->default_threads != 0)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_threads: \"%s\" kernels run %d-thread workgroups only, not %d",
+                        c->name, c->default_threads, threads);
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_threads: %d is not a power of two in 64..1024", threads);
+    }
+    c->threads = threads;
+    return MFH_OK;
+}
+
+int mfh_get_launch_threads(const char* kernel, int32_t* threads)
+{
+    LaunchCfg* c = find_cfg(kernel);
+    if (!c) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_get_launch_threads: unknown kernel family \"%s\"", kernel ? kernel : "(null)");
+    if (threads) *threads = c->threads;
     return MFH_OK;
 }
 

@@ -200,3 +200,29 @@ def test_launch_config_set_keep_and_restore():
         M.set_launch_config("fp8", 0, 3)
     with pytest.raises(M.MFHError):
         M.set_launch_config("nope", 1, 1)
+
+
+def test_launch_threads_set_keep_restore_and_limits():
+    assert M.get_launch_threads("fp8") == 256
+    assert M.get_launch_threads("fused") == 0  # each generated kernel's default
+    k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "threads_default")
+    assert "__launch_bounds__(64)" in k.source and "gridDim.x * 64;" in k.source
+    try:
+        M.set_launch_threads("fused", 256)
+        assert M.get_launch_threads("fused") == 256
+        M.set_launch_threads("fused", 0)  # 0 keeps
+        assert M.get_launch_threads("fused") == 256
+        k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "threads_256")
+        assert "__launch_bounds__(256)" in k.source and "blockIdx.x * 256 + threadIdx.x" in k.source
+        for bad in (32, 96, 2048):
+            with pytest.raises(M.MFHError, match="power of two"):
+                M.set_launch_threads("fused", bad)
+        assert M.get_launch_threads("fused") == 256
+    finally:
+        M.set_launch_threads("fused", -1)
+    assert M.get_launch_threads("fused") == 0
+    M.set_launch_threads("axpy", 256)
+    with pytest.raises(M.MFHError, match="256-thread workgroups only"):
+        M.set_launch_threads("axpy", 128)
+    with pytest.raises(M.MFHError, match="unknown kernel family"):
+        M.set_launch_threads("nope", 64)

@@ -1,7 +1,8 @@
 """GPU tests of launch shapes: every streaming kernel family gives the same
 bits under small capped grids (one workgroup per CU, so each workgroup walks
 many chunks, with 1, 2 and 4 items per thread) as under its default one-shot
-grid, at sizes with ragged tails and on unaligned buffers.  The default shape
+grid, at sizes with ragged tails and on unaligned buffers; generated kernels
+also under workgroups of 128, 256 and 1024 threads.  The default shape
 itself is pinned against the oracle here and in the per-family test files."""
 import numpy as np
 import pytest
@@ -22,6 +23,7 @@ def gpu():
     yield
     for fam in ("fp8", "int4", "axpy", "axpy16", "convert", "fused"):
         M.set_launch_config(fam, -1, -1)
+    M.set_launch_threads("fused", -1)
 
 
 def under_shapes(family, run):
@@ -149,4 +151,14 @@ def test_fused_shapes():
         k2.launch([px, pbias, psc, pr], po2, x.size, stream())
         return to_host(o, np.uint8).tobytes() + to_host(o2, np.uint8).tobytes()
 
-    under_shapes("fused", run)
+    want = under_shapes("fused", run)
+    # workgroup sizes other than the default one wave, one-shot and capped
+    try:
+        for threads in (128, 256, 1024):
+            M.set_launch_threads("fused", threads)
+            for bpc, u in ((-1, -1), (1, 2)):
+                M.set_launch_config("fused", bpc, u)
+                assert run() == want, f"fused: {threads} threads, shape ({bpc}, {u}) changed the result"
+    finally:
+        M.set_launch_threads("fused", -1)
+        M.set_launch_config("fused", -1, -1)
