@@ -47,23 +47,24 @@ MFH_DEV void store_one(void* out, mfh_i64 i, mfh_u32 enc)
 // ---------------------------------------------------------------------------
 
 // Item = 8 codes (16-bit output) or 4 codes (f32 output) -> one 16-byte store.
-// A block takes chunks of kBlock * U consecutive items (thread t holds items
-// t, t + kBlock, ...), so each store instruction of a wave writes 1 KiB
-// contiguously.  The grid normally has one block per chunk ("one-shot": no
+// A block of BS threads takes chunks of BS * U consecutive items (thread t
+// holds items t, t + BS, ...), so each store instruction of a wave writes
+// 1 KiB contiguously; with BS < 256 the table build takes 256 / BS entries
+// per thread.  The grid normally has one block per chunk ("one-shot": no
 // block outlives its chunk, so the blocks sweep memory in dispatch order) and
 // loops only when there are more chunks than the largest grid.  A block
 // issues its first chunk's loads before building the table, so the load
 // latency covers the build; stores are streaming (StreamOut: non-temporal).
 // Measured at [4096, 14336] on MI355X: 7.0 TB/s against 5.4 for plain
 // stores in a grid-stride loop at 6 blocks per CU.
-template <int OUT, int U>
-__global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict__ in,
+template <int OUT, int U, int BS>
+__global__ __launch_bounds__(BS) void k_dequant_fp8(const mfh_u8* __restrict__ in,
                                                         void* __restrict__ out, mfh_i64 n,
                                                         float scale, int fmt, int vec_ok)
 {
     __shared__ mfh_u32 lut[256];
     constexpr int kCodes = OUT == kFloat32 ? 4 : 8;
-    constexpr mfh_i64 kChunk = (mfh_i64)kBlock * U;
+    constexpr mfh_i64 kChunk = (mfh_i64)BS * U;
     const mfh_u32 t = threadIdx.x;
     const mfh_i64 nitems = vec_ok ? n / kCodes : 0;
     const mfh_i64 nchunks = (nitems + kChunk - 1) / kChunk;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict
     auto load = [&](mfh_i64 c) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const mfh_i64 i = c * kChunk + u * kBlock + t;
+            const mfh_i64 i = c * kChunk + u * BS + t;
             if (i < nitems) {
                 if constexpr (kCodes == 8) w[u] = reinterpret_cast<const u32x2*>(in)[i];
                 else w[u] = u32x2{reinterpret_cast<const mfh_u32*>(in)[i], 0u};
@@ -80,9 +81,9 @@ __global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict
     };
     mfh_i64 c = blockIdx.x;
     if (c < nchunks) load(c);
-    {
-        mfh_u32 bits = fmt == kF8E4M3 ? mfh_e4m3_bits(t) : mfh_e5m2_bits(t);
-        lut[t] = encode_one<OUT>(mfh_scale_mul(mfh_f32(bits), scale));
+    for (mfh_u32 e = t; e < 256; e += BS) {
+        mfh_u32 bits = fmt == kF8E4M3 ? mfh_e4m3_bits(e) : mfh_e5m2_bits(e);
+        lut[e] = encode_one<OUT>(mfh_scale_mul(mfh_f32(bits), scale));
     }
     __syncthreads();
     for (; c < nchunks; c += gridDim.x) {
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict
         const StreamOut dst(reinterpret_cast<u32x4*>(out) + first, nitems - first);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int j = u * kBlock + (int)t;
+            const int j = u * BS + (int)t;
             if (first + j >= nitems) break;
             const mfh_u32 x = w[u][0], y = w[u][1];
             if constexpr (OUT == kFloat32) {
@@ -104,8 +105,8 @@ __global__ __launch_bounds__(kBlock) void k_dequant_fp8(const mfh_u8* __restrict
             }
         }
     }
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
-    for (mfh_i64 i = nitems * kCodes + (mfh_i64)blockIdx.x * kBlock + t; i < n; i += stride)
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    for (mfh_i64 i = nitems * kCodes + (mfh_i64)blockIdx.x * BS + t; i < n; i += stride)
         store_one<OUT>(out, i, lut[in[i]]);
 }
 
@@ -390,11 +391,14 @@ struct Fp8Launch {
         int64_t items = vec_ok ? std::max<int64_t>(n / codes, 1) : n;
         const mfh_u8* src = static_cast<const mfh_u8*>(in);
         const int u = items_per_thread(Kern::kFp8);
-        unsigned grid = grid_for(items, dev, Kern::kFp8, u);
-        if (u == 4) k_dequant_fp8<OUT, 4><<<grid, kBlock, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
-        else if (u == 2) k_dequant_fp8<OUT, 2><<<grid, kBlock, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
-        else k_dequant_fp8<OUT, 1><<<grid, kBlock, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
-        return launch_status("k_dequant_fp8");
+        return with_block(threads_per_block(Kern::kFp8), [&](auto block) {
+            constexpr int BS = decltype(block)::value;
+            const unsigned grid = grid_for(items, dev, Kern::kFp8, u, BS);
+            if (u == 4) k_dequant_fp8<OUT, 4, BS><<<grid, BS, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
+            else if (u == 2) k_dequant_fp8<OUT, 2, BS><<<grid, BS, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
+            else k_dequant_fp8<OUT, 1, BS><<<grid, BS, 0, stream>>>(src, out, n, scale, fmt, vec_ok);
+            return launch_status("k_dequant_fp8");
+        });
     }
 };
 

@@ -30,15 +30,15 @@ MFH_DEV float axpy_step(float y, float x, float alpha)
     return y + product;
 }
 
-template <int U>
-__global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, const float* __restrict__ x,
+template <int U, int BS>
+__global__ __launch_bounds__(BS) void k_axpy_f32(float* __restrict__ y, const float* __restrict__ x,
                                                      mfh_i64 n, float alpha, int vec_ok)
 {
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
     const mfh_i64 nvec = vec_ok ? (n >> 2) : 0;
     u32x4* yv = reinterpret_cast<u32x4*>(y);
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride * U) {
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nvec; v += stride * U) {
         u32x4 a[U], b[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -58,21 +58,21 @@ __global__ __launch_bounds__(kBlock) void k_axpy_f32(float* __restrict__ y, cons
             store_nt(&yv[i], o);
         }
     }
-    for (mfh_i64 i = nvec * 4 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+    for (mfh_i64 i = nvec * 4 + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride)
         y[i] = axpy_step(y[i], x[i], alpha);
 }
 
 // 16-bit storage: decode, the same f32 step, re-encode (axpyOntoHost tensor
 // path, runtime/axpy.go:120-161, in one pass instead of five).
-template <int DT, int U>
-__global__ __launch_bounds__(kBlock) void k_axpy16(mfh_u16* __restrict__ y, const mfh_u16* __restrict__ x,
+template <int DT, int U, int BS>
+__global__ __launch_bounds__(BS) void k_axpy16(mfh_u16* __restrict__ y, const mfh_u16* __restrict__ x,
                                                    mfh_i64 n, float alpha, int vec_ok)
 {
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
     const mfh_i64 nvec = vec_ok ? (n >> 3) : 0;
     u32x4* yv = reinterpret_cast<u32x4*>(y);
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nvec; v += stride * U) {
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nvec; v += stride * U) {
         u32x4 a[U], b[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -96,16 +96,19 @@ __global__ __launch_bounds__(kBlock) void k_axpy16(mfh_u16* __restrict__ y, cons
             store_nt(&yv[i], o);
         }
     }
-    for (mfh_i64 i = nvec * 8 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    for (mfh_i64 i = nvec * 8 + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride) {
         float r = axpy_step(dec16<DT>(y[i]), dec16<DT>(x[i]), alpha);
         y[i] = (mfh_u16)(enc16x2<DT>(r, 0.0f) & 0xffffu);
     }
 }
 
-template <int DT, int U>
-void launch_axpy16(unsigned grid, hipStream_t s, mfh_u16* y, const mfh_u16* x, int64_t n, float alpha, int vec_ok)
+template <int DT, int BS>
+void launch_axpy16(int u, unsigned grid, hipStream_t s, mfh_u16* y, const mfh_u16* x, int64_t n, float alpha,
+                   int vec_ok)
 {
-    k_axpy16<DT, U><<<grid, kBlock, 0, s>>>(y, x, n, alpha, vec_ok);
+    if (u == 4) k_axpy16<DT, 4, BS><<<grid, BS, 0, s>>>(y, x, n, alpha, vec_ok);
+    else if (u == 2) k_axpy16<DT, 2, BS><<<grid, BS, 0, s>>>(y, x, n, alpha, vec_ok);
+    else k_axpy16<DT, 1, BS><<<grid, BS, 0, s>>>(y, x, n, alpha, vec_ok);
 }
 
 template <int DT>
@@ -202,30 +205,31 @@ void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype,
     case kFloat32: {
         int64_t items = vec_ok ? std::max<int64_t>(count >> 2, 1) : count;
         const int u = items_per_thread(Kern::kAxpy);
-        unsigned grid = grid_for(items, dev, Kern::kAxpy, u);
         auto* yy = static_cast<float*>(y);
         auto* xx = static_cast<const float*>(x);
-        if (u == 4) k_axpy_f32<4><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
-        else if (u == 2) k_axpy_f32<2><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
-        else k_axpy_f32<1><<<grid, kBlock, 0, s>>>(yy, xx, count, alpha, vec_ok);
+        with_block(threads_per_block(Kern::kAxpy), [&](auto block) {
+            constexpr int BS = decltype(block)::value;
+            const unsigned grid = grid_for(items, dev, Kern::kAxpy, u, BS);
+            if (u == 4) k_axpy_f32<4, BS><<<grid, BS, 0, s>>>(yy, xx, count, alpha, vec_ok);
+            else if (u == 2) k_axpy_f32<2, BS><<<grid, BS, 0, s>>>(yy, xx, count, alpha, vec_ok);
+            else k_axpy_f32<1, BS><<<grid, BS, 0, s>>>(yy, xx, count, alpha, vec_ok);
+            return 0;
+        });
         break;
     }
     case kBFloat16:
     case kFloat16: {
         int64_t items = vec_ok ? std::max<int64_t>(count >> 3, 1) : count;
         const int u = items_per_thread(Kern::kAxpy16);
-        unsigned grid = grid_for(items, dev, Kern::kAxpy16, u);
         auto* yy = static_cast<mfh_u16*>(y);
         auto* xx = static_cast<const mfh_u16*>(x);
-        if (dtype == kBFloat16) {
-            if (u == 4) launch_axpy16<kBFloat16, 4>(grid, s, yy, xx, count, alpha, vec_ok);
-            else if (u == 2) launch_axpy16<kBFloat16, 2>(grid, s, yy, xx, count, alpha, vec_ok);
-            else launch_axpy16<kBFloat16, 1>(grid, s, yy, xx, count, alpha, vec_ok);
-        } else {
-            if (u == 4) launch_axpy16<kFloat16, 4>(grid, s, yy, xx, count, alpha, vec_ok);
-            else if (u == 2) launch_axpy16<kFloat16, 2>(grid, s, yy, xx, count, alpha, vec_ok);
-            else launch_axpy16<kFloat16, 1>(grid, s, yy, xx, count, alpha, vec_ok);
-        }
+        with_block(threads_per_block(Kern::kAxpy16), [&](auto block) {
+            constexpr int BS = decltype(block)::value;
+            const unsigned grid = grid_for(items, dev, Kern::kAxpy16, u, BS);
+            if (dtype == kBFloat16) launch_axpy16<kBFloat16, BS>(u, grid, s, yy, xx, count, alpha, vec_ok);
+            else launch_axpy16<kFloat16, BS>(u, grid, s, yy, xx, count, alpha, vec_ok);
+            return 0;
+        });
         break;
     }
     default:

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "common.hpp"
 #include "codec.hpp"
@@ -20,18 +21,32 @@ namespace mfh {
 typedef mfh_u32 u32x4 __attribute__((ext_vector_type(4)));
 typedef mfh_u32 u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBlock = 256;  // 4 wave64 per workgroup
-// A dispatch counts its work-items in 32 bits: grids stay below 2^32 / kBlock.
-constexpr int64_t kMaxGrid = (int64_t(1) << 32) / kBlock - 1;
+constexpr int kBlock = 256;  // 4 wave64 per workgroup: families without a size setting
 
-// Grid for `items` work items of `per_thread` items each, capped at
-// compute_units * blocks_per_cu(k); threads loop over the rest.
-inline unsigned grid_for(int64_t items, const Device* dev, Kern k, int per_thread = 1)
+// Grid for `items` work items of `per_thread` items each in workgroups of
+// `block` threads, capped at compute_units * blocks_per_cu(k); threads loop
+// over the rest.  A dispatch counts its work-items in 32 bits, so grids stay
+// below 2^32 / block.
+inline unsigned grid_for(int64_t items, const Device* dev, Kern k, int per_thread = 1, int block = kBlock)
 {
     int64_t threads = (items + per_thread - 1) / per_thread;
-    int64_t need = (threads + kBlock - 1) / kBlock;
-    int64_t cap = std::min<int64_t>((int64_t)dev->compute_units * blocks_per_cu(k), kMaxGrid);
+    int64_t need = (threads + block - 1) / block;
+    int64_t cap = std::min<int64_t>((int64_t)dev->compute_units * blocks_per_cu(k), (int64_t(1) << 32) / block - 1);
     return (unsigned)std::max<int64_t>(1, std::min(need, cap));
+}
+
+// Runs f(std::integral_constant<int, BS>{}) with BS the workgroup size
+// `threads` (64, 128 or 256; anything else runs 256), so that a launcher
+// picks the kernel instantiation and its grid from one reading of the
+// family's setting.
+template <typename F>
+int with_block(int threads, F&& f)
+{
+    switch (threads) {
+    case 64: return f(std::integral_constant<int, 64>{});
+    case 128: return f(std::integral_constant<int, 128>{});
+    default: return f(std::integral_constant<int, 256>{});
+    }
 }
 
 int launch_status(const char* what);

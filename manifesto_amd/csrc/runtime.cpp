@@ -156,6 +156,7 @@ struct LaunchCfg {
     std::atomic<int> bpc;
     std::atomic<int> unroll;  // 0: the kernel family chooses (fused: per kernel)
     std::atomic<int> threads;  // threads per workgroup; 0: the family's default
+    unsigned allowed;          // workgroup sizes the family runs: bit k set for 2^k threads
     int default_bpc = 0, default_unroll = 0, default_threads = 0;  // filled from the initial values
 };
 // Large enough that every thread runs exactly one step at any size that
@@ -164,23 +165,34 @@ struct LaunchCfg {
 constexpr int kMaxBlocksPerCu = 1 << 16;
 // Defaults measured on MI355X (256 CUs) with streaming loads and stores:
 // every family runs one-shot, FP8 and Int4 with two items per thread, axpy
-// and the casts with one.  0 for the fused family means "per kernel": each
-// generated kernel carries its shape (see fusion.cpp).  The ahead-of-time
-// families are compiled for 256-thread workgroups; generated kernels take
-// their workgroup size at compile time (default 64, fusion.cpp).
+// and the casts with one.  Workgroup sizes (BASELINE sizes, graph-timed
+// bench, against 256 threads): FP8 128 (+0.4%; 64 is slower), axpy 64
+// (+2.3%; 128 is slower), Int4 256 (128 and 64 lose 2-3%).  0 for the fused
+// family means "per kernel": each generated kernel carries its shape (see
+// fusion.cpp), one-wave workgroups unless set.
+constexpr unsigned kSizes64To256 = (1u << 6) | (1u << 7) | (1u << 8);
+constexpr unsigned kSizes64To1024 = kSizes64To256 | (1u << 9) | (1u << 10);
 LaunchCfg g_cfg[(int)Kern::kCount] = {
-    {"fp8", {kMaxBlocksPerCu}, {2}, {256}}, {"int4", {kMaxBlocksPerCu}, {2}, {256}},
-    {"axpy", {kMaxBlocksPerCu}, {1}, {256}}, {"axpy16", {kMaxBlocksPerCu}, {1}, {256}},
-    {"convert", {kMaxBlocksPerCu}, {1}, {256}}, {"fused", {0}, {0}, {0}},
+    {"fp8", {kMaxBlocksPerCu}, {2}, {128}, kSizes64To256},
+    {"int4", {kMaxBlocksPerCu}, {2}, {256}, 1u << 8},
+    {"axpy", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
+    {"axpy16", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
+    {"convert", {kMaxBlocksPerCu}, {1}, {256}, 1u << 8},
+    {"fused", {0}, {0}, {0}, kSizes64To1024},
 };
 
-// Workgroup sizes a family can run: the ahead-of-time kernels only the one
-// they are compiled for, generated kernels any power of two from one wave
-// (64 threads) to 1024.
 bool threads_supported(const LaunchCfg& c, int threads)
 {
-    if (c.default_threads != 0) return threads == c.default_threads;
-    return threads >= 64 && threads <= 1024 && (threads & (threads - 1)) == 0;
+    return threads > 0 && threads <= 1024 && (threads & (threads - 1)) == 0 &&
+           (c.allowed & (unsigned)threads) != 0;
+}
+
+std::string allowed_sizes(const LaunchCfg& c)
+{
+    std::string text;
+    for (int t = 64; t <= 1024; t *= 2)
+        if (c.allowed & (unsigned)t) text += (text.empty() ? "" : ", ") + std::to_string(t);
+    return text;
 }
 std::once_flag g_cfg_env_once;
 
@@ -323,12 +335,9 @@ int mfh_set_launch_threads(const char* kernel, int32_t threads)
         c->threads = c->default_threads;
         return MFH_OK;
     }
-    if (!threads_supported(*c, threads)) {
-        if (c->default_threads != 0)
-            return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_threads: \"%s\" kernels run %d-thread workgroups only, not %d",
-                        c->name, c->default_threads, threads);
-        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_threads: %d is not a power of two in 64..1024", threads);
-    }
+    if (!threads_supported(*c, threads))
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_set_launch_threads: \"%s\" kernels run workgroups of %s threads, not %d",
+                    c->name, allowed_sizes(*c).c_str(), threads);
     c->threads = threads;
     return MFH_OK;
 }

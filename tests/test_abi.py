@@ -203,7 +203,8 @@ def test_launch_config_set_keep_and_restore():
 
 
 def test_launch_threads_set_keep_restore_and_limits():
-    assert M.get_launch_threads("fp8") == 256
+    # defaults: the measured workgroup size of each family
+    assert [M.get_launch_threads(f) for f in ("fp8", "int4", "axpy", "axpy16", "convert")] == [128, 256, 64, 64, 256]
     assert M.get_launch_threads("fused") == 0  # each generated kernel's default
     k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "threads_default")
     assert "__launch_bounds__(64)" in k.source and "gridDim.x * 64;" in k.source
@@ -215,14 +216,23 @@ def test_launch_threads_set_keep_restore_and_limits():
         k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "threads_256")
         assert "__launch_bounds__(256)" in k.source and "blockIdx.x * 256 + threadIdx.x" in k.source
         for bad in (32, 96, 2048):
-            with pytest.raises(M.MFHError, match="power of two"):
+            with pytest.raises(M.MFHError, match=f"workgroups of 64, 128, 256, 512, 1024 threads, not {bad}"):
                 M.set_launch_threads("fused", bad)
         assert M.get_launch_threads("fused") == 256
     finally:
         M.set_launch_threads("fused", -1)
     assert M.get_launch_threads("fused") == 0
-    M.set_launch_threads("axpy", 256)
-    with pytest.raises(M.MFHError, match="256-thread workgroups only"):
-        M.set_launch_threads("axpy", 128)
+    try:
+        for t in (64, 128, 256):
+            M.set_launch_threads("fp8", t)
+            assert M.get_launch_threads("fp8") == t
+        with pytest.raises(M.MFHError, match="workgroups of 64, 128, 256 threads, not 512"):
+            M.set_launch_threads("axpy", 512)
+        with pytest.raises(M.MFHError, match="workgroups of 256 threads, not 128"):
+            M.set_launch_threads("int4", 128)
+        M.set_launch_threads("int4", 256)
+    finally:
+        M.set_launch_threads("fp8", -1)
+    assert M.get_launch_threads("fp8") == 128
     with pytest.raises(M.MFHError, match="unknown kernel family"):
         M.set_launch_threads("nope", 64)

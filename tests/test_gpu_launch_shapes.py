@@ -1,8 +1,9 @@
 """GPU tests of launch shapes: every streaming kernel family gives the same
 bits under small capped grids (one workgroup per CU, so each workgroup walks
 many chunks, with 1, 2 and 4 items per thread) as under its default one-shot
-grid, at sizes with ragged tails and on unaligned buffers; generated kernels
-also under workgroups of 128, 256 and 1024 threads.  The default shape
+grid, at sizes with ragged tails and on unaligned buffers, at every
+workgroup size the family runs (FP8 and axpy 64, 128 and 256 threads;
+generated kernels also 1024).  The default shape
 itself is pinned against the oracle here and in the per-family test files."""
 import numpy as np
 import pytest
@@ -15,6 +16,8 @@ from gpu_util import empty_dev, log, stream, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 1), (1, 2), (1, 4), (3, 2), (-1, -1)]  # (workgroups per CU, items per thread); -1: default
+# workgroup sizes each ahead-of-time family runs besides its default
+THREADS = {"fp8": (64, 128, 256), "axpy": (64, 128, 256), "axpy16": (64, 128, 256)}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -23,19 +26,26 @@ def gpu():
     yield
     for fam in ("fp8", "int4", "axpy", "axpy16", "convert", "fused"):
         M.set_launch_config(fam, -1, -1)
-    M.set_launch_threads("fused", -1)
+        M.set_launch_threads(fam, -1)
 
 
 def under_shapes(family, run):
-    """Runs `run()` (which returns host bytes) under every shape of SHAPES and
-    checks that all results equal the default shape's."""
+    """Runs `run()` (which returns host bytes) under every shape of SHAPES, at
+    every workgroup size of THREADS, and checks that all results equal the
+    default shape's."""
     M.set_launch_config(family, -1, -1)
+    M.set_launch_threads(family, -1)
     want = run()
-    for bpc, u in SHAPES:
-        M.set_launch_config(family, bpc, u)
-        got = run()
-        assert got == want, f"{family}: launch shape ({bpc}, {u}) changed the result"
-    M.set_launch_config(family, -1, -1)
+    try:
+        for threads in THREADS.get(family, (-1,)):
+            M.set_launch_threads(family, threads)
+            for bpc, u in SHAPES:
+                M.set_launch_config(family, bpc, u)
+                got = run()
+                assert got == want, f"{family}: launch shape ({bpc}, {u}) at {threads} threads changed the result"
+    finally:
+        M.set_launch_config(family, -1, -1)
+        M.set_launch_threads(family, -1)
     return want
 
 
