@@ -120,6 +120,8 @@ int tensor_ok(const mfh_tensor* t)
     return MFH_OK;
 }
 
+}  // namespace
+
 // NewShape (tensor/shape.go:32-60): negative dimensions and overflowing
 // products are invalid; any zero dimension makes the element count zero.
 int make_shape(const int64_t* shape, int32_t rank, std::vector<int64_t>* dims, int64_t* elements)
@@ -143,6 +145,8 @@ int make_shape(const int64_t* shape, int32_t rank, std::vector<int64_t>* dims, i
     *elements = zero ? 0 : n;
     return MFH_OK;
 }
+
+namespace {
 
 int ensure_staging(BackendState& s)
 {

@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "../../include/mfh_backend.h"
 #include "common.hpp"
@@ -27,6 +28,11 @@ struct Source {
     virtual ~Source() = default;
     virtual int read(void* dst, size_t offset, size_t len) = 0;
 };
+
+// NewShape (tensor/shape.go:32-60): the dimensions and element count of
+// `shape`, or MFH_ERR_SHAPE_INVALID for a negative dimension or an element
+// count past INT64_MAX.
+int make_shape(const int64_t* shape, int32_t rank, std::vector<int64_t>* dims, int64_t* elements);
 
 // Checks the shape against `n_bytes` of plan.src, allocates the stored
 // tensor and streams the source through the backend's staging ring (waiting

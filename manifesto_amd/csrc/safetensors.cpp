@@ -12,6 +12,7 @@
 
 #include <cctype>
 #include <cerrno>
+#include <cstdint>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -378,10 +379,12 @@ int entry_range(const mfh_safetensors& f, const Entry& e, int64_t* at, size_t* l
     if (e.end < e.begin || e.begin < 0)
         return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors read \"%s\": bad data_offsets [%lld, %lld]", e.name.c_str(),
                     (long long)e.begin, (long long)e.end);
+    // compared against the bytes after the header first, so that offsets
+    // near INT64_MAX cannot overflow the sums below
+    if (e.end > f.file_size - f.data_base)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors read \"%s\": unexpected EOF", e.name.c_str());
     *at = f.data_base + e.begin;
     *len = (size_t)(e.end - e.begin);
-    if (*at + (int64_t)*len > f.file_size)
-        return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors read \"%s\": unexpected EOF", e.name.c_str());
     return MFH_OK;
 }
 
@@ -541,12 +544,15 @@ int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_back
         if (group <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors: group must be positive, got %lld", (long long)group);
         if (se->dtype != kFloat32 && se->dtype != kFloat16 && se->dtype != kBFloat16)
             return fail(MFH_ERR_DTYPE_UNSUPPORTED, "safetensors: scales \"%s\" are not F32/F16/BF16", se->name.c_str());
-        int64_t elements = 1;
-        for (int64_t d : e->shape) elements *= d;
+        int64_t elements;
+        std::vector<int64_t> dims;
+        MFH_TRY(make_shape(e->shape.data(), (int32_t)e->shape.size(), &dims, &elements));
         int64_t s_at;
         size_t s_len;
         MFH_TRY(entry_range(*file, *se, &s_at, &s_len));
-        const size_t need = (size_t)((elements + group - 1) / group) * dtype_size(se->dtype);
+        const int64_t groups = elements / group + (elements % group != 0);
+        const size_t ssize = (size_t)dtype_size(se->dtype);
+        const size_t need = (uint64_t)groups <= SIZE_MAX / ssize ? (size_t)groups * ssize : SIZE_MAX;
         if (s_len != need)
             return fail(MFH_ERR_SHAPE_MISMATCH, "safetensors: scales \"%s\" hold %zu bytes, %lld elements in groups of "
                         "%lld need %zu", se->name.c_str(), s_len, (long long)elements, (long long)group, need);

@@ -114,6 +114,14 @@ def test_truncated_file_and_out_of_range_reads(tmp_path):
         f.read("a")
     with pytest.raises(M.MFHError, match='safetensors read "b": bad data_offsets'):
         f.read("b")
+    # offsets near INT64_MAX: an EOF, not a wrapped sum that reads elsewhere
+    big = (1 << 63) - 1
+    g = SafeTensorsFile(write_raw(tmp_path / "big.safetensors",
+                                  {"c": {"dtype": "U8", "shape": [1], "data_offsets": [big - 1, big]},
+                                   "d": {"dtype": "U8", "shape": [1], "data_offsets": [0, big]}}, b"\0" * 4))
+    for name in ("c", "d"):
+        with pytest.raises(M.MFHError, match=f'safetensors read "{name}": unexpected EOF'):
+            g.read(name)
     with pytest.raises(M.MFHError):
         SafeTensorsFile(tmp_path / "missing.safetensors")
 
