@@ -223,35 +223,41 @@ MFH_MATH float mfh_sigmoid_fast(float v, bool& rare)
     return (float)mfh_fma(r, mfh_fma(-den, r, 1.0), r);
 }
 
-// silu(v) = v / (1 + e^-v); below -87 (and -Inf, NaN) the f64 form, where the
-// result underflows to denormals and -0, and +Inf, which the f64 form maps to
-// +Inf (every v that the clamp to [-87, FLT_MAX] changes).
+// silu(v) = v / (1 + e^-v).  One clamp to [-87, 200] serves the computation
+// and the rare test: every v it changes takes the f64 form, i.e. v < -87 (and
+// -Inf), where the result underflows to denormals and -0, NaN, and v > 200
+// (+Inf included), where the result is v itself (the quotient's residual step
+// would turn +Inf into NaN).
 MFH_MATH float mfh_silu_fast(float v, bool& rare)
 {
     int k;
-    const float p = mfh_exp_core(-mfh_med3f(v, -87.0f, 104.0f), &k);
-    rare |= mfh_med3f(v, -87.0f, 3.40282347e38f) != v;
+    const float m = mfh_med3f(v, -87.0f, 200.0f);
+    rare |= m != v;
+    const float p = mfh_exp_core(-m, &k);
     return mfh_div_one_plus(v, p, k);
 }
 
 // Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
 // t = -2 inner log2(e) = d w, w = KA + KB d^2, formed and reduced in f64 (the
 // cubic needs more than f32's 24 bits where E is large) and 2^f evaluated in
-// f32.  Within 2 f32 ulps of the reference over every f32 input.  Above
-// v = 14 the reference's tanh is exactly 1 in f64 and gelu(v) = v, which the
-// clamped d reproduces.  Below v = -4.9 (inner < -9.3) the reference's
-// 1 + tanh cancels in f64, so that rare range, +Inf and NaN (every v that the
-// clamp to [-4.9, FLT_MAX] changes) take the reference form itself.
+// f32.  Within 2 f32 ulps of the reference over every f32 input.  One clamp
+// to [-4.9, 1024] serves the computation and the rare test: every v it
+// changes takes the reference form, i.e. v < -4.9 (inner < -9.3), where the
+// reference's 1 + tanh cancels in f64, NaN, and v > 1024 (+Inf included).
+// Inside the clamp |t| < 1.2e8, so k fits the int32 of the round-to-integer
+// trick, and above v = 14 E underflows to 0 and the result is v, as the
+// reference's tanh is exactly 1 there.
 #define MFH_GELU_KA (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_LOG2E_D)
 #define MFH_GELU_KB (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_GELU_A_D * MFH_LOG2E_D)
 MFH_MATH float mfh_gelu_fast(float v, bool& rare)
 {
-    const double d = (double)mfh_med3f(v, -5.0f, 14.0f);
+    const float c = mfh_med3f(v, -4.9f, 1024.0f);
+    rare |= c != v;
+    const double d = (double)c;
     const double w = mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA);
     const double tk = mfh_fma(w, d, MFH_ROUND_INT_D);
     const double kd = tk - MFH_ROUND_INT_D;
     const float p = mfh_exp2_poly((float)mfh_fma(w, d, -kd));
-    rare |= mfh_med3f(v, -4.9f, 3.40282347e38f) != v;
     return mfh_div_one_plus_short(v, p, mfh_low_int(tk));
 }
 
