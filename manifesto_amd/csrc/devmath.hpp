@@ -12,8 +12,10 @@
 //   e^a:          Cody & Waite reduction a = k ln2 + r (ln2 split into a
 //                 16-bit head and an f32 tail), e^r by a degree-6 polynomial
 //                 (constants from gen_exp_poly.py), then scaled by 2^k.
-//   2^f:          for |f| <= 1/2 a degree-6 polynomial (gen_exp_poly.py),
-//                 used where the argument is formed and reduced in f64.
+//   2^f:          for |f| <= 1/2 the hardware v_exp_f32 where the argument
+//                 is formed and reduced in f64 (gelu: within budget over
+//                 every f32 input, checked on the GPU), or a degree-8 f64
+//                 polynomial (sigmoid, gen_exp_poly.py).
 //   n * sigmoid(z) = n / (1 + E), E = e^-z, with z clamped (v_med3) to the
 //                 range where E is a finite f32, the exact tail of 1 + E
 //                 recovered by Fast2Sum, and the quotient corrected by one
@@ -42,6 +44,10 @@
 #define mfh_ldexp(x, k) std::ldexp((double)(x), (int)(k))
 #define mfh_rcpf(x) (1.0f / (float)(x))
 #define mfh_rcp(x) (1.0 / (double)(x))
+// Host stand-in for the hardware 2^x (v_exp_f32): libm's exp2f, which is more
+// accurate, so the host sweep does not model gelu's device error; the GPU
+// tests check the device gelu over every f32 input instead.
+#define mfh_exp2f_hw(x) std::exp2((float)(x))
 #define mfh_tanh_f64(x) std::tanh((double)(x))
 #define mfh_exp_f64(x) std::exp((double)(x))
 #define mfh_log_f64(x) std::log((double)(x))
@@ -65,6 +71,7 @@ extern "C" __device__ double __ocml_log_f64(double);
 #define mfh_ldexp(x, k) __builtin_amdgcn_ldexp((x), (k))
 #define mfh_rcpf(x) __builtin_amdgcn_rcpf(x)
 #define mfh_rcp(x) __builtin_amdgcn_rcp(x)
+#define mfh_exp2f_hw(x) __builtin_amdgcn_exp2f(x)
 #define mfh_tanh_f64(x) __ocml_tanh_f64(x)
 #define mfh_exp_f64(x) __ocml_exp_f64(x)
 #define mfh_log_f64(x) __ocml_log_f64(x)
@@ -97,18 +104,6 @@ MFH_MATH float mfh_exp_poly(float r)
     q = mfh_fmaf(q, r, 0.4999999403953552f);     // 0x3efffffe
     q = mfh_fmaf(q, r, 1.0f);
     return mfh_fmaf(q, r, 1.0f);
-}
-
-// 2^f for |f| <= 1/2: 1 + f(c1 + f(c2 + ... + f c6)), within 0.94 f32 ulp.
-MFH_MATH float mfh_exp2_poly(float f)
-{
-    float q = 0.00015370704932138324f;           // 0x39212c6c
-    q = mfh_fmaf(q, f, 0.0013399848248809576f);  // 0x3aafa26e
-    q = mfh_fmaf(q, f, 0.009618373587727547f);   // 0x3c1d9662
-    q = mfh_fmaf(q, f, 0.05550329014658928f);    // 0x3d63576b
-    q = mfh_fmaf(q, f, 0.24022647738456726f);    // 0x3e75fdee
-    q = mfh_fmaf(q, f, 0.6931471824645996f);     // 0x3f317218
-    return mfh_fmaf(q, f, 1.0f);
 }
 
 // 2^f for |f| <= 1/2 in f64: degree 8, relative error below 2^-39.9 with
@@ -239,8 +234,11 @@ MFH_MATH float mfh_silu_fast(float v, bool& rare)
 
 // Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
 // t = -2 inner log2(e) = d w, w = KA + KB d^2, formed and reduced in f64 (the
-// cubic needs more than f32's 24 bits where E is large) and 2^f evaluated in
-// f32.  Within 2 f32 ulps of the reference over every f32 input.  One clamp
+// cubic needs more than f32's 24 bits where E is large) and 2^f, |f| <= 1/2,
+// evaluated by the hardware v_exp_f32 (one instruction for the polynomial's
+// six; measured on MI355X: the gelu chain +2-3%).  Within 2 f32 ulps of the
+// reference over every f32 input (measured on the device: 96.4% identical,
+// the same as with the polynomial).  One clamp
 // to [-4.9, 1024] serves the computation and the rare test: every v it
 // changes takes the reference form, i.e. v < -4.9 (inner < -9.3), where the
 // reference's 1 + tanh cancels in f64, NaN, and v > 1024 (+Inf included).
@@ -257,7 +255,7 @@ MFH_MATH float mfh_gelu_fast(float v, bool& rare)
     const double w = mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA);
     const double tk = mfh_fma(w, d, MFH_ROUND_INT_D);
     const double kd = tk - MFH_ROUND_INT_D;
-    const float p = mfh_exp2_poly((float)mfh_fma(w, d, -kd));
+    const float p = mfh_exp2f_hw((float)mfh_fma(w, d, -kd));
     return mfh_div_one_plus_short(v, p, mfh_low_int(tk));
 }
 

@@ -1,0 +1,79 @@
+"""Every f32 input through the device's fast Sigmoid, Silu and Gelu nodes.
+
+The fast forms run on the GPU over all 2^32 f32 bit patterns (in chunks)
+beside the MFH_FUSION_PRECISE forms, which restate the reference's f64
+formulas (codegen/cpu.go:186-200) and round once, so they are within one f32
+ulp of the oracle (they differ only where an f64 result sits at an f32
+rounding tie that two f64 libraries round differently).  NaN positions must
+match.  Every input where the fast form is `tol` or more ulps from the
+precise form is then checked against the CPU oracle itself, which it must be
+within `tol` of; every other input is within tol - 1 of the precise form and
+so within tol of the oracle.  This covers the device math the host sweep
+(test_devmath_host.py) cannot model: the hardware reciprocal, and gelu's
+hardware v_exp_f32.
+"""
+import numpy as np
+import pytest
+
+import manifesto_amd as M
+import oracle as O
+
+from gpu_util import log, stream
+
+pytestmark = pytest.mark.gpu
+
+CHUNK = 1 << 28
+TOL = {O.N_SIGMOID: 1, O.N_SILU: 2, O.N_GELU: 2}
+
+
+def ulp_key(bits):
+    """Monotone integer key of f32 bit patterns (int32 or int64 tensor/array)."""
+    import torch
+    if isinstance(bits, np.ndarray):
+        b = bits.astype(np.int64)
+        return np.where(b < 0, -(b & 0x7FFFFFFF), b)
+    b = bits.to(torch.int64)
+    return torch.where(b < 0, -(b & 0x7FFFFFFF), b)
+
+
+@pytest.mark.parametrize("node", sorted(TOL))
+def test_fast_activation_every_f32_input(node):
+    import torch
+    M.init(0)
+    tol = TOL[node]
+    nodes = O.flatten((node, ("in", 0)))
+    ops = [(M.FLOAT32, M.OPERAND_FULL, 0)]
+    fast_k = M.FusedKernel(nodes, ops, M.FLOAT32, f"exh_fast_{node}")
+    precise_k = M.FusedKernel(nodes, ops, M.FLOAT32, f"exh_precise_{node}", M.FUSION_PRECISE)
+    fast = torch.empty(CHUNK, dtype=torch.int32, device="cuda")
+    precise = torch.empty(CHUNK, dtype=torch.int32, device="cuda")
+    hist = torch.zeros(tol + 3, dtype=torch.int64, device="cuda")
+    candidates = []
+    for c in range((1 << 32) // CHUNK):
+        log(f"node {node}: bit patterns [{c * CHUNK:#x}, {(c + 1) * CHUNK:#x})")
+        x = (torch.arange(c * CHUNK, (c + 1) * CHUNK, dtype=torch.int64, device="cuda") - (1 << 31)).to(torch.int32)
+        fast_k.launch([x.data_ptr()], fast.data_ptr(), CHUNK, stream())
+        precise_k.launch([x.data_ptr()], precise.data_ptr(), CHUNK, stream())
+        nan_f = (fast & 0x7FFFFFFF) > 0x7F800000
+        nan_p = (precise & 0x7FFFFFFF) > 0x7F800000
+        bad = int((nan_f != nan_p).sum())
+        assert bad == 0, f"node {node}: {bad} NaN mismatches in chunk {c}"
+        d = (ulp_key(fast) - ulp_key(precise)).abs()
+        d = torch.where(nan_f, torch.zeros_like(d), d)
+        hist += torch.bincount(d.clamp(max=tol + 2), minlength=tol + 3)
+        idx = torch.nonzero(d >= tol).flatten()
+        if idx.numel():
+            candidates.append(torch.stack([x[idx], fast[idx]], 1).cpu().numpy())
+    h = hist.tolist()
+    log(f"node {node}: ulps from the precise form {h} (last bin: {tol + 2} or more)")
+    assert sum(h) == 1 << 32
+    assert h[0] / (1 << 32) > 0.95, f"node {node}: only {h[0] / (1 << 32):.4f} identical to the precise form"
+    if not candidates:
+        return
+    a = np.concatenate(candidates)
+    want = O.eval_unary(node, a[:, 0].view(np.float32)).view(np.int32)
+    dd = np.abs(ulp_key(a[:, 1]) - ulp_key(want))
+    log(f"node {node}: {a.shape[0]} inputs {tol}+ ulps from the precise form, at most {int(dd.max())} from the oracle")
+    i = int(np.argmax(dd))
+    assert dd.max() <= tol, (f"node {node}: {int(dd.max())} ulp from the oracle at x bits {a[i, 0] & 0xFFFFFFFF:#x}: "
+                             f"got {a[i, 1] & 0xFFFFFFFF:#x} want {want[i] & 0xFFFFFFFF:#x}")
