@@ -328,15 +328,15 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // dispatch order).  Measured on MI355X against grid-stride loops at 4-24
     // blocks per CU: +11% on the SwiGLU chain and +9% on the f16 gelu chain;
     // a no-compute 2:1 read:write stream gains 17% the same way.  One item per
-    // thread, except where the fast element math mixes f32 with f64 work
-    // (Gelu, Sigmoid): two items per thread give the gelu chain +5% and the
-    // sigmoid chain 0-3%, while SwiGLU, Silu and add/mul chains lose 2-4% and
-    // the precise (f64 library) forms gain nothing.  Workgroups of one wave
-    // (kFusedThreads).  mfh_set_launch_config("fused", ...) and
+    // thread, except where the fast element math is mostly f64 (Sigmoid): two
+    // items per thread give a sigmoid chain 0-3%, while SwiGLU, Silu, add/mul
+    // chains and (since its 2^f runs on v_exp_f32) the gelu chain lose 2-6%
+    // and the precise (f64 library) forms gain nothing.  Workgroups of one
+    // wave (kFusedThreads).  mfh_set_launch_config("fused", ...) and
     // mfh_set_launch_threads("fused", ...) override these.
     bool f64_fast = false;
     for (const mfh_ast_node& node : list)
-        if (!precise && (node.type == kNodeGelu || node.type == kNodeSigmoid)) f64_fast = true;
+        if (!precise && node.type == kNodeSigmoid) f64_fast = true;
     const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : f64_fast ? 2 : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
     const int block = threads_per_block(Kern::kFused) > 0 ? threads_per_block(Kern::kFused) : kFusedThreads;

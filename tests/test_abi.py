@@ -81,8 +81,10 @@ def test_emit_hip_broadcast_operands():
     assert "const float x1 = mfh_ld1_f16(p1, (i % 4096LL));" in src  # element loop decodes
     assert "const float s2 = mfh_ld1_f32(p2, 0);" in src
     assert "mfh_gelu_fast(t1, q)" in src and "mfh_gelu(t1)" in src
-    # gelu mixes f32 with f64 work: two items per thread by default
-    assert "8 elements per item, 2 item(s) per thread" in src
+    # one item per thread; only a Sigmoid (mostly f64 work) takes two by default
+    assert "8 elements per item, 1 item(s) per thread" in src
+    sig = M.FusedKernel(flatten((N_SIGMOID, ("in", 0))), [(M.FLOAT16, M.OPERAND_FULL, 0)], M.FLOAT16, "sig")
+    assert "8 elements per item, 2 item(s) per thread" in sig.source
     precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)
     assert "mfh_gelu_ref(" in precise.source and "_fast(" not in precise.source.split("EmitHIP")[1]
     assert "if (q)" not in precise.source and "1 item(s) per thread" in precise.source
