@@ -252,6 +252,90 @@ __global__ __launch_bounds__(kBlock) void k_convert16_vec(const void* __restrict
     }
 }
 
+// Byte size of an unpacked numeric dtype, at compile time.
+template <int DT>
+constexpr int size_of()
+{
+    return DT == kFloat64 || DT == kInt64 || DT == kUint64 ? 8
+           : DT == kFloat32 || DT == kInt32 || DT == kUint32 ? 4
+           : DT == kFloat16 || DT == kBFloat16 || DT == kInt16 || DT == kUint16 ? 2 : 1;
+}
+
+// BytesToFloat32 (decode_at) of element k of a register copy of consecutive
+// elements of dtype IN, `w` holding them as little-endian dwords.
+template <int IN>
+MFH_DEV float decode_reg(const mfh_u32* w, int k)
+{
+    constexpr int S = size_of<IN>();
+    if constexpr (S == 8) {
+        const mfh_u64 b = (mfh_u64)w[2 * k] | ((mfh_u64)w[2 * k + 1] << 32);
+        if constexpr (IN == kFloat64) return f64_to_f32(__builtin_bit_cast(double, b));
+        else if constexpr (IN == kInt64) return (float)(double)(long long)b;
+        else return (float)(double)b;
+    } else if constexpr (S == 4) {
+        if constexpr (IN == kFloat32) return mfh_f32(w[k]);
+        else if constexpr (IN == kInt32) return (float)(double)(int)w[k];
+        else return (float)(double)w[k];
+    } else if constexpr (S == 2) {
+        const mfh_u32 h = (w[k >> 1] >> ((k & 1) * 16)) & 0xffffu;
+        if constexpr (IN == kFloat16) return mfh_f16_to_f32(h);
+        else if constexpr (IN == kBFloat16) return mfh_bf16_to_f32(h);
+        else if constexpr (IN == kInt16) return (float)(short)h;
+        else return (float)h;
+    } else {
+        const mfh_u32 b = (w[k >> 2] >> ((k & 3) * 8)) & 0xffu;
+        if constexpr (IN == kInt8) return (float)(signed char)b;
+        else return (float)b;
+    }
+}
+
+// Any unpacked numeric dtype -> {f32, bf16, f16}, one 16-byte store per item
+// (4 elements for f32 output, 8 for 16-bit) and the item's source bytes read
+// with 4-, 8- or 16-byte loads (up to four 16-byte loads for 8-byte
+// sources): the element loop's 1-, 2- or 4-byte accesses moved 1.4-3.8 TB/s,
+// and this layout, like every streaming kernel here, writes 1 KiB per wave
+// store instruction.  Loads are non-temporal when an item reads at least as
+// many bytes as it writes.  Elements past the last whole item run the
+// element loop.
+template <int IN, int OUT>
+__global__ __launch_bounds__(kBlock) void k_convert_vec(const void* __restrict__ in, void* __restrict__ out,
+                                                        mfh_i64 n)
+{
+    constexpr int E = OUT == kFloat32 ? 4 : 8;      // elements per item
+    constexpr int B = E * size_of<IN>();            // source bytes per item
+    constexpr int W = B / 4;                        // source dwords per item
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 nitems = n / E;
+    u32x4* dst = reinterpret_cast<u32x4*>(out);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
+        mfh_u32 w[W];
+        const char* src = static_cast<const char*>(in) + v * B;
+        if constexpr (B >= 16) {
+#pragma unroll
+            for (int q = 0; q < B / 16; q++) {
+                const u32x4 x = load_nt(reinterpret_cast<const u32x4*>(src) + q);
+                w[4 * q] = x[0], w[4 * q + 1] = x[1], w[4 * q + 2] = x[2], w[4 * q + 3] = x[3];
+            }
+        } else if constexpr (B == 8) {
+            const u32x2 x = *reinterpret_cast<const u32x2*>(src);
+            w[0] = x[0], w[1] = x[1];
+        } else {
+            w[0] = *reinterpret_cast<const mfh_u32*>(src);
+        }
+        u32x4 o;
+        if constexpr (OUT == kFloat32) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) o[k] = mfh_bits(decode_reg<IN>(w, k));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++) o[k] = encode_pair<OUT>(decode_reg<IN>(w, 2 * k), decode_reg<IN>(w, 2 * k + 1));
+        }
+        store_nt(&dst[v], o);
+    }
+    for (mfh_i64 i = nitems * E + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        store_one<OUT>(out, i, encode_one<OUT>(decode_at<IN>(in, i)));
+}
+
 // f32 -> 16-bit storage, 4 elements per item (16-byte load, 8-byte store).
 template <int OUT>
 __global__ __launch_bounds__(kBlock) void k_narrow_f32_vec(const u32x4* __restrict__ in,
@@ -461,10 +545,17 @@ struct ConvertLaunch {
                 return launch_status("k_narrow_f32_vec");
             }
         }
-        unsigned grid = grid_for(n, dev, Kern::kConvert);
+        // every other source: whole 16-byte output items when both buffers
+        // are aligned for them, else the element loop
+        const int src_size = dtype_size(in_dt);
+        const bool vec = src_size > 0 && aligned(in, (unsigned)std::min(per * src_size, 16)) && aligned16(out);
+        unsigned grid = vec ? grid_for(std::max<int64_t>(n / per, 1), dev, Kern::kConvert) : grid_for(n, dev, Kern::kConvert);
         switch (in_dt) {
 #define MFH_CONVERT_CASE(DT) \
-    case DT: k_convert<DT, OUT><<<grid, kBlock, 0, stream>>>(in, out, n); break;
+    case DT:                                                                              \
+        if (vec) k_convert_vec<DT, OUT><<<grid, kBlock, 0, stream>>>(in, out, n);         \
+        else k_convert<DT, OUT><<<grid, kBlock, 0, stream>>>(in, out, n);                 \
+        break;
         MFH_CONVERT_CASE(kFloat64)
         MFH_CONVERT_CASE(kFloat32)
         MFH_CONVERT_CASE(kFloat16)

@@ -206,22 +206,27 @@ def test_convert_f32_narrowing_rounding_classes(out_dt):
 
 
 @pytest.mark.parametrize("in_dt, np_dt", [
-    (O.FLOAT64, np.float64), (O.INT8, np.int8), (O.INT16, np.int16), (O.INT32, np.int32),
-    (O.INT64, np.int64), (O.UINT8, np.uint8), (O.UINT16, np.uint16), (O.UINT32, np.uint32),
-    (O.UINT64, np.uint64)])
-@pytest.mark.parametrize("out_dt", [O.FLOAT32, O.BFLOAT16])
-def test_convert_other_numeric_dtypes(in_dt, np_dt, out_dt):
-    rng = np.random.default_rng(in_dt)
-    raw = rng.integers(0, 256, size=8 * 50001, dtype=np.uint8)
-    a = raw.view(np_dt)[:50001]
-    if in_dt == O.FLOAT64:
+    (O.FLOAT64, np.float64), (O.FLOAT32, np.float32), (O.INT8, np.int8), (O.INT16, np.int16),
+    (O.INT32, np.int32), (O.INT64, np.int64), (O.UINT8, np.uint8), (O.UINT16, np.uint16),
+    (O.UINT32, np.uint32), (O.UINT64, np.uint64)])
+@pytest.mark.parametrize("out_dt", [O.FLOAT32, O.BFLOAT16, O.FLOAT16])
+@pytest.mark.parametrize("n, pad", [(50001, 0), (50001, 1), (7, 0), (3, 0)])
+def test_convert_other_numeric_dtypes(in_dt, np_dt, out_dt, n, pad):
+    # aligned sources take whole 16-byte output items plus an element tail;
+    # a source one byte off its alignment runs the element loop
+    rng = np.random.default_rng(in_dt * 7 + n)
+    raw = rng.integers(0, 256, size=8 * n, dtype=np.uint8)
+    a = raw.view(np_dt)[:n]
+    if in_dt == O.FLOAT64 and n > 10:
         a = np.concatenate([a, np.array([np.nan, -np.inf, 1e300, -1e-320, 0.1], dtype=np.float64)])
-    src, sp = to_dev(a)
+    if in_dt == O.FLOAT32 and n > 10:  # NaN payloads and denormals pass through unchanged
+        a = np.concatenate([a, np.array([0x7FC00001, 0xFF800000, 0x00000001, 0x80000000], np.uint32).view(np.float32)])
+    src, sp = to_dev(a, pad=pad)
     out, op = empty_dev(a.size * OUT_SIZE[out_dt])
     M.convert(op, out_dt, sp, in_dt, a.size, stream())
     got = to_host(out, OUT_NP[out_dt])
-    conv = O.bytes_to_f32 if out_dt == O.FLOAT32 else O.bytes_to_bf16
-    bits_equal(got, conv(in_dt, a), f"convert {in_dt}->{out_dt}")
+    conv = {O.FLOAT32: O.bytes_to_f32, O.BFLOAT16: O.bytes_to_bf16, O.FLOAT16: O.bytes_to_f16}[out_dt]
+    bits_equal(got, conv(in_dt, a), f"convert {in_dt}->{out_dt} n={n} pad={pad}")
 
 
 @pytest.mark.parametrize("fmt", [O.F8E4M3, O.F8E5M2])
