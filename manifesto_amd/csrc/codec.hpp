@@ -86,33 +86,33 @@ MFH_DEV mfh_u32 mfh_e5m2_bits(mfh_u32 code)
 template <int MB, int BIAS, int EMAX, int MINSUB, mfh_u32 SAT, mfh_u32 MAXF>
 MFH_DEV mfh_u32 mfh_fp8_encode(float value)
 {
-    const mfh_u32 u = mfh_bits(value);
-    const mfh_u32 sign = (u >> 24) & 0x80u;
-    const mfh_u32 a = u & 0x7fffffffu;
-    if (a > 0x7f800000u) return 0x7fu;                 // NaN
-    if (a > MAXF) return sign | SAT;                   // Inf and above the largest finite value
-    if (a == 0u) return sign;
-    mfh_i32 e = (mfh_i32)(a >> 23) - 127 + BIAS;
-    const mfh_u32 mant = a & 0x7fffffu;
+    // The same cases, computed for every element without a branch (the
+    // per-case branches of a direct transcription diverge within a wave):
     constexpr mfh_u32 drop = 23 - MB;                  // 20 (E4M3) or 21 (E5M2)
-    if (e <= 0) {
-        if (e < MINSUB) return sign;
-        const mfh_u32 full = mant | 0x800000u;
-        const mfh_u32 shift = drop - (mfh_u32)e;       // 20 - e / 21 - e, at most 24
-        const mfh_u32 t = full >> shift;
-        const mfh_u32 rest = full & ((1u << shift) - 1u), half = 1u << (shift - 1u);
-        const mfh_u32 r = t + ((rest > half) || (rest == half && (t & 1u)) ? 1u : 0u);
-        return sign | (r >= (1u << MB) ? (1u << MB) : r);
-    }
-    if (e >= EMAX) return sign | SAT;
-    mfh_u32 m = mant >> drop;
-    const mfh_u32 rest = mant & ((1u << drop) - 1u), half = 1u << (drop - 1u);
-    m += (rest > half) || (rest == half && (m & 1u)) ? 1u : 0u;
-    if (m >= (1u << MB)) {
-        m = 0u;
-        if (++e >= EMAX) return sign | SAT;
-    }
-    return sign | ((mfh_u32)e << MB) | m;
+    constexpr mfh_u32 kNormal = (128u - BIAS) << 23;   // |x| from here on has biased e >= 1
+    const mfh_u32 u = mfh_bits(value);
+    const mfh_u32 a = u & 0x7fffffffu;
+    // e >= 1: the exponent and top MB mantissa bits rounded to nearest even
+    // by one integer add; a carry out of the mantissa bumps the exponent,
+    // which is the reference's "m >= 1 << MB: m = 0, e++" step
+    const mfh_u32 r = a + ((1u << (drop - 1u)) - 1u) + ((a >> drop) & 1u);
+    const mfh_u32 normal = (r >> drop) - ((127u - BIAS) << MB);
+    // e <= 0: the hidden-bit mantissa shifted right by drop - e and rounded
+    // to nearest even is |x| * 2^(BIAS + MB) rounded to an integer (exact
+    // scaling, then the 2^23 round-to-integer add); below biased e = MINSUB
+    // zero; a result reaching 1 << MB stays there
+    constexpr float kScale = (float)(1u << (BIAS + MB));
+    constexpr float kZeroBelow = MINSUB + MB >= 0 ? (float)(1u << (MINSUB + MB >= 0 ? MINSUB + MB : 0))
+                                                  : 1.0f / (float)(1u << (MINSUB + MB < 0 ? -(MINSUB + MB) : 0));
+    const float y = mfh_f32(a) * kScale;
+    const mfh_u32 t = mfh_bits((y < kZeroBelow ? 0.0f : y) + 8388608.0f) - 0x4b000000u;
+    const mfh_u32 sub = t < (1u << MB) ? t : (1u << MB);
+    mfh_u32 code = a < kNormal ? sub : normal;
+    // above the largest finite value, Inf, and a rounded biased exponent at
+    // the top field value saturate
+    code = (a > MAXF || r >= ((mfh_u32)(EMAX + 127 - BIAS) << 23)) ? SAT : code;
+    code |= (u >> 24) & 0x80u;
+    return a > 0x7f800000u ? 0x7fu : code;             // NaN, whatever its sign
 }
 
 MFH_DEV mfh_u32 mfh_e4m3_encode(float v) { return mfh_fp8_encode<3, 7, 15, -3, 0x7eu, 0x43e00000u>(v); }

@@ -418,9 +418,78 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ 
         out[i] = (mfh_u8)encode_fp8<FMT>(decode_any<IN>(in, i));
 }
 
+// Unpacked numeric dtype -> FP8 with every load instruction of a wave
+// reading 1 KiB contiguously: a wave takes chunks of 4 KiB of source, lane l
+// the 16-byte pieces l, l + 64, l + 128 and l + 192 of its chunk, and writes
+// the 16 / size codes of each piece next to its neighbours' (16-, 8-, 4- or
+// 2-byte stores).  One lane taking 16 consecutive elements instead (64
+// bytes of f32) spreads each load instruction over 4 KiB: f32 -> e4m3 ran
+// at 4.4 TB/s that way.  Elements past the last whole chunk run the element
+// loop.
+template <int IN, int FMT>
+__global__ __launch_bounds__(kBlock) void k_encode_fp8_wave(const void* __restrict__ in, mfh_u8* __restrict__ out,
+                                                            mfh_i64 n)
+{
+    constexpr int S = size_of<IN>();
+    constexpr int P = 16 / S;          // elements (and output bytes) per 16-byte piece
+    constexpr int kPieces = 4;         // pieces per lane per chunk
+    constexpr mfh_i64 kChunk = 64 * kPieces * P;  // elements per wave chunk
+    const int lane = (int)threadIdx.x & 63;
+    const mfh_i64 waves = (mfh_i64)gridDim.x * (kBlock / 64);
+    const mfh_i64 nchunks = n / kChunk;
+    for (mfh_i64 c = (mfh_i64)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6); c < nchunks; c += waves) {
+        u32x4 x[kPieces];
+#pragma unroll
+        for (int q = 0; q < kPieces; q++)
+            x[q] = load_nt(reinterpret_cast<const u32x4*>(in) + c * (64 * kPieces) + q * 64 + lane);
+#pragma unroll
+        for (int q = 0; q < kPieces; q++) {
+            const mfh_u32 w[4] = {x[q][0], x[q][1], x[q][2], x[q][3]};
+            mfh_u32 code[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int k = 0; k < P; k++) code[k >> 2] |= encode_fp8<FMT>(decode_reg<IN>(w, k)) << ((k & 3) * 8);
+            const mfh_i64 e0 = c * kChunk + (mfh_i64)(q * 64 + lane) * P;
+            if constexpr (P == 16) store_nt(reinterpret_cast<u32x4*>(out + e0), u32x4{code[0], code[1], code[2], code[3]});
+            else if constexpr (P == 8) store_nt(reinterpret_cast<u32x2*>(out + e0), u32x2{code[0], code[1]});
+            else if constexpr (P == 4) store_nt(reinterpret_cast<mfh_u32*>(out + e0), code[0]);
+            else store_nt(reinterpret_cast<mfh_u16*>(out + e0), (mfh_u16)code[0]);
+        }
+    }
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    for (mfh_i64 i = nchunks * kChunk + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        out[i] = (mfh_u8)encode_fp8<FMT>(decode_at<IN>(in, i));
+}
+
 template <int FMT>
 int launch_encode_fp8(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
 {
+    // unpacked numeric sources: whole 4 KiB source chunks per wave when the
+    // buffers are aligned for 16-byte loads and 16 / size-byte stores
+    const int size = in_dt == kF8E4M3 || in_dt == kF8E5M2 || in_dt == kInt4 ? 0 : dtype_size(in_dt);
+    if (size > 0 && aligned16(in) && (reinterpret_cast<uintptr_t>(out) & (uintptr_t)(16 / size - 1)) == 0) {
+        const int64_t chunk_elems = 64 * 4 * (16 / size);
+        const unsigned grid = grid_for(std::max<int64_t>(n / chunk_elems, 1) * 64, dev, Kern::kConvert);
+        switch (in_dt) {
+#define MFH_ENCODE_WAVE_CASE(DT) \
+    case DT: k_encode_fp8_wave<DT, FMT><<<grid, kBlock, 0, stream>>>(in, out, n); break;
+            MFH_ENCODE_WAVE_CASE(kFloat64)
+            MFH_ENCODE_WAVE_CASE(kFloat32)
+            MFH_ENCODE_WAVE_CASE(kFloat16)
+            MFH_ENCODE_WAVE_CASE(kBFloat16)
+            MFH_ENCODE_WAVE_CASE(kInt64)
+            MFH_ENCODE_WAVE_CASE(kInt32)
+            MFH_ENCODE_WAVE_CASE(kInt16)
+            MFH_ENCODE_WAVE_CASE(kInt8)
+            MFH_ENCODE_WAVE_CASE(kUint64)
+            MFH_ENCODE_WAVE_CASE(kUint32)
+            MFH_ENCODE_WAVE_CASE(kUint16)
+            MFH_ENCODE_WAVE_CASE(kUint8)
+#undef MFH_ENCODE_WAVE_CASE
+        default:
+            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+        }
+        return launch_status("k_encode_fp8_wave");
+    }
     const bool wide = in_dt == kFloat32 || in_dt == kBFloat16 || in_dt == kFloat16;
     const int vec_ok = aligned16(out) && (!wide || aligned16(in)) && n >= 16;
     const int64_t items = vec_ok ? n / 16 : n;
