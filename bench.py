@@ -356,7 +356,7 @@ def time_cpu(w, budget_s=3.0, threads=1):
 
 def profile_run(torch, M, O, reps):
     """Eager launches for rocprofv3: every workload kernel `reps` times, then a
-    plain f32 copy of 64 MiB (mfh_convert f32->f32, the k_convert kernel) whose
+    plain f32 copy of 64 MiB (mfh_convert f32->f32, the k_convert_vec kernel) whose
     FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes."""
     for cls in WORKLOADS:
         w = cls(torch, M, O)
@@ -373,7 +373,7 @@ def profile_run(torch, M, O, reps):
     for _ in range(reps):
         M.convert(dst.data_ptr(), M.FLOAT32, src.data_ptr(), M.FLOAT32, n, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    log(f"profiled calibration copy: k_convert<f32,f32> {n * 4} bytes read + {n * 4} written, x{reps}")
+    log(f"profiled calibration copy: k_convert_vec<f32,f32> {n * 4} bytes read + {n * 4} written, x{reps}")
 
 
 def load_traffic():
