@@ -373,8 +373,9 @@ MFH_DEV float decode_any(const void* in, mfh_i64 i)
     else return decode_at<IN>(in, i);
 }
 
-// Item = 16 elements -> one 16-byte store of codes.  f32 and 16-bit sources
-// are read with 16-byte loads; other sources element by element.
+// FP8 and Int4 sources, and any source whose buffers are not aligned for
+// k_encode_fp8_wave: item = 16 elements decoded one by one -> one 16-byte
+// store of codes when the output is 16-byte aligned, else the element loop.
 template <int IN, int FMT>
 __global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ in, mfh_u8* __restrict__ out,
                                                        mfh_i64 n, int vec_ok)
@@ -383,35 +384,14 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ 
     const mfh_i64 nitems = vec_ok ? n / 16 : 0;
     u32x4* dst = reinterpret_cast<u32x4*>(out);
     for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
-        float f[16];
-        if constexpr (IN == kFloat32) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(in) + v * 4;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                u32x4 w = load_nt(src + q);
-#pragma unroll
-                for (int k = 0; k < 4; k++) f[4 * q + k] = mfh_f32(w[k]);
-            }
-        } else if constexpr (IN == kBFloat16 || IN == kFloat16) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(in) + v * 2;
-#pragma unroll
-            for (int q = 0; q < 2; q++) {
-                u32x4 w = load_nt(src + q);
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    f[8 * q + 2 * k] = dec16<IN>(w[k] & 0xffffu);
-                    f[8 * q + 2 * k + 1] = dec16<IN>(w[k] >> 16);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 16; k++) f[k] = decode_any<IN>(in, v * 16 + k);
-        }
         u32x4 o;
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            o[q] = encode_fp8<FMT>(f[4 * q]) | (encode_fp8<FMT>(f[4 * q + 1]) << 8) |
-                   (encode_fp8<FMT>(f[4 * q + 2]) << 16) | (encode_fp8<FMT>(f[4 * q + 3]) << 24);
+        for (int q = 0; q < 4; q++) {
+            mfh_u32 word = 0u;
+#pragma unroll
+            for (int k = 0; k < 4; k++) word |= encode_fp8<FMT>(decode_any<IN>(in, v * 16 + 4 * q + k)) << (8 * k);
+            o[q] = word;
+        }
         store_nt(&dst[v], o);
     }
     for (mfh_i64 i = nitems * 16 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
@@ -490,8 +470,7 @@ int launch_encode_fp8(const Device* dev, mfh_u8* out, const void* in, int in_dt,
         }
         return launch_status("k_encode_fp8_wave");
     }
-    const bool wide = in_dt == kFloat32 || in_dt == kBFloat16 || in_dt == kFloat16;
-    const int vec_ok = aligned16(out) && (!wide || aligned16(in)) && n >= 16;
+    const int vec_ok = aligned16(out) && n >= 16;
     const int64_t items = vec_ok ? n / 16 : n;
     const unsigned grid = grid_for(items, dev, Kern::kConvert);
     switch (in_dt) {
