@@ -231,13 +231,13 @@ MFH_DEV float dec16(mfh_u32 h)
 // 16-bit storage -> any output, one 16-byte store per item: 8 elements for a
 // 16-bit output, 4 for f32.  (The cast that sits between a bf16/f16 tensor and
 // an f32 fusion in the reference.)
-template <int IN, int OUT>
-__global__ __launch_bounds__(kBlock) void k_convert16_vec(const void* __restrict__ in, void* __restrict__ out,
+template <int IN, int OUT, int BS>
+__global__ __launch_bounds__(BS) void k_convert16_vec(const void* __restrict__ in, void* __restrict__ out,
                                                           mfh_i64 nitems)
 {
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
     u32x4* dst = reinterpret_cast<u32x4*>(out);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nitems; v += stride) {
         if constexpr (OUT == kFloat32) {
             u32x2 w = reinterpret_cast<const u32x2*>(in)[v];
             store_nt(&dst[v], u32x4{mfh_bits(dec16<IN>(w[0] & 0xffffu)), mfh_bits(dec16<IN>(w[0] >> 16)),
@@ -297,17 +297,17 @@ MFH_DEV float decode_reg(const mfh_u32* w, int k)
 // store instruction.  Loads are non-temporal when an item reads at least as
 // many bytes as it writes.  Elements past the last whole item run the
 // element loop.
-template <int IN, int OUT>
-__global__ __launch_bounds__(kBlock) void k_convert_vec(const void* __restrict__ in, void* __restrict__ out,
+template <int IN, int OUT, int BS>
+__global__ __launch_bounds__(BS) void k_convert_vec(const void* __restrict__ in, void* __restrict__ out,
                                                         mfh_i64 n)
 {
     constexpr int E = OUT == kFloat32 ? 4 : 8;      // elements per item
     constexpr int B = E * size_of<IN>();            // source bytes per item
     constexpr int W = B / 4;                        // source dwords per item
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
     const mfh_i64 nitems = n / E;
     u32x4* dst = reinterpret_cast<u32x4*>(out);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nitems; v += stride) {
         mfh_u32 w[W];
         const char* src = static_cast<const char*>(in) + v * B;
         if constexpr (B >= 16) {
@@ -332,17 +332,17 @@ __global__ __launch_bounds__(kBlock) void k_convert_vec(const void* __restrict__
         }
         store_nt(&dst[v], o);
     }
-    for (mfh_i64 i = nitems * E + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+    for (mfh_i64 i = nitems * E + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride)
         store_one<OUT>(out, i, encode_one<OUT>(decode_at<IN>(in, i)));
 }
 
 // f32 -> 16-bit storage, 4 elements per item (16-byte load, 8-byte store).
-template <int OUT>
-__global__ __launch_bounds__(kBlock) void k_narrow_f32_vec(const u32x4* __restrict__ in,
+template <int OUT, int BS>
+__global__ __launch_bounds__(BS) void k_narrow_f32_vec(const u32x4* __restrict__ in,
                                                            u32x2* __restrict__ out, mfh_i64 nitems)
 {
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nitems; v += stride) {
         u32x4 a = load_nt(in + v);
         store_nt(&out[v], u32x2{encode_pair<OUT>(mfh_f32(a[0]), mfh_f32(a[1])),
                                 encode_pair<OUT>(mfh_f32(a[2]), mfh_f32(a[3]))});
@@ -406,8 +406,8 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ 
 // bytes of f32) spreads each load instruction over 4 KiB: f32 -> e4m3 ran
 // at 4.4 TB/s that way.  Elements past the last whole chunk run the element
 // loop.
-template <int IN, int FMT>
-__global__ __launch_bounds__(kBlock) void k_encode_fp8_wave(const void* __restrict__ in, mfh_u8* __restrict__ out,
+template <int IN, int FMT, int BS>
+__global__ __launch_bounds__(BS) void k_encode_fp8_wave(const void* __restrict__ in, mfh_u8* __restrict__ out,
                                                             mfh_i64 n)
 {
     constexpr int S = size_of<IN>();
@@ -415,9 +415,9 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8_wave(const void* __restri
     constexpr int kPieces = 4;         // pieces per lane per chunk
     constexpr mfh_i64 kChunk = 64 * kPieces * P;  // elements per wave chunk
     const int lane = (int)threadIdx.x & 63;
-    const mfh_i64 waves = (mfh_i64)gridDim.x * (kBlock / 64);
+    const mfh_i64 waves = (mfh_i64)gridDim.x * (BS / 64);
     const mfh_i64 nchunks = n / kChunk;
-    for (mfh_i64 c = (mfh_i64)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6); c < nchunks; c += waves) {
+    for (mfh_i64 c = (mfh_i64)blockIdx.x * (BS / 64) + (threadIdx.x >> 6); c < nchunks; c += waves) {
         u32x4 x[kPieces];
 #pragma unroll
         for (int q = 0; q < kPieces; q++)
@@ -435,9 +435,50 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8_wave(const void* __restri
             else store_nt(reinterpret_cast<mfh_u16*>(out + e0), (mfh_u16)code[0]);
         }
     }
-    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
-    for (mfh_i64 i = nchunks * kChunk + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    for (mfh_i64 i = nchunks * kChunk + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride)
         out[i] = (mfh_u8)encode_fp8<FMT>(decode_at<IN>(in, i));
+}
+
+// Workgroup size of a cast unless the launch config sets one.  Measured at
+// 2^26 elements against 256 threads: one wave wins wherever the output is at
+// most twice the source (f32 -> bf16 +13%, f32 copy +4%, bf16 -> f32 +3.5%,
+// int32 -> f32 +3%, FP8 encode +1%) and loses where it is four times the
+// source (int8 -> f32 -19%), which keeps 256.
+int cast_threads(int in_dt, int out_size)
+{
+    const int set = threads_per_block(Kern::kConvert);
+    if (set > 0) return set;
+    const int src = dtype_size(in_dt);
+    return src > 0 && out_size >= 4 * src ? 256 : 64;
+}
+
+template <int FMT, int BS>
+int launch_encode_fp8_wave(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, int size,
+                           hipStream_t stream)
+{
+    const int64_t chunk_elems = 64 * 4 * (16 / size);
+    const unsigned grid = grid_for(std::max<int64_t>(n / chunk_elems, 1) * 64, dev, Kern::kConvert, 1, BS);
+    switch (in_dt) {
+#define MFH_ENCODE_WAVE_CASE(DT) \
+    case DT: k_encode_fp8_wave<DT, FMT, BS><<<grid, BS, 0, stream>>>(in, out, n); break;
+        MFH_ENCODE_WAVE_CASE(kFloat64)
+        MFH_ENCODE_WAVE_CASE(kFloat32)
+        MFH_ENCODE_WAVE_CASE(kFloat16)
+        MFH_ENCODE_WAVE_CASE(kBFloat16)
+        MFH_ENCODE_WAVE_CASE(kInt64)
+        MFH_ENCODE_WAVE_CASE(kInt32)
+        MFH_ENCODE_WAVE_CASE(kInt16)
+        MFH_ENCODE_WAVE_CASE(kInt8)
+        MFH_ENCODE_WAVE_CASE(kUint64)
+        MFH_ENCODE_WAVE_CASE(kUint32)
+        MFH_ENCODE_WAVE_CASE(kUint16)
+        MFH_ENCODE_WAVE_CASE(kUint8)
+#undef MFH_ENCODE_WAVE_CASE
+    default:
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+    }
+    return launch_status("k_encode_fp8_wave");
 }
 
 template <int FMT>
@@ -446,30 +487,10 @@ int launch_encode_fp8(const Device* dev, mfh_u8* out, const void* in, int in_dt,
     // unpacked numeric sources: whole 4 KiB source chunks per wave when the
     // buffers are aligned for 16-byte loads and 16 / size-byte stores
     const int size = in_dt == kF8E4M3 || in_dt == kF8E5M2 || in_dt == kInt4 ? 0 : dtype_size(in_dt);
-    if (size > 0 && aligned16(in) && (reinterpret_cast<uintptr_t>(out) & (uintptr_t)(16 / size - 1)) == 0) {
-        const int64_t chunk_elems = 64 * 4 * (16 / size);
-        const unsigned grid = grid_for(std::max<int64_t>(n / chunk_elems, 1) * 64, dev, Kern::kConvert);
-        switch (in_dt) {
-#define MFH_ENCODE_WAVE_CASE(DT) \
-    case DT: k_encode_fp8_wave<DT, FMT><<<grid, kBlock, 0, stream>>>(in, out, n); break;
-            MFH_ENCODE_WAVE_CASE(kFloat64)
-            MFH_ENCODE_WAVE_CASE(kFloat32)
-            MFH_ENCODE_WAVE_CASE(kFloat16)
-            MFH_ENCODE_WAVE_CASE(kBFloat16)
-            MFH_ENCODE_WAVE_CASE(kInt64)
-            MFH_ENCODE_WAVE_CASE(kInt32)
-            MFH_ENCODE_WAVE_CASE(kInt16)
-            MFH_ENCODE_WAVE_CASE(kInt8)
-            MFH_ENCODE_WAVE_CASE(kUint64)
-            MFH_ENCODE_WAVE_CASE(kUint32)
-            MFH_ENCODE_WAVE_CASE(kUint16)
-            MFH_ENCODE_WAVE_CASE(kUint8)
-#undef MFH_ENCODE_WAVE_CASE
-        default:
-            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
-        }
-        return launch_status("k_encode_fp8_wave");
-    }
+    if (size > 0 && aligned16(in) && (reinterpret_cast<uintptr_t>(out) & (uintptr_t)(16 / size - 1)) == 0)
+        return with_block(cast_threads(in_dt, 1), [&](auto block) {
+            return launch_encode_fp8_wave<FMT, decltype(block)::value>(dev, out, in, in_dt, n, size, stream);
+        });
     const int vec_ok = aligned16(out) && n >= 16;
     const int64_t items = vec_ok ? n / 16 : n;
     const unsigned grid = grid_for(items, dev, Kern::kConvert);
@@ -577,31 +598,40 @@ template <int OUT>
 struct ConvertLaunch {
     static int run(const Device* dev, void* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
     {
+        return with_block(cast_threads(in_dt, OUT == kFloat32 ? 4 : 2), [&](auto block) {
+            return run_bs<decltype(block)::value>(dev, out, in, in_dt, n, stream);
+        });
+    }
+
+    template <int BS>
+    static int run_bs(const Device* dev, void* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
+    {
         constexpr int per = OUT == kFloat32 ? 4 : 8;
         if ((in_dt == kBFloat16 || in_dt == kFloat16) && aligned(in, per * 2) && aligned16(out) && n % per == 0) {
             int64_t nitems = n / per;
-            unsigned grid = grid_for(nitems, dev, Kern::kConvert);
-            if (in_dt == kBFloat16) k_convert16_vec<kBFloat16, OUT><<<grid, kBlock, 0, stream>>>(in, out, nitems);
-            else k_convert16_vec<kFloat16, OUT><<<grid, kBlock, 0, stream>>>(in, out, nitems);
+            unsigned grid = grid_for(nitems, dev, Kern::kConvert, 1, BS);
+            if (in_dt == kBFloat16) k_convert16_vec<kBFloat16, OUT, BS><<<grid, BS, 0, stream>>>(in, out, nitems);
+            else k_convert16_vec<kFloat16, OUT, BS><<<grid, BS, 0, stream>>>(in, out, nitems);
             return launch_status("k_convert16_vec");
         }
         if constexpr (OUT != kFloat32) {
             if (in_dt == kFloat32 && aligned16(in) && aligned(out, 8) && n % 4 == 0) {
                 int64_t nitems = n / 4;
-                k_narrow_f32_vec<OUT><<<grid_for(nitems, dev, Kern::kConvert), kBlock, 0, stream>>>(
+                k_narrow_f32_vec<OUT, BS><<<grid_for(nitems, dev, Kern::kConvert, 1, BS), BS, 0, stream>>>(
                     static_cast<const u32x4*>(in), static_cast<u32x2*>(out), nitems);
                 return launch_status("k_narrow_f32_vec");
             }
         }
         // every other source: whole 16-byte output items when both buffers
-        // are aligned for them, else the element loop
+        // are aligned for them, else the element loop (256 threads)
         const int src_size = dtype_size(in_dt);
         const bool vec = src_size > 0 && aligned(in, (unsigned)std::min(per * src_size, 16)) && aligned16(out);
-        unsigned grid = vec ? grid_for(std::max<int64_t>(n / per, 1), dev, Kern::kConvert) : grid_for(n, dev, Kern::kConvert);
+        const unsigned grid = vec ? grid_for(std::max<int64_t>(n / per, 1), dev, Kern::kConvert, 1, BS)
+                                  : grid_for(n, dev, Kern::kConvert);
         switch (in_dt) {
-#define MFH_CONVERT_CASE(DT) \
+#define MFH_CONVERT_CASE(DT)                                                                  \
     case DT:                                                                              \
-        if (vec) k_convert_vec<DT, OUT><<<grid, kBlock, 0, stream>>>(in, out, n);         \
+        if (vec) k_convert_vec<DT, OUT, BS><<<grid, BS, 0, stream>>>(in, out, n);         \
         else k_convert<DT, OUT><<<grid, kBlock, 0, stream>>>(in, out, n);                 \
         break;
         MFH_CONVERT_CASE(kFloat64)

@@ -169,7 +169,8 @@ constexpr int kMaxBlocksPerCu = 1 << 16;
 // bench, against 256 threads): FP8 128 (+0.4%; 64 is slower), axpy 64
 // (+2.3%; 128 is slower), Int4 256 (128 and 64 lose 2-3%).  0 for the fused
 // family means "per kernel": each generated kernel carries its shape (see
-// fusion.cpp), one-wave workgroups unless set.
+// fusion.cpp), one-wave workgroups unless set; for the casts "per cast"
+// (cast_threads in dequant.hip).
 constexpr unsigned kSizes64To256 = (1u << 6) | (1u << 7) | (1u << 8);
 constexpr unsigned kSizes64To1024 = kSizes64To256 | (1u << 9) | (1u << 10);
 LaunchCfg g_cfg[(int)Kern::kCount] = {
@@ -177,7 +178,7 @@ LaunchCfg g_cfg[(int)Kern::kCount] = {
     {"int4", {kMaxBlocksPerCu}, {2}, {256}, 1u << 8},
     {"axpy", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
     {"axpy16", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
-    {"convert", {kMaxBlocksPerCu}, {1}, {256}, 1u << 8},
+    {"convert", {kMaxBlocksPerCu}, {1}, {0}, kSizes64To256},
     {"fused", {0}, {0}, {0}, kSizes64To1024},
 };
 

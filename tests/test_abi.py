@@ -206,7 +206,7 @@ def test_launch_config_set_keep_and_restore():
 
 def test_launch_threads_set_keep_restore_and_limits():
     # defaults: the measured workgroup size of each family
-    assert [M.get_launch_threads(f) for f in ("fp8", "int4", "axpy", "axpy16", "convert")] == [128, 256, 64, 64, 256]
+    assert [M.get_launch_threads(f) for f in ("fp8", "int4", "axpy", "axpy16", "convert")] == [128, 256, 64, 64, 0]
     assert M.get_launch_threads("fused") == 0  # each generated kernel's default
     k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "threads_default")
     assert "__launch_bounds__(64)" in k.source and "gridDim.x * 64;" in k.source
