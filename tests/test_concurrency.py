@@ -6,7 +6,8 @@ CPU: generated kernels compiled concurrently (the hiprtc cache is shared and
 keyed by source text) come out identical to serial compiles, and each
 thread's mfh_last_error holds its own failure.  GPU: dequant, axpy and
 fused launches from eight threads, each on its own stream and buffers,
-match the oracle.
+match the oracle, and so do eight threads uploading, dequantising, running
+resident axpy and downloading through one shared backend.
 """
 import threading
 
@@ -122,3 +123,44 @@ def test_concurrent_launches_on_separate_streams():
         assert np.array_equal(o4.view(np.uint16), want_int4), f"thread {k}: int4"
         assert np.array_equal(oy.view(np.uint32), want_axpy.view(np.uint32)), f"thread {k}: axpy"
         assert np.array_equal(oc.view(np.uint16), want_chain), f"thread {k}: chain"
+
+
+@pytest.mark.gpu
+def test_one_backend_from_many_threads():
+    # tensor.Backend shared by goroutines: uploads through the one staging
+    # ring (f32 as is, FP8 and Int4 dequantised on the device), resident axpy
+    # and downloads interleave across threads; every tensor keeps its bytes
+    from manifesto_amd.backend import Backend
+    M.init(0)
+    b = Backend(0)
+    rng = np.random.default_rng(12)
+    n = (20 << 20) + 3  # more than one 16 MiB staging chunk for the f32 upload
+    x = rng.uniform(-1, 1, n).astype(np.float32)
+    codes = rng.integers(0, 256, n, dtype=np.uint8)
+    m = (1 << 21) + 4  # Int4 nibbles, groups of 64
+    packed = rng.integers(0, 256, m // 2, dtype=np.uint8)
+    scales = O.f32_to_f16(rng.uniform(0.005, 0.02, m // 64).astype(np.float32))
+    want_fp8 = O.dequant_fp8(codes, O.F8E4M3, 0.5, O.BFLOAT16).tobytes()
+    want_int4 = O.dequant_int4(packed, m, scales, O.FLOAT16, 64, O.BFLOAT16).tobytes()
+    results = {}
+    try:
+        def work(k):
+            y0 = np.random.default_rng(100 + k).uniform(-1, 1, n).astype(np.float32)
+            ty = b.upload([n], O.FLOAT32, y0)
+            tx = b.upload([n], O.FLOAT32, x)
+            t8 = b.upload_fp8([n], O.F8E4M3, codes, 0.5)
+            t4 = b.upload_int4([m], packed, scales, O.FLOAT16, 64)
+            b.axpy_onto_resident(ty, tx, 0.25 * (k + 1))
+            results[k] = (bytes(b.download(ty)[1]), bytes(b.download(t8)[1]), bytes(b.download(t4)[1]),
+                          O.axpy_f32(y0, x, 0.25 * (k + 1)).tobytes())
+            for t in (ty, tx, t8, t4):
+                t.close()
+
+        run_threads(work)
+    finally:
+        b.release()
+    for k in range(THREADS):
+        got_y, got_8, got_4, want_y = results[k]
+        assert got_y == want_y, f"thread {k}: axpy"
+        assert got_8 == want_fp8, f"thread {k}: fp8 upload"
+        assert got_4 == want_int4, f"thread {k}: int4 upload"
