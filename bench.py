@@ -13,7 +13,7 @@ the f16 gelu chain, Int4) are measured the same way and listed under
 -O2 -ffp-contract=off) timed on this host, single-threaded as the Go loops
 run; "cpu_baseline_all_cores" splits the same sample over the host's threads.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only N]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only N] [--sweep] [--profile REPS]
 """
 from __future__ import annotations
 
@@ -68,6 +68,7 @@ def _rand_u8(torch, n, gen):
 class Axpy(Workload):
     cfg, name, dtype = 1, "axpy f32 y=0.75*x+y, N=2^24, x,y~U[-1,1]", "f32"
     n = 1 << 24
+    bytes_for = staticmethod(lambda n: 12 * n)
     bytes_per_step = 12 * n
     kernel = "k_axpy_f32"
 
@@ -96,6 +97,7 @@ class Axpy(Workload):
 class Fp8(Workload):
     cfg, name, dtype = 2, "fp8_e4m3 -> bf16 dequant [4096,14336], per-tensor scale 0.0125", "f32"
     n = 4096 * 14336
+    bytes_for = staticmethod(lambda n: 3 * n + 4)
     bytes_per_step = 3 * n + 4
     kernel = "k_dequant_fp8<bf16>"
 
@@ -124,6 +126,7 @@ class Fp8(Workload):
 class SwiGLU(Workload):
     cfg, name, dtype = 3, "fused silu(gate)*up, bf16 [8192,14336] ~N(0,1) -> bf16", "f32"
     n = 8192 * 14336
+    bytes_for = staticmethod(lambda n: 6 * n)
     bytes_per_step = 6 * n
     kernel = "fused_swiglu"
 
@@ -161,6 +164,7 @@ class SwiGLU(Workload):
 class GeluChain(Workload):
     cfg, name, dtype = 4, "fused gelu_tanh((x+bias)*s)+residual, f16 [4,4096,4096], bias[4096], s=1.1", "f32"
     n = 4 * 4096 * 4096
+    bytes_for = staticmethod(lambda n: 6 * n + 4096 * 2)
     bytes_per_step = 6 * n + 4096 * 2
     kernel = "fused_gelu_chain"
 
@@ -207,6 +211,7 @@ class GeluChain(Workload):
 class Int4(Workload):
     cfg, name, dtype = 5, "int4 -> bf16 dequant [14336,4096], f16 scale per 128", "f32"
     n = 14336 * 4096
+    bytes_for = staticmethod(lambda n: n // 2 + (n // 128) * 2 + 2 * n)
     bytes_per_step = n // 2 + (n // 128) * 2 + 2 * n
     kernel = "k_dequant_int4<bf16,f16>"
 
@@ -376,6 +381,28 @@ def profile_run(torch, M, O, reps):
     log(f"profiled calibration copy: k_convert_vec<f32,f32> {n * 4} bytes read + {n * 4} written, x{reps}")
 
 
+def sweep_run(torch, M, O, steps, warmup):
+    """--sweep: every BASELINE kernel at launch sizes from 1/64 to 4x its
+    config's (the same workload, element count scaled and rounded to whole
+    4096-element rows), timed exactly as the bench times a step (a graph of
+    `steps` launches over rotated buffer sets, after the warm-up replays).
+    One JSON line per kernel and size: the HBM rate against the launch size
+    shows where the per-launch ramp stops mattering."""
+    for cls in WORKLOADS:
+        for f in (1 / 64, 1 / 16, 1 / 4, 1, 4):
+            n = max(4096, int(cls.n * f) // 4096 * 4096)
+            sized = type(cls.__name__, (cls,), {"n": n, "bytes_per_step": cls.bytes_for(n)})
+            w = sized(torch, M, O)
+            w.setup()
+            ms, _, _ = time_gpu(w, steps, warmup)
+            gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
+            print(json.dumps({"config": cls.cfg, "kernel": cls.kernel, "elements": n,
+                              "bytes_per_step": w.bytes_per_step, "scale": f, "us_per_step": round(ms * 1e3, 2),
+                              "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}), flush=True)
+            del w
+            torch.cuda.empty_cache()
+
+
 def load_traffic():
     """HBM bytes per dispatch of the headline kernel from the committed
     rocprofv3 PMC summary (profiles/pmc_traffic.json), or None."""
@@ -395,6 +422,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", type=int, default=0, help="measure only this BASELINE config")
+    ap.add_argument("--sweep", action="store_true",
+                    help="each BASELINE kernel at 1/64 to 4x its config's launch size (one JSON line each)")
     ap.add_argument("--profile", type=int, default=0, metavar="REPS",
                     help="eager launches of every kernel REPS times (for rocprofv3), no timing")
     args = ap.parse_args()
@@ -413,6 +442,9 @@ def main():
     log(f"device: {props.name} ({props.multi_processor_count} CUs)")
     if args.profile:
         profile_run(torch, M, O, args.profile)
+        return
+    if args.sweep:
+        sweep_run(torch, M, O, args.steps, args.warmup)
         return
 
     results = {}
