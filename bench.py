@@ -4,7 +4,8 @@ Headline (BASELINE.json metric, configs[1]): FP8 e4m3 -> bf16 dequantisation of
 a [4096, 14336] byte tensor with a per-tensor f32 scale of 0.0125, reported as
 achieved HBM GB/s (algorithmic bytes / kernel time) and as a fraction of the
 MI355X's 8 TB/s.  One step = one kernel launch over one resident batch.  Buffer
-sets are rotated so the footprint exceeds the 256 MB Infinity Cache, and the
+sets are rotated (at least four, and at least twice the 256 MB Infinity Cache
+in flight), and the
 timed steps are replayed from a captured HIP graph so the clock sees kernel
 time, not Python launch overhead; the W warm-up steps replay the same graph
 first, so the timed replay runs at the settled clock of sustained load.  The other BASELINE configs (axpy, SwiGLU,
@@ -51,7 +52,7 @@ class Workload:
         return self.torch.cuda.current_stream().cuda_stream
 
     def rotations(self):
-        return max(2, -(-2 * MALL_BYTES // self.bytes_per_step))
+        return max(4, -(-2 * MALL_BYTES // self.bytes_per_step))
 
     def setup(self):
         for _ in range(self.rotations()):
