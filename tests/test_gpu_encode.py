@@ -105,7 +105,7 @@ def test_encode_other_numeric_sources(fmt, in_dt, np_dt):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("in_dt", [O.FLOAT32, O.BFLOAT16])
 @pytest.mark.parametrize("n, pad, out_pad", [(1, 0, 0), (15, 0, 0), (16, 0, 0), (17, 0, 0), (1000003, 0, 0),
-                                             (4096, 2, 1), (4097, 0, 3)])
+                                             (4096, 2, 1), (4097, 0, 3), (40000, 0, 8)])
 def test_encode_tails_and_misaligned(fmt, in_dt, n, pad, out_pad):
     rng = np.random.default_rng(n)
     v = (rng.normal(0, 64, n) * np.exp(rng.uniform(-8, 4, n))).astype(np.float32)
