@@ -10,7 +10,13 @@ the product library never loads it.
 
 Parity status per function (details in oracle.c):
 - codecs, converters, axpy, scalar broadcast, linspace, dequant: pinned by
-  the reference's golden vectors and by closed forms (tests/test_oracle_*.py);
+  the reference's golden vectors and by closed forms (tests/test_oracle_*.py):
+  FP8 decode over every code, FP8 encode by brute-force nearest-even plus the
+  hand-derived subnormal quirks of both formats, scaled FP8 dequant against
+  the closed-form value times an f32 scale narrowed by torch / numpy (with
+  scales where an f64 product would differ), 16-bit axpy against numpy f32
+  arithmetic narrowed by torch / numpy, wide integers against numpy's
+  f64 conversion;
 - evaluator transcendentals (exp, log, tanh, sigmoid, silu, gelu): pinned to
   <=1 f32 ulp by independent f64 formulas; their last bit follows glibc, not
   Go's math package (which is absent here) — "parity unpinned" in that bit.

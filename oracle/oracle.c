@@ -5,8 +5,12 @@
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
  * it; the product library never does.
  *
- * Parity pins (what fixes each function beyond this restatement) are listed
- * per function and exercised by tests/test_oracle_*.py.  One function is
+ * Parity pins (what fixes each function beyond this restatement) are
+ * exercised by tests/test_oracle_*.py: golden vectors from the reference's
+ * tests, closed forms over every FP8 / Int4 / F16 code, library narrowings
+ * (numpy, torch) for BF16 / F16 encode, scaled FP8 dequant and 16-bit axpy,
+ * numpy's f64 conversion for wide integers, and hand-derived tables for the
+ * FP8 encoders' subnormal quirks.  One function is
  * "parity unpinned" in its last bit: the f64 transcendentals inside the
  * evaluator (glibc exp/log/tanh here, Go's math.Exp/Log/Tanh in the
  * reference); both are sub-ulp accurate in f64, so the f32 results agree

@@ -362,3 +362,239 @@ def test_checks_catch_planted_mistakes(golden):
     # gelu written as v*sigmoid(1.702 v) is off by far more than 1 ulp.
     v = np.float32(1.0)
     assert abs(float(v * expit(1.702 * v)) - float(O.eval_unary(O.N_GELU, np.array([v]))[0])) > 1e-4
+
+
+# --------------------------------------------------------------------------
+# Scaled FP8 dequant: closed-form decode, one numpy f32 multiply, then a
+# library narrowing (torch bf16, numpy f16).  Nothing here calls the oracle's
+# own decode or encode.
+# --------------------------------------------------------------------------
+
+# Scales: the config-2 scale, identity, a negative one, products that land in
+# f32 denormals, products that overflow f16 / bf16 / f32, signed zeros, and
+# scales where a product formed in f64 and rounded once to the output dtype
+# differs from the f32 product narrowed (found by search; bf16 for e4m3
+# 0x40e22e8b, 0x40f35556, e5m2 0x3ffd2492; f16 for e4m3 0x40f79555, e5m2
+# 0x41178aab).
+_FP8_SCALE_BITS = [0x3C4CCCCD, 0x3F800000, 0xC0600000, 0x09800000, 0x7149F2CA, 0x7E967699, 0x00000000,
+                   0x80000000, 0x40E22E8B, 0x40F35556, 0x3FFD2492, 0x40F79555, 0x41178AAB]
+
+
+def _closed_values(fmt):
+    closed = e4m3_closed if fmt == O.F8E4M3 else e5m2_closed
+    vals = [closed(c) for c in range(256)]
+    nan = np.array([v is None for v in vals])
+    return np.array([0.0 if v is None else v for v in vals], dtype=np.float32), nan
+
+
+def _torch_bf16_bits(x):
+    torch = pytest.importorskip("torch")
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16).view(torch.int16) \
+        .numpy().view(np.uint16)
+
+
+def _narrow(x, out_dtype):
+    with np.errstate(over="ignore"):
+        if out_dtype == O.FLOAT32:
+            return np.ascontiguousarray(x, dtype=np.float32).copy()
+        if out_dtype == O.BFLOAT16:
+            return _torch_bf16_bits(x)
+        return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def _as_bits(a):
+    a = np.asarray(a)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+@pytest.mark.parametrize("fmt", [O.F8E4M3, O.F8E5M2])
+@pytest.mark.parametrize("out_dtype", [O.FLOAT32, O.BFLOAT16, O.FLOAT16])
+def test_dequant_fp8_is_closed_form_times_f32_scale_then_narrowed(fmt, out_dtype):
+    codes = np.arange(256, dtype=np.uint8)
+    vals, nan = _closed_values(fmt)
+    for sb in _FP8_SCALE_BITS:
+        scale = from_bits(np.array([sb], np.uint32))[0]
+        with np.errstate(over="ignore", invalid="ignore"):
+            prod = (vals * scale).astype(np.float32)
+        ok = ~nan & ~np.isnan(prod)  # Inf*0 has its own rule below
+        want = _as_bits(_narrow(prod, out_dtype))
+        got = _as_bits(O.dequant_fp8(codes, fmt, float(scale), out_dtype))
+        assert np.array_equal(got[ok], want[ok]), (fmt, out_dtype, hex(sb))
+
+
+def _nan_narrow(u32, out_dtype):
+    """The reference narrowing of a NaN bit pattern (dtype/bfloat16.go:48-50,
+    dtype/float16.go:273-278), stated directly."""
+    u32 = int(u32)
+    if out_dtype == O.FLOAT32:
+        return u32
+    if out_dtype == O.BFLOAT16:
+        return (u32 >> 16) | 0x0040
+    return ((u32 >> 16) & 0x8000) | 0x7C00 | 0x0200 | ((u32 & 0x7FFFFF) >> 13)
+
+
+@pytest.mark.parametrize("out_dtype", [O.FLOAT32, O.BFLOAT16, O.FLOAT16])
+def test_dequant_fp8_nan_and_inf_rules(out_dtype):
+    # The scale multiply is build-defined with x86 mulss NaN rules made
+    # explicit: a NaN code keeps its quieted NaN, a NaN scale propagates
+    # quieted, Inf * 0 is the x86 default NaN 0xffc00000.
+    def one(code, fmt, scale):
+        return int(_as_bits(O.dequant_fp8(np.array([code], np.uint8), fmt, scale, out_dtype))[0])
+
+    for code, bits32 in ((0x7F, 0x7FC00000), (0xFF, 0xFFC00000)):
+        for scale in (0.0125, 0.0, -1.0, float("inf"), float("nan")):
+            assert one(code, O.F8E4M3, scale) == _nan_narrow(bits32, out_dtype), (hex(code), scale)
+    for code, bits32 in ((0x7D, 0x7FE00000), (0x7E, 0x7FC00000), (0x7F, 0x7FE00000), (0xFD, 0xFFE00000)):
+        assert one(code, O.F8E5M2, 2.0) == _nan_narrow(bits32, out_dtype), hex(code)
+    snan_scale = float(from_bits(np.array([0x7F800001], np.uint32))[0])
+    assert one(0x38, O.F8E4M3, snan_scale) == _nan_narrow(0x7FC00001, out_dtype)
+    for code in (0x7C, 0xFC):  # e5m2 +-Inf times +-0
+        for zero in (0.0, -0.0):
+            assert one(code, O.F8E5M2, zero) == _nan_narrow(0xFFC00000, out_dtype)
+    for code in (0x00, 0x80):  # +-0 times Inf
+        assert one(code, O.F8E4M3, float("inf")) == _nan_narrow(0xFFC00000, out_dtype)
+    pinf = {O.FLOAT32: 0x7F800000, O.BFLOAT16: 0x7F80, O.FLOAT16: 0x7C00}[out_dtype]
+    assert one(0x7C, O.F8E5M2, 3.0) == pinf
+    assert one(0xFC, O.F8E5M2, -3.0) == pinf
+
+
+# --------------------------------------------------------------------------
+# axpy in a 16-bit storage dtype: decode, y + fl32(alpha * x) in f32, narrow.
+# --------------------------------------------------------------------------
+
+def _storage_decode(u16, dtype):
+    if dtype == O.FLOAT16:
+        return u16.view(np.float16).astype(np.float32)
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("dtype", [O.BFLOAT16, O.FLOAT16])
+def test_axpy_storage_is_f32_axpy_then_library_narrowing(dtype):
+    rng = np.random.default_rng(11)
+    n = 1 << 16
+    y16 = rng.integers(0, 1 << 16, n, dtype=np.uint32).astype(np.uint16)
+    x16 = rng.integers(0, 1 << 16, n, dtype=np.uint32).astype(np.uint16)
+    yv, xv = _storage_decode(y16, dtype), _storage_decode(x16, dtype)
+    for alpha in (0.75, -1.0 / 3.0, 1e-3, 3e4):
+        a = np.float32(alpha)
+        with np.errstate(all="ignore"):
+            ref32 = (yv + (a * xv).astype(np.float32)).astype(np.float32)
+        ok = ~np.isnan(ref32)
+        want = _narrow(ref32, dtype)
+        got = O.axpy_storage(y16, x16, float(a), dtype)
+        assert np.array_equal(got[ok], want[ok]), (dtype, alpha)
+        assert ok.mean() > 0.9
+
+
+# --------------------------------------------------------------------------
+# Wide integers: BytesToFloat64 is a correctly rounded conversion,
+# BytesToFloat32 goes through it (two roundings; convert.go:132-145).
+# --------------------------------------------------------------------------
+
+def _wide_int_probe(np_type):
+    info = np.iinfo(np_type)
+    rng = np.random.default_rng(12)
+    bits = 8 * np.dtype(np_type).itemsize
+    r = rng.integers(0, 1 << 62, 1 << 14, dtype=np.uint64)
+    r = (r << np.uint64(2)) | rng.integers(0, 4, r.size, dtype=np.uint64)  # all 64 bits random
+    r = (r >> np.uint64(64 - bits)).astype(np.dtype(f"u{bits // 8}")).view(np_type)
+    edges = [info.min, info.max, 0, 1, -1, (1 << 24) + 1, (1 << 24) + 3, (1 << 31) - 1]
+    if bits == 64:
+        # exact ties after the f64 rounding: 2^60 + 2^36 + 1 rounds to the
+        # even f32 2^60 through f64, to 2^60 + 2^37 when rounded once
+        edges += [(1 << 60) + (1 << 36) + 1, (1 << 62) + (1 << 38) + 1, (1 << 53) + 1, (1 << 63) - 1]
+    edges = [e for e in edges if info.min <= e <= info.max]
+    return np.concatenate([r, np.array([np_type(e) for e in edges], dtype=np_type)])
+
+
+@pytest.mark.parametrize("np_type, dt", [(np.int32, O.INT32), (np.int64, O.INT64), (np.uint32, O.UINT32),
+                                         (np.uint64, O.UINT64)])
+def test_wide_ints_convert_through_f64(np_type, dt):
+    v = _wide_int_probe(np_type)
+    f64 = O.bytes_to_f64(dt, v)
+    assert np.array_equal(f64, v.astype(np.float64))
+    f32 = O.bytes_to_f32(dt, v)
+    assert np.array_equal(bits(f32), bits(v.astype(np.float64).astype(np.float32)))
+
+
+def test_wide_int_double_rounding_is_kept():
+    v = np.array([(1 << 60) + (1 << 36) + 1], dtype=np.int64)
+    assert O.bytes_to_f32(O.INT64, v)[0] == np.float32(2.0 ** 60)
+    # rounded once it would be the next f32 up: the two-step path is observable
+    assert float(Fraction((1 << 60) + (1 << 37))) == float(np.float32(v.astype(np.float32)[0]))
+    u = np.array([(1 << 63) + (1 << 39) + 1], dtype=np.uint64)
+    assert O.bytes_to_f32(O.UINT64, u)[0] == np.float32(2.0 ** 63)
+
+
+# --------------------------------------------------------------------------
+# E5M2 subnormal encode quirk, values derived by hand from
+# dtype/fp8.go:190-249: for an f32 exponent E, the branch shifts the 24-bit
+# significand right by 21 - (E + 15), one bit short of the subnormal grid
+# (units of 2^-16), so the code is twice the textbook one: [2^-15, 2^-14)
+# rounds to 4..7 and clamps to 0x04, [2^-16, 2^-15) gives 1.m * 2 rounded
+# half-even (2, 3 or 4), and anything below 2^-16 is zero.
+# --------------------------------------------------------------------------
+
+E5M2_SUBNORMAL_QUIRK = [
+    (2.0 ** -15, 0x04), (1.5 * 2.0 ** -15, 0x04), (1.99 * 2.0 ** -15, 0x04), (2.0 ** -14, 0x04),
+    (2.0 ** -16, 0x02), (1.25 * 2.0 ** -16, 0x02), (1.375 * 2.0 ** -16, 0x03), (1.5 * 2.0 ** -16, 0x03),
+    (1.625 * 2.0 ** -16, 0x03), (1.75 * 2.0 ** -16, 0x04), (1.999 * 2.0 ** -16, 0x04),
+    (2.0 ** -17, 0x00), (1.999 * 2.0 ** -17, 0x00), (2.0 ** -30, 0x00),
+    (-(2.0 ** -16), 0x82), (-(2.0 ** -15), 0x84), (-(2.0 ** -17), 0x80),
+]
+
+
+def test_e5m2_subnormal_encode_quirk():
+    for v, code in E5M2_SUBNORMAL_QUIRK:
+        assert O.f32_to_e5m2(v) == code, (v, hex(code))
+    xs = np.array([v for v, _ in E5M2_SUBNORMAL_QUIRK], np.float32)
+    assert O.f32_to_fp8(xs, O.F8E5M2).tolist() == [c for _, c in E5M2_SUBNORMAL_QUIRK]
+
+
+def _e5m2_nearest_even_subnormal(v):
+    """What a textbook encoder gives in the subnormal range (units of 2^-16,
+    ties to even, carrying into the normal 0x04)."""
+    q = v / 2.0 ** -16
+    r = math.floor(q)
+    frac = q - r
+    if frac > 0.5 or (frac == 0.5 and r % 2 == 1):
+        r += 1
+    return min(r, 4)
+
+
+def test_new_checks_catch_planted_mistakes():
+    # Planted in restatements written here, never in the product.
+    codes = np.arange(256, dtype=np.uint8)
+    vals, nan = _closed_values(O.F8E4M3)
+    fin = ~nan
+    # (1) the product formed in f64 and rounded once to bf16 fails the
+    #     composition check at the searched scale
+    s = from_bits(np.array([0x40E22E8B], np.uint32))[0]
+    p64 = vals[fin].astype(np.float64) * np.float64(s)
+    m, e = np.frexp(p64)
+    once = (np.ldexp(np.rint(m * 256.0), e - 8).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    want = _narrow((vals[fin] * s).astype(np.float32), O.BFLOAT16)
+    assert not np.array_equal(once, want)
+    assert np.array_equal(O.dequant_fp8(codes, O.F8E4M3, float(s), O.BFLOAT16)[fin], want)
+    # (2) the scale narrowed to bf16 before the multiply fails it at 0.0125
+    s = np.float32(0.0125)
+    s_bf16 = from_bits(np.array([int(_narrow(np.array([s]), O.BFLOAT16)[0]) << 16], np.uint32))[0]
+    early = _narrow((vals[fin] * s_bf16).astype(np.float32), O.BFLOAT16)
+    assert not np.array_equal(early, _narrow((vals[fin] * s).astype(np.float32), O.BFLOAT16))
+    # (3) nearest-even subnormals fail the hand-derived e5m2 quirk table
+    textbook = [_e5m2_nearest_even_subnormal(v) for v, c in E5M2_SUBNORMAL_QUIRK if 0 < v < 2.0 ** -14]
+    quirk = [c for v, c in E5M2_SUBNORMAL_QUIRK if 0 < v < 2.0 ** -14]
+    assert textbook != quirk
+    # (4) a single-rounding int64 -> f32 conversion fails the wide-int check
+    v = np.array([(1 << 60) + (1 << 36) + 1], dtype=np.int64)
+    assert v.astype(np.float32)[0] != v.astype(np.float64).astype(np.float32)[0]
+    # (5) an FMA-contracted 16-bit axpy fails the storage check on some input
+    rng = np.random.default_rng(13)
+    y = _storage_decode(rng.integers(0, 1 << 16, 4096, dtype=np.uint32).astype(np.uint16), O.FLOAT16)
+    x = _storage_decode(rng.integers(0, 1 << 16, 4096, dtype=np.uint32).astype(np.uint16), O.FLOAT16)
+    a = np.float32(-1.0 / 3.0)
+    ok = np.isfinite(x) & np.isfinite(y) & (np.abs(x) < 1e4) & (np.abs(y) < 1e4)
+    fused = np.array([np.float32(float(Fraction(float(a)) * Fraction(float(xi)) + Fraction(float(yi))))
+                      for xi, yi in zip(x[ok], y[ok])], dtype=np.float32)
+    unfused = (y[ok] + (a * x[ok]).astype(np.float32)).astype(np.float32)
+    assert not np.array_equal(_narrow(fused, O.FLOAT16), _narrow(unfused, O.FLOAT16))
