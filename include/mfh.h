@@ -14,10 +14,12 @@
  *
  * Return codes: MFH_OK (0) or a negative MFH_ERR_*; mfh_last_error() gives the
  * calling thread's message.  Entry points that the reference declares without
- * an error channel (mfh_axpy mirrors axpyDevice.Axpy) record failures in a
- * sticky per-process error that mfh_stream_sync and mfh_take_sticky_error
- * report, as the reference's zero-host-sync rule requires
- * (scripts/check_banned.sh:34-55).
+ * an error channel (mfh_axpy mirrors axpyDevice.Axpy) record failures as a
+ * sticky error of the stream the work was meant for, which that stream's
+ * mfh_stream_sync (or mfh_take_sticky_error) reports, as the reference's
+ * zero-host-sync rule requires (scripts/check_banned.sh:34-55).  Each stream
+ * keeps its own: a thread syncing its stream never receives the failure of
+ * work meant for another thread's stream.
  */
 #ifndef MFH_H
 #define MFH_H
@@ -55,9 +57,10 @@ int mfh_shutdown(void);
 /* Thread-local message of the last failing call on this thread. */
 const char* mfh_last_error(void);
 
-/* Returns and clears the sticky error left by entry points without an error
- * channel (mfh_axpy); MFH_OK when there is none. */
-int mfh_take_sticky_error(void);
+/* Returns and clears the first sticky error left on `stream` by entry points
+ * without an error channel (mfh_axpy), making its message the calling
+ * thread's last error; MFH_OK when there is none.  Needs no device. */
+int mfh_take_sticky_error(void* stream);
 
 /* Capabilities (tensor/backend.go:82-110): total device bytes, native
  * alignment in bytes, number of compute units. */
@@ -73,8 +76,8 @@ int mfh_free(void* ptr);
 int mfh_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int mfh_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 
-/* Waits for `stream`; reports a pending sticky error.  Tensor.Sync
- * (tensor/tensor.go:114). */
+/* Waits for `stream`; reports the stream's pending sticky error.
+ * Tensor.Sync (tensor/tensor.go:114). */
 int mfh_stream_sync(void* stream);
 
 /* Launch shape of one family of streaming kernels: workgroups per compute
@@ -111,7 +114,7 @@ int mfh_get_launch_threads(const char* kernel, int32_t* threads);
  * contract as axpyDevice.Axpy (runtime/axpy.go:13-15), called where
  * axpyOntoResident dispatches (runtime/axpy.go:84-90); the host loop it
  * replaces is runtime/axpy.go:115-117 and :145-147.  No return value: errors
- * are sticky. */
+ * are sticky on `stream`. */
 void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype, void* stream);
 
 /* out[i] = in[i] op scalar, op 0 add, 1 sub, 2 mul, 3 div, computed in f32

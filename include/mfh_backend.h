@@ -120,8 +120,10 @@ int32_t mfh_tensor_state(const mfh_tensor* tensor);
  * NULL once closed. */
 void* mfh_tensor_dispatch_pointer(const mfh_tensor* tensor);
 
-/* Tensor.Sync: waits for pending work on the tensor; reports the sticky
- * error of an entry point without an error channel (mfh_axpy). */
+/* Tensor.Sync: waits for pending work on the tensor, on whichever backend's
+ * stream it was queued; reports the sticky error (mfh_axpy has no error
+ * channel) of the tensor's backend stream, else of the stream whose resident
+ * axpy last wrote it. */
 int mfh_tensor_sync(mfh_tensor* tensor);
 
 /* Tensor.Slice (1-D zero-copy view of `length` elements from `start`) and
@@ -142,8 +144,10 @@ int mfh_tensor_release(mfh_tensor* tensor);
  * of this backend, after the reference's checks and with its messages
  * ("math.axpy: tensor location does not match backend", "... y dtype %s does
  * not match x dtype %s", "... y length %d does not match x length %d"), then
- * axpyDevice.Axpy on the backend stream.  Asynchronous; Sync or Download
- * observes the result. */
+ * axpyDevice.Axpy on the backend stream.  y and x may be held by other
+ * backends: the launch waits for work still queued on either, and their
+ * owners' Download, Sync, Close and shutdown wait for it.  Asynchronous;
+ * Sync or Download observes the result. */
 int mfh_axpy_onto_resident(mfh_backend* backend, mfh_tensor* y, const mfh_tensor* x, float alpha);
 
 #ifdef __cplusplus

@@ -66,7 +66,7 @@ def _declare(L):
         "mfh_init": (c.c_int, [c.c_int]),
         "mfh_shutdown": (c.c_int, []),
         "mfh_last_error": (c.c_char_p, []),
-        "mfh_take_sticky_error": (c.c_int, []),
+        "mfh_take_sticky_error": (c.c_int, [vp]),
         "mfh_capabilities": (c.c_int, [c.POINTER(i64), c.POINTER(i32), c.POINTER(i32)]),
         "mfh_alloc": (c.c_int, [c.POINTER(vp), c.c_size_t]),
         "mfh_free": (c.c_int, [vp]),
@@ -112,8 +112,9 @@ def init(device: int = 0) -> None:
     check(lib().mfh_init(device))
 
 
-def take_sticky_error() -> None:
-    check(lib().mfh_take_sticky_error())
+def take_sticky_error(stream: int = 0) -> None:
+    """Raises the first sticky error left on `stream` (and clears it)."""
+    check(lib().mfh_take_sticky_error(stream))
 
 
 def stream_sync(stream: int = 0) -> None:

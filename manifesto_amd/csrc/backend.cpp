@@ -36,7 +36,8 @@ struct Storage {
     size_t bytes = 0;
     bool freed = false;
     bool pending = false;
-    hipEvent_t done = nullptr;  // recorded after the last queued write
+    hipEvent_t done = nullptr;       // recorded after the last queued work that touches it
+    hipStream_t writer = nullptr;    // stream of the last resident axpy that wrote it
 };
 
 struct BackendState {
@@ -62,6 +63,9 @@ struct BackendState {
         };
         if (stream) keep(hipStreamSynchronize(stream), "hipStreamSynchronize");
         for (const auto& s : owned) {
+            // work queued on another backend's stream (a resident axpy) may
+            // still touch it
+            if (s->pending && s->done) keep(hipEventSynchronize(s->done), "hipEventSynchronize");
             if (s->done) keep(hipEventDestroy(s->done), "hipEventDestroy");
             s->done = nullptr;
             if (s->ptr) keep(hipFree(s->ptr), "hipFree");
@@ -77,7 +81,10 @@ struct BackendState {
             pinned[i] = dstage[i] = nullptr;
             slot_free[i] = nullptr;
         }
-        if (stream) keep(hipStreamDestroy(stream), "hipStreamDestroy");
+        if (stream) {
+            drop_sticky(stream);
+            keep(hipStreamDestroy(stream), "hipStreamDestroy");
+        }
         stream = nullptr;
         return rc;
     }
@@ -230,6 +237,38 @@ int wait_storage(Storage& st)
     st.pending = false;
     return MFH_OK;
 }
+
+// Marks work just queued on `stream` as the storage's last: every later
+// reader, close or backend shutdown waits for it through `done`.
+int mark_pending(Storage& st, hipStream_t stream)
+{
+    if (!st.done) MFH_TRY(check_hip(hipEventCreateWithFlags(&st.done, hipEventDisableTiming), "hipEventCreate"));
+    MFH_TRY(check_hip(hipEventRecord(st.done, stream), "hipEventRecord"));
+    st.pending = true;
+    return MFH_OK;
+}
+
+// The sticky error a tensor's owner sees at Sync / Download: its backend
+// stream's first, else that of the stream whose resident axpy last wrote it.
+int take_tensor_sticky(hipStream_t own, const Storage& st)
+{
+    int rc = take_sticky(own);
+    if (rc == MFH_OK && st.writer && st.writer != own) rc = take_sticky(st.writer);
+    return rc;
+}
+
+// Holds the mutexes of distinct backend states, taken in address order so
+// that threads combining the same backends in different roles cannot
+// deadlock.
+struct StateLocks {
+    std::vector<std::unique_lock<std::mutex>> held;
+    explicit StateLocks(std::vector<BackendState*> states)
+    {
+        std::sort(states.begin(), states.end());
+        states.erase(std::unique(states.begin(), states.end()), states.end());
+        for (BackendState* b : states) held.emplace_back(b->mu);
+    }
+};
 
 }  // namespace
 
@@ -459,7 +498,7 @@ int mfh_backend_download(mfh_backend* backend, const mfh_tensor* tensor, uint8_t
         prev_len = len;
         at += len;
     }
-    return mfh_take_sticky_error();
+    return take_tensor_sticky(s.stream, st);
 }
 
 int mfh_backend_close(mfh_backend* backend)
@@ -519,7 +558,7 @@ int mfh_tensor_sync(mfh_tensor* t)
     std::lock_guard<std::mutex> lock(t->backend->mu);
     MFH_TRY(wait_storage(*t->storage));
     if (t->backend->stream) MFH_TRY(check_hip(hipStreamSynchronize(t->backend->stream), "hipStreamSynchronize"));
-    return mfh_take_sticky_error();
+    return take_tensor_sticky(t->backend->stream, *t->storage);
 }
 
 int mfh_tensor_slice(const mfh_tensor* t, int64_t start, int64_t length, mfh_tensor** view)
@@ -607,12 +646,25 @@ int mfh_axpy_onto_resident(mfh_backend* backend, mfh_tensor* y, const mfh_tensor
     if (!stored_as_is(y->dtype))
         return fail(MFH_ERR_DTYPE_UNSUPPORTED, "math.axpy: dtype %s has no device axpy", dtype_string(y->dtype));
     BackendState& s = *backend->state;
-    std::lock_guard<std::mutex> lock(s.mu);
-    // Order after uploads queued on other backends' streams.
-    for (const mfh_tensor* t : {static_cast<const mfh_tensor*>(y), x})
-        if (t->backend.get() != &s && t->storage->pending && t->storage->done)
-            MFH_TRY(check_hip(hipStreamWaitEvent(s.stream, t->storage->done, 0), "hipStreamWaitEvent"));
+    // y and x may belong to other backends: their owners' state changes
+    // (close, download, shutdown) are held off while the launch is queued.
+    StateLocks locks({&s, y->backend.get(), x->backend.get()});
+    if (s.closed) return fail(MFH_ERR_CLOSED, "tensor: backend closed");
+    MFH_TRY(tensor_ok(y));
+    MFH_TRY(tensor_ok(x));
+    Storage& ys = *y->storage;
+    Storage& xs = *x->storage;
+    // Order after work still queued on the tensors (uploads, earlier axpys),
+    // on whichever stream it runs.
+    for (Storage* st : {&ys, &xs})
+        if (st->pending && st->done)
+            MFH_TRY(check_hip(hipStreamWaitEvent(s.stream, st->done, 0), "hipStreamWaitEvent"));
     mfh_axpy(mfh_tensor_dispatch_pointer(y), mfh_tensor_dispatch_pointer(x), y->elements, alpha, y->dtype, s.stream);
+    // Later readers of y, and closes of either tensor through its own
+    // backend, wait for this launch.
+    MFH_TRY(mark_pending(ys, s.stream));
+    if (&xs != &ys) MFH_TRY(mark_pending(xs, s.stream));
+    ys.writer = s.stream;
     return MFH_OK;
 }
 

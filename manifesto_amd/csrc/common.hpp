@@ -34,8 +34,13 @@ int64_t bytes_for(int dtype, int64_t elements);
 
 // Sets the calling thread's last error and returns `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-// Records a sticky error (entry points without an error channel).
-void fail_sticky(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Records a sticky error of an entry point without an error channel against
+// the stream its work was meant for; take_sticky(stream) returns and clears
+// that stream's first error (MFH_OK when none) and makes its message the
+// calling thread's last error; drop_sticky forgets a stream being destroyed.
+void fail_sticky(hipStream_t stream, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+int take_sticky(hipStream_t stream);
+void drop_sticky(hipStream_t stream);
 int check_hip(hipError_t err, const char* what);
 
 struct Device {

@@ -185,21 +185,21 @@ extern "C" {
 
 void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype, void* stream)
 {
+    hipStream_t s = (hipStream_t)stream;
     const Device* dev;
     if (bind_device(&dev) != MFH_OK) {
-        fail_sticky(MFH_ERR_NOT_INITIALIZED, "mfh_axpy: mfh_init has not been called");
+        fail_sticky(s, MFH_ERR_NOT_INITIALIZED, "mfh_axpy: mfh_init has not been called");
         return;
     }
     if (count < 0) {
-        fail_sticky(MFH_ERR_INVALID_ARGUMENT, "mfh_axpy: negative count %lld", (long long)count);
+        fail_sticky(s, MFH_ERR_INVALID_ARGUMENT, "mfh_axpy: negative count %lld", (long long)count);
         return;
     }
     if (count == 0) return;
     if (!y || !x) {
-        fail_sticky(MFH_ERR_INVALID_ARGUMENT, "mfh_axpy: NULL buffer");
+        fail_sticky(s, MFH_ERR_INVALID_ARGUMENT, "mfh_axpy: NULL buffer");
         return;
     }
-    hipStream_t s = (hipStream_t)stream;
     int vec_ok = aligned16(y) && aligned16(x);
     switch (dtype) {
     case kFloat32: {
@@ -233,11 +233,11 @@ void mfh_axpy(void* y, const void* x, int64_t count, float alpha, uint8_t dtype,
         break;
     }
     default:
-        fail_sticky(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_axpy: dtype %s is not f32/bf16/f16", dtype_name(dtype));
+        fail_sticky(s, MFH_ERR_DTYPE_UNSUPPORTED, "mfh_axpy: dtype %s is not f32/bf16/f16", dtype_name(dtype));
         return;
     }
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess) fail_sticky(MFH_ERR_DEVICE, "mfh_axpy: launch failed: %s", hipGetErrorString(err));
+    if (err != hipSuccess) fail_sticky(s, MFH_ERR_DEVICE, "mfh_axpy: launch failed: %s", hipGetErrorString(err));
 }
 
 int mfh_scalar_broadcast(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype, int64_t count,

@@ -5,6 +5,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <unordered_map>
 
 #include "common.hpp"
 
@@ -12,9 +13,15 @@ namespace mfh {
 
 namespace {
 thread_local std::string t_last_error;
-std::atomic<int> g_sticky_code{MFH_OK};
+// Sticky errors of entry points without an error channel, one per stream the
+// failed work was meant for: each stream's owner collects its own at its
+// next synchronisation, whichever thread fails or syncs first.
+struct Sticky {
+    int code = MFH_OK;
+    std::string msg;
+};
 std::mutex g_sticky_mu;
-std::string g_sticky_msg;
+std::unordered_map<hipStream_t, Sticky> g_sticky;
 std::mutex g_init_mu;
 Device g_device;
 std::atomic<bool> g_ready{false};
@@ -36,18 +43,36 @@ int fail(int code, const char* fmt, ...)
     return code;
 }
 
-void fail_sticky(int code, const char* fmt, ...)
+void fail_sticky(hipStream_t stream, int code, const char* fmt, ...)
 {
     va_list ap;
     va_start(ap, fmt);
     std::string msg = vformat(fmt, ap);
     va_end(ap);
     std::lock_guard<std::mutex> lock(g_sticky_mu);
-    if (g_sticky_code.load() == MFH_OK) {
-        g_sticky_msg = msg;
-        g_sticky_code.store(code);
+    Sticky& e = g_sticky[stream];
+    if (e.code == MFH_OK) {  // the first failure on a stream is the one reported
+        e.code = code;
+        e.msg = msg;
     }
     t_last_error = msg;
+}
+
+int take_sticky(hipStream_t stream)
+{
+    std::lock_guard<std::mutex> lock(g_sticky_mu);
+    auto it = g_sticky.find(stream);
+    if (it == g_sticky.end()) return MFH_OK;
+    const int code = it->second.code;
+    t_last_error = it->second.msg;
+    g_sticky.erase(it);
+    return code;
+}
+
+void drop_sticky(hipStream_t stream)
+{
+    std::lock_guard<std::mutex> lock(g_sticky_mu);
+    g_sticky.erase(stream);
 }
 
 int check_hip(hipError_t err, const char* what)
@@ -256,14 +281,7 @@ int mfh_version(void) { return 100; }
 
 const char* mfh_last_error(void) { return t_last_error.c_str(); }
 
-int mfh_take_sticky_error(void)
-{
-    std::lock_guard<std::mutex> lock(g_sticky_mu);
-    int code = g_sticky_code.exchange(MFH_OK);
-    if (code != MFH_OK) t_last_error = g_sticky_msg;
-    g_sticky_msg.clear();
-    return code;
-}
+int mfh_take_sticky_error(void* stream) { return take_sticky((hipStream_t)stream); }
 
 int mfh_init(int device)
 {
@@ -393,7 +411,7 @@ int mfh_stream_sync(void* stream)
     const Device* dev;
     MFH_TRY(bind_device(&dev));
     MFH_TRY(check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize"));
-    return mfh_take_sticky_error();
+    return take_sticky((hipStream_t)stream);
 }
 
 }  // extern "C"

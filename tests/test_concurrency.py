@@ -76,6 +76,68 @@ def test_last_error_is_per_thread():
         assert f'"family{k}"' in seen[k], seen[k]
 
 
+def test_sticky_errors_are_per_stream():
+    # The odd threads' axpys fail (the library has no device here), each on
+    # its own stream handle; every odd thread then finds its failure on its
+    # stream, once, and no even thread finds one on its own, although all the
+    # failures were recorded before anyone collected.  The handles are never
+    # dereferenced: the calls fail before any device work.
+    if M.lib().mfh_capabilities(None, None, None) == 0:
+        pytest.skip("library already initialised on a device")
+    barrier = threading.Barrier(THREADS)
+    seen = {}
+
+    def fail_k(k):
+        handle = 0x1000 * (k + 1)
+        if k % 2:
+            M.axpy(1, 1, 4, 1.0, M.FLOAT32, handle)
+        barrier.wait()  # every failure is recorded before any thread collects
+        try:
+            M.take_sticky_error(handle)
+            seen[k] = "ok"
+        except M.MFHError as e:
+            seen[k] = str(e)
+        M.take_sticky_error(handle)  # collected once
+
+    run_threads(fail_k)
+    for k in range(THREADS):
+        if k % 2:
+            assert "mfh_axpy: mfh_init has not been called" in seen[k], (k, seen[k])
+        else:
+            assert seen[k] == "ok", (k, seen[k])
+
+
+@pytest.mark.gpu
+def test_sticky_error_reaches_only_its_streams_owner():
+    import torch
+    M.init(0)
+    y = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+    x = torch.ones(1 << 16, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    barrier = threading.Barrier(2)
+    outcome = {}
+
+    def work(k):
+        s = streams[k].cuda_stream
+        if k == 0:
+            M.axpy(y.data_ptr(), x.data_ptr(), y.numel(), 1.0, M.INT32, s)  # unsupported: sticky on s
+        barrier.wait()
+        if k == 1:
+            M.axpy(y.data_ptr(), x.data_ptr(), y.numel(), 2.0, M.FLOAT32, s)
+        try:
+            M.stream_sync(s)
+            outcome[k] = "ok"
+        except M.MFHError as e:
+            outcome[k] = str(e)
+
+    run_threads(work, 2)
+    assert "is not f32/bf16/f16" in outcome[0], outcome
+    assert outcome[1] == "ok", outcome
+    M.stream_sync(streams[0].cuda_stream)  # consumed
+    assert float(y.cpu()[0]) == 2.0
+
+
 @pytest.mark.gpu
 def test_concurrent_launches_on_separate_streams():
     import torch

@@ -185,6 +185,37 @@ def test_axpy_onto_resident(backend):
         backend.axpy_onto_resident(z, backend.upload([4], O.FLOAT32, np.zeros(4, np.float32)), 1.0)
 
 
+def test_axpy_through_another_backend():
+    # y and x held by backend A, the axpy queued through backend B: A's
+    # download, sync and close are ordered after B's launch.
+    a, b = Backend(0), Backend(0)
+    try:
+        rng = np.random.default_rng(2)
+        n = (48 << 20) // 4 + 7  # larger than the staging ring, so the launch is still running at download
+        yv, xv = rng.uniform(-1, 1, n).astype(np.float32), rng.uniform(-1, 1, n).astype(np.float32)
+        y = a.upload([n], O.FLOAT32, yv)
+        x = a.upload_async([n], O.FLOAT32, xv)
+        for k in range(3):
+            b.axpy_onto_resident(y, x, 0.5 + k)
+        assert y.state() in (STATE_PENDING, STATE_READY)
+        want = O.axpy_f32(O.axpy_f32(O.axpy_f32(yv, xv, 0.5), xv, 1.5), xv, 2.5)
+        got = np.frombuffer(a.download(y)[1], np.float32)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        # bf16: the reference's golden case through the second backend, then
+        # the tensors close through their owner right after the launch
+        yb = a.upload([3], O.BFLOAT16, O.f32_to_bf16(np.array([1, 2, 3], np.float32)))
+        xb = a.upload([3], O.BFLOAT16, O.f32_to_bf16(np.array([4, 5, 6], np.float32)))
+        b.axpy_onto_resident(yb, xb, 0.5)
+        yb.sync()
+        assert O.bytes_to_f32(O.BFLOAT16, np.frombuffer(a.download(yb)[1], np.uint8)).tolist() == [3, 4.5, 6]
+        b.axpy_onto_resident(y, x, 1.0)
+        x.close()
+        y.close()
+    finally:
+        b.release()
+        a.release()
+
+
 def test_backend_close_invalidates_tensors():
     b = Backend(0)
     t = b.upload([4], O.FLOAT32, np.ones(4, np.float32))
