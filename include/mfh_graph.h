@@ -180,6 +180,32 @@ int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, 
 /* Bytes of the graph's device workspace (0 before the first call). */
 int64_t mfh_graph_workspace_bytes(const mfh_graph* graph);
 
+/* Bytes of the per-device static scratch of mfh_graph_call_noalloc. */
+#define MFH_GRAPH_SCRATCH_BYTES (64u << 20)
+
+/* mfh_graph_call without allocating anything on the device.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same bindings, results and errors as mfh_graph_call, except:
+ *   - the call's constants and intermediates live in one static device
+ *     scratch array of MFH_GRAPH_SCRATCH_BYTES per GPU (held from mfh_init
+ *     until the process ends); a call that needs more fails with
+ *     MFH_ERR_INVALID_ARGUMENT before anything is queued;
+ *   - everything runs as plain kernel launches (and device-to-device copies
+ *     for outputs not written in place) on `stream`: no auxiliary streams,
+ *     events, replay capture, host-to-device copies or memsets;
+ *   - it compiles and loads no kernel: each one the call needs must have been
+ *     loaded by an earlier mfh_graph_call with the same value dtypes and the
+ *     same operand modes (full, scalar, repeating row of the same length),
+ *     else MFH_ERR_INVALID_ARGUMENT;
+ *   - every call on one GPU, whatever its graph, uses that GPU's one scratch
+ *     array and leaves its contents there.  Nothing in it needs to start at
+ *     zero (each call writes its constants, and every intermediate is written
+ *     before it is read), but calls that overlap on one GPU (different
+ *     streams, or threads, without ordering between them) race. */
+int mfh_graph_call_noalloc(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
+                           int32_t n_outputs, void* stream);
+
 /* Launch replay (no counterpart in the reference, whose CallGraph dispatches
  * node by node): a call identical to an earlier one (same value names,
  * pointers, dtypes and counts, same workspace and stream budget) is captured

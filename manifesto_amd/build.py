@@ -22,8 +22,8 @@ LIB = os.path.join(HERE, "libmfh.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["runtime.cpp", "dequant.hip", "hostmath.hip", "fusion.cpp", "graph.cpp", "plan.cpp", "backend.cpp",
-           "safetensors.cpp"]
+SOURCES = ["runtime.cpp", "dequant.hip", "hostmath.hip", "scratch.hip", "fusion.cpp", "graph.cpp", "plan.cpp",
+           "backend.cpp", "safetensors.cpp"]
 PRELUDE_PARTS = ["codec.hpp", "devmath.hpp", "fusion_io.hpp"]
 
 COMMON_FLAGS = [

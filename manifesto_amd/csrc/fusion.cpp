@@ -231,13 +231,16 @@ int compile_source(const std::string& source, const std::string& kernel_name, st
     return MFH_OK;
 }
 
-int load_function(CodeObject& obj, int device, hipFunction_t* fn)
+int load_function(CodeObject& obj, int device, bool may_load, hipFunction_t* fn)
 {
     std::lock_guard<std::mutex> lock(obj.mu);
     if (obj.function && obj.device == device) {
         *fn = obj.function;
         return MFH_OK;
     }
+    if (!may_load)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: kernel %s is not loaded on device %d",
+                    obj.kernel_name.c_str(), device);
     if (obj.module) {
         g_module_generation.fetch_add(1);
         (void)hipModuleUnload(obj.module);
@@ -456,7 +459,7 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
 }
 
 int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
-            hipStream_t stream)
+            hipStream_t stream, bool may_load)
 {
     if (!kernel) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: kernel is empty");
     if (n_inputs != (int)kernel->inputs.size())
@@ -480,7 +483,7 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
             vec_ok = false;
     }
     hipFunction_t fn;
-    MFH_TRY(load_function(*kernel->code, dev->ordinal, &fn));
+    MFH_TRY(load_function(*kernel->code, dev->ordinal, may_load, &fn));
     int64_t nvec = vec_ok ? count / kernel->vec : 0;
     int64_t items = nvec > 0 ? (nvec + kernel->unroll - 1) / kernel->unroll : count;
     int64_t need = (items + kernel->block - 1) / kernel->block;

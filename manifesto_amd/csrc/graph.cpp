@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "fusion.hpp"
 #include "plan.hpp"
+#include "scratch.hpp"
 
 namespace mfh {
 namespace {
@@ -145,6 +146,13 @@ struct HIPKernel {
     uint32_t flags = 0;
     std::map<std::string, KernelPtr> variants;
     const mfh_kernel* full = nullptr;
+
+    // The variant for `ops` if it was compiled before, else NULL.
+    const mfh_kernel* find(const std::vector<mfh_operand>& ops) const
+    {
+        auto it = variants.find(signature(ops));
+        return it == variants.end() ? nullptr : it->second.get();
+    }
 
     int variant(const std::vector<mfh_operand>& ops, const mfh_kernel** out)
     {
@@ -628,9 +636,11 @@ int operand_mode(int64_t c, int64_t n, mfh_operand* op)
 }
 
 // Binds inputs and outputs and lowers every node to a launch.  With
-// `shapes_only` the values' data pointers are not needed (planning).
+// `shapes_only` the values' data pointers are not needed (planning); without
+// `may_compile` an unfused node whose one-node kernel was never generated is
+// an error instead of a compile.
 int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
-            bool shapes_only, Prepared* P)
+            bool shapes_only, Prepared* P, bool may_compile = true)
 {
     if ((n_inputs > 0 && !inputs) || (n_outputs > 0 && !outputs) || n_inputs < 0 || n_outputs < 0)
         return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: bad value list");
@@ -697,6 +707,9 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
                 return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: fused node \"%s\" has %d inputs, its kernel %d",
                             node.id.c_str(), (int)node.inputs.size(), (int)kernel->inputs.size());
         } else if (int32_t type = elementwise_type(node.op)) {
+            if (!node.solo && !may_compile)
+                return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" has no kernel yet (make one "
+                            "mfh_graph_call with these values first)", node.id.c_str());
             if (!node.solo) {
                 if ((int)node.inputs.size() != node_arity(type))
                     return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" (%s) has %d inputs, want %d",
@@ -822,7 +835,8 @@ int graph_streams(Graph& g, int n_streams, int n_events)
 // The launches of one call on `ls` and the graph's other streams: fork from
 // `ls`, every node with its waits and signals, join back into `ls`, then the
 // output copies.  With `ls` capturing, this records the call as a graph.
-int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipStream_t ls)
+int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipStream_t ls, void* workspace,
+               bool may_load = true)
 {
     std::vector<Slot>& slots = P.slots;
     if (n_streams > 1) {
@@ -830,7 +844,7 @@ int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipSt
         for (int s = 1; s < n_streams; s++)
             MFH_TRY(check_hip(hipStreamWaitEvent(g.aux[s - 1], g.fork, 0), "hipStreamWaitEvent(fork)"));
     }
-    char* base = static_cast<char*>(g.ws);
+    char* base = static_cast<char*>(workspace);
     auto addr = [&](const Slot& s) -> void* {
         return s.kind == Slot::kInput || s.kind == Slot::kBound ? s.ptr : base + s.offset;
     };
@@ -843,10 +857,13 @@ int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipSt
         for (const mfh_sync_event& e : pn.barriers)
             if (e.wait) MFH_TRY(check_hip(hipStreamWaitEvent(s, g.events[e.event_id], 0), "hipStreamWaitEvent(barrier)"));
         const mfh_kernel* k = nullptr;
-        MFH_TRY(st.kernel->variant(st.ops, &k));
+        if (may_load) MFH_TRY(st.kernel->variant(st.ops, &k));
+        else if (!(k = st.kernel->find(st.ops)))
+            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" has no kernel for these operands yet "
+                        "(make one mfh_graph_call with these values first)", g.nodes[st.node]->id.c_str());
         ptrs.clear();
         for (int o : st.operands) ptrs.push_back(addr(slots[o]));
-        MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, s));
+        MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, s, may_load));
         for (const mfh_sync_event& e : pn.barriers)
             if (!e.wait) MFH_TRY(check_hip(hipEventRecord(g.events[e.event_id], s), "hipEventRecord(barrier)"));
     }
@@ -862,6 +879,33 @@ int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipSt
                               "hipMemcpyAsync(graph output)"));
     }
     return MFH_OK;
+}
+
+// Places a call's values in its workspace and returns the bytes it needs:
+// constants first, then the intermediates, placed so that a region is reused
+// only after every launch touching its previous value is ordered before the
+// new writer.  A step's result never shares memory with its operands, and a
+// value copied out at the end is kept to the end.
+int64_t lay_out(Prepared& P, const Topology& topo)
+{
+    std::vector<Slot>& slots = P.slots;
+    const int64_t const_bytes = align_up((int64_t)P.constants.size() * 4);
+    std::vector<OrderedValue> values;
+    std::vector<int> value_slot;
+    for (int i = 0; i < (int)slots.size(); i++) {
+        const Slot& s = slots[i];
+        if (s.kind != Slot::kArena) continue;
+        OrderedValue v;
+        v.producer = s.producer;
+        v.users = s.readers;
+        if (s.pinned) v.users.push_back(kPinned);
+        v.size = std::max<int64_t>(1, s.count) * dtype_size(s.dtype);
+        values.push_back(std::move(v));
+        value_slot.push_back(i);
+    }
+    const int64_t arena = place_ordered(values, order_of(topo.nodes), kAlign);
+    for (size_t k = 0; k < values.size(); k++) slots[value_slot[k]].offset = const_bytes + values[k].offset;
+    return const_bytes + arena;
 }
 
 // Everything a call's launches depend on: value names, pointers, dtypes and
@@ -928,7 +972,6 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
 
     Prepared P;
     MFH_TRY(prepare(g, inputs, n_inputs, outputs, n_outputs, false, &P));
-    std::vector<Slot>& slots = P.slots;
 
     // Streams: ScheduleStreams over the launches (ir/stream_scheduler.go:56).
     Topology topo = launch_topology(g, P);
@@ -939,27 +982,7 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         for (const mfh_sync_event& e : n.barriers) n_events = std::max(n_events, e.event_id + 1);
     }
 
-    // Workspace: constants, then the intermediates, placed so that a region
-    // is reused only after every launch touching its previous value is
-    // ordered before the new writer.  A step's result never shares memory
-    // with its operands, and a value copied out at the end is kept to the end.
-    const int64_t const_bytes = align_up((int64_t)P.constants.size() * 4);
-    std::vector<OrderedValue> values;
-    std::vector<int> value_slot;
-    for (int i = 0; i < (int)slots.size(); i++) {
-        const Slot& s = slots[i];
-        if (s.kind != Slot::kArena) continue;
-        OrderedValue v;
-        v.producer = s.producer;
-        v.users = s.readers;
-        if (s.pinned) v.users.push_back(kPinned);
-        v.size = std::max<int64_t>(1, s.count) * dtype_size(s.dtype);
-        values.push_back(std::move(v));
-        value_slot.push_back(i);
-    }
-    const int64_t arena = place_ordered(values, order_of(topo.nodes), kAlign);
-    for (size_t k = 0; k < values.size(); k++) slots[value_slot[k]].offset = const_bytes + values[k].offset;
-    const int64_t need = const_bytes + arena;
+    const int64_t need = lay_out(P, topo);
     const bool captured = capturing != hipStreamCaptureStatusNone;
     if (need > g.ws_bytes && captured)
         return fail(MFH_ERR_INVALID_ARGUMENT,
@@ -1007,7 +1030,7 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         hipGraphExec_t exec = nullptr;
         if (!g.capture) MFH_TRY(check_hip(hipStreamCreateWithFlags(&g.capture, hipStreamNonBlocking), "hipStreamCreateWithFlags"));
         if (hipStreamBeginCapture(g.capture, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-            const int rc = launch_all(g, P, topo, n_streams, g.capture);
+            const int rc = launch_all(g, P, topo, n_streams, g.capture, g.ws);
             const hipError_t end = hipStreamEndCapture(g.capture, &graph);
             if (rc == MFH_OK && end == hipSuccess && graph &&
                 hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess)
@@ -1027,7 +1050,7 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
             g.replay_broken = true;
         }
     }
-    if (!launched) MFH_TRY(launch_all(g, P, topo, n_streams, stream));
+    if (!launched) MFH_TRY(launch_all(g, P, topo, n_streams, stream, g.ws));
     g.streams_used = n_streams;
     if (captured) return MFH_OK;
     if (replayable && !seen) {
@@ -1051,6 +1074,38 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
     g.last_stream = stream;
     g.called = true;
     return MFH_OK;
+}
+
+// mfh_graph_call on the caller's stream alone, with the call's constants and
+// intermediates in the static device scratch, and nothing compiled, loaded
+// or allocated.
+int graph_call_noalloc(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
+                       int32_t n_outputs, hipStream_t stream)
+{
+    const Device* dev;
+    MFH_TRY(bind_device(&dev));
+    void* base = nullptr;
+    MFH_TRY(scratch_address(dev->ordinal, &base));
+    Prepared P;
+    MFH_TRY(prepare(g, inputs, n_inputs, outputs, n_outputs, false, &P, false));
+    Topology topo = launch_topology(g, P);
+    MFH_TRY(schedule_streams(topo, 1));
+    for (const PlanNode& n : topo.nodes)
+        if (n.stream != 0 || !n.barriers.empty())
+            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" was scheduled off the caller's stream",
+                        n.name.c_str());
+    const int64_t need = lay_out(P, topo);
+    if (need > (int64_t)MFH_GRAPH_SCRATCH_BYTES)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "graph call (no allocation): the call needs %lld bytes of scratch, "
+                    "the static scratch holds %lld", (long long)need, (long long)MFH_GRAPH_SCRATCH_BYTES);
+    // Every kernel must be loaded already; checked before anything is queued.
+    for (const Step& st : P.steps)
+        if (!st.kernel->find(st.ops))
+            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" has no kernel for these operands yet "
+                        "(make one mfh_graph_call with these values first)", g.nodes[st.node]->id.c_str());
+    if (!P.constants.empty())
+        MFH_TRY(put_constants(static_cast<float*>(base), P.constants.data(), (int64_t)P.constants.size(), stream));
+    return launch_all(g, P, topo, 1, stream, base, false);
 }
 
 // compiler.PlanGraph (compiler/plan.go:242-290): buildPlanningTopology
@@ -1445,6 +1500,13 @@ int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, 
 }
 
 int64_t mfh_graph_workspace_bytes(const mfh_graph* graph) { return graph ? graph->ws_bytes : -1; }
+
+int mfh_graph_call_noalloc(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
+                           int32_t n_outputs, void* stream)
+{
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "graph is NULL");
+    return graph_call_noalloc(*graph, inputs, n_inputs, outputs, n_outputs, (hipStream_t)stream);
+}
 
 int mfh_graph_set_max_streams(mfh_graph* graph, int32_t max_streams)
 {

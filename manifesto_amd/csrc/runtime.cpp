@@ -8,6 +8,7 @@
 #include <unordered_map>
 
 #include "common.hpp"
+#include "scratch.hpp"
 
 namespace mfh {
 
@@ -294,6 +295,8 @@ int mfh_init(int device)
     MFH_TRY(check_hip(hipSetDevice(device), "hipSetDevice"));
     hipDeviceProp_t prop;
     MFH_TRY(check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties"));
+    // the allocation-free graph call's scratch address on this device
+    MFH_TRY(scratch_setup(device));
     g_device.ordinal = device;
     g_device.compute_units = prop.multiProcessorCount;
     g_device.total_bytes = (int64_t)prop.totalGlobalMem;

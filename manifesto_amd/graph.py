@@ -98,6 +98,7 @@ def _L():
             "mfh_codegen_attach_kernels": (c.c_int, [vp, c.POINTER(i32), i32, c.c_uint32, c.POINTER(i32)]),
             "mfh_graph_kernel": (c.c_int, [vp, i32, i32, c.POINTER(vp)]),
             "mfh_graph_call": (c.c_int, [vp, c.POINTER(Value), i32, c.POINTER(Value), i32, vp]),
+            "mfh_graph_call_noalloc": (c.c_int, [vp, c.POINTER(Value), i32, c.POINTER(Value), i32, vp]),
             "mfh_graph_workspace_bytes": (i64, [vp]),
             "mfh_graph_set_replay": (c.c_int, [vp, i32]),
             "mfh_graph_replayed_calls": (i64, [vp]),
@@ -305,6 +306,14 @@ class Graph:
         to torch tensors."""
         ins, outs = self._values(inputs), self._values(outputs)
         check(_L().mfh_graph_call(self._h, ins, len(inputs), outs, len(outputs), stream))
+
+    def call_noalloc(self, inputs: dict, outputs: dict, stream: int = 0) -> None:
+        """mfh_graph_call_noalloc: the same call with its constants and
+        intermediates in the library's static device scratch, nothing
+        allocated, compiled or loaded (an earlier `call` with the same value
+        dtypes and operand modes loads the kernels)."""
+        ins, outs = self._values(inputs), self._values(outputs)
+        check(_L().mfh_graph_call_noalloc(self._h, ins, len(inputs), outs, len(outputs), stream))
 
     @staticmethod
     def _values(mapping):
