@@ -349,17 +349,32 @@ __global__ __launch_bounds__(BS) void k_narrow_f32_vec(const u32x4* __restrict__
     }
 }
 
+bool aligned(const void* p, unsigned bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
+
 // ---------------------------------------------------------------------------
-// Any numeric dtype -> FP8 (BytesToFloat8E4M3 / BytesToFloat8E5M2,
-// dtype/convert/convert.go:194-232: BytesToFloat32, then the saturating RNE
-// quantiser of codec.hpp)
+// Any numeric dtype -> one byte per element: FP8 (BytesToFloat8E4M3 /
+// BytesToFloat8E5M2, dtype/convert/convert.go:194-232: BytesToFloat32, then
+// the saturating RNE quantiser of codec.hpp) or Int8 (BytesToInt8, :235-263:
+// BytesToFloat64, saturation to [-128, 127], truncation toward zero)
 // ---------------------------------------------------------------------------
 
-template <int FMT>
-MFH_DEV mfh_u32 encode_fp8(float v)
+// int8(v) after BytesToInt8's saturation.  A NaN passes both of the
+// reference's comparisons and Go converts it to 0 on amd64 and arm64; -Inf
+// and +Inf saturate.  Values in range truncate toward zero (v_cvt_i32_f32 /
+// v_cvt_i32_f64 truncate).
+template <typename F>
+MFH_DEV mfh_u32 i8_of(F v)
 {
-    if constexpr (FMT == kF8E4M3) return mfh_e4m3_encode(v);
-    else return mfh_e5m2_encode(v);
+    const F c = v < F(-128) ? F(-128) : (v > F(127) ? F(127) : v);
+    return c == c ? (mfh_u32)(int)c & 0xffu : 0u;
+}
+
+template <int ENC>
+MFH_DEV mfh_u32 encode_byte(float v)
+{
+    if constexpr (ENC == kF8E4M3) return mfh_e4m3_encode(v);
+    else if constexpr (ENC == kF8E5M2) return mfh_e5m2_encode(v);
+    else return i8_of(v);
 }
 
 // BytesToFloat32 of element i for every source dtype, FP8 and Int4 included.
@@ -373,12 +388,32 @@ MFH_DEV float decode_any(const void* in, mfh_i64 i)
     else return decode_at<IN>(in, i);
 }
 
+// The output byte of element i.  Int8 from f64 truncates the f64 value
+// itself (its f32 rounding could cross an integer); every other source is
+// exact in f32, or (64-bit integers) rounds monotonically, which saturation
+// and truncation cannot tell apart from its f64 value.
+template <int IN, int ENC>
+MFH_DEV mfh_u32 byte_at(const void* in, mfh_i64 i)
+{
+    if constexpr (ENC == kInt8 && IN == kFloat64) return i8_of(static_cast<const double*>(in)[i]);
+    else return encode_byte<ENC>(decode_any<IN>(in, i));
+}
+
+// The same for element k of a register copy of consecutive elements.
+template <int IN, int ENC>
+MFH_DEV mfh_u32 byte_reg(const mfh_u32* w, int k)
+{
+    if constexpr (ENC == kInt8 && IN == kFloat64)
+        return i8_of(__builtin_bit_cast(double, (mfh_u64)w[2 * k] | ((mfh_u64)w[2 * k + 1] << 32)));
+    else return encode_byte<ENC>(decode_reg<IN>(w, k));
+}
+
 // FP8 and Int4 sources, and any source whose buffers are not aligned for
-// k_encode_fp8_wave: item = 16 elements decoded one by one -> one 16-byte
+// k_encode_byte_wave: item = 16 elements decoded one by one -> one 16-byte
 // store of codes when the output is 16-byte aligned, else the element loop.
-template <int IN, int FMT>
-__global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ in, mfh_u8* __restrict__ out,
-                                                       mfh_i64 n, int vec_ok)
+template <int IN, int ENC>
+__global__ __launch_bounds__(kBlock) void k_encode_byte(const void* __restrict__ in, mfh_u8* __restrict__ out,
+                                                        mfh_i64 n, int vec_ok)
 {
     const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
     const mfh_i64 nitems = vec_ok ? n / 16 : 0;
@@ -389,43 +424,43 @@ __global__ __launch_bounds__(kBlock) void k_encode_fp8(const void* __restrict__ 
         for (int q = 0; q < 4; q++) {
             mfh_u32 word = 0u;
 #pragma unroll
-            for (int k = 0; k < 4; k++) word |= encode_fp8<FMT>(decode_any<IN>(in, v * 16 + 4 * q + k)) << (8 * k);
+            for (int k = 0; k < 4; k++) word |= byte_at<IN, ENC>(in, v * 16 + 4 * q + k) << (8 * k);
             o[q] = word;
         }
         store_nt(&dst[v], o);
     }
     for (mfh_i64 i = nitems * 16 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
-        out[i] = (mfh_u8)encode_fp8<FMT>(decode_any<IN>(in, i));
+        out[i] = (mfh_u8)byte_at<IN, ENC>(in, i);
 }
 
-// Unpacked numeric dtype -> FP8 with every load instruction of a wave
-// reading 1 KiB contiguously: a wave takes chunks of 4 KiB of source, lane l
-// the 16-byte pieces l, l + 64, l + 128 and l + 192 of its chunk, and writes
-// the 16 / size codes of each piece next to its neighbours' (16-, 4- or
-// 2-byte stores; 2-byte sources pair adjacent pieces into one 16-byte
-// store, 2-4% faster than two 8-byte ones).  One lane taking 16 consecutive elements instead (64
-// bytes of f32) spreads each load instruction over 4 KiB: f32 -> e4m3 ran
-// at 4.4 TB/s that way.  Elements past the last whole chunk run the element
-// loop.
-template <int IN, int FMT, int BS>
-__global__ __launch_bounds__(BS) void k_encode_fp8_wave(const void* __restrict__ in, mfh_u8* __restrict__ out,
-                                                            mfh_i64 n)
+// Unpacked numeric dtype -> one byte per element with every load instruction
+// of a wave reading 1 KiB contiguously: a wave takes chunks of 4 KiB of
+// source, lane l the 16-byte pieces l, l + 64, l + 128 and l + 192 of its
+// chunk, and writes the 16 / size output bytes of each piece next to its
+// neighbours' (16-, 4- or 2-byte stores, 8-byte ones for 2-byte sources).
+// With PAIR (2-byte sources, output 16-byte aligned) lane l takes the
+// adjacent pieces 2l, 2l + 1 (and 128 + 2l, 129 + 2l) so that their 16
+// bytes leave in one 16-byte store instead of two 8-byte ones: 2-4% faster.
+// One lane taking 16 consecutive elements instead (64 bytes of f32) spreads
+// each load instruction over 4 KiB: f32 -> e4m3 ran at 4.4 TB/s that way.
+// Elements past the last whole chunk run the element loop.
+template <int IN, int ENC, int BS, bool PAIR>
+__global__ __launch_bounds__(BS) void k_encode_byte_wave(const void* __restrict__ in, mfh_u8* __restrict__ out,
+                                                             mfh_i64 n)
 {
     constexpr int S = size_of<IN>();
     constexpr int P = 16 / S;          // elements (and output bytes) per 16-byte piece
     constexpr int kPieces = 4;         // pieces per lane per chunk
     constexpr mfh_i64 kChunk = 64 * kPieces * P;  // elements per wave chunk
+    static_assert(!PAIR || P == 8, "pairs are for 2-byte sources");
     const int lane = (int)threadIdx.x & 63;
     const mfh_i64 waves = (mfh_i64)gridDim.x * (BS / 64);
     const mfh_i64 nchunks = n / kChunk;
     for (mfh_i64 c = (mfh_i64)blockIdx.x * (BS / 64) + (threadIdx.x >> 6); c < nchunks; c += waves) {
-        // 2-byte sources: lane l takes the adjacent pieces 2l, 2l + 1 (and
-        // 128 + 2l, 129 + 2l) so that their 16 codes leave in one 16-byte store
-        constexpr bool kPair = P == 8;
         u32x4 x[kPieces];
 #pragma unroll
         for (int q = 0; q < kPieces; q++) {
-            const int piece = kPair ? (q >> 1) * 128 + 2 * lane + (q & 1) : q * 64 + lane;
+            const int piece = PAIR ? (q >> 1) * 128 + 2 * lane + (q & 1) : q * 64 + lane;
             x[q] = load_nt(reinterpret_cast<const u32x4*>(in) + c * (64 * kPieces) + piece);
         }
         mfh_u32 prev[2] = {0u, 0u};
@@ -434,9 +469,9 @@ __global__ __launch_bounds__(BS) void k_encode_fp8_wave(const void* __restrict__
             const mfh_u32 w[4] = {x[q][0], x[q][1], x[q][2], x[q][3]};
             mfh_u32 code[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int k = 0; k < P; k++) code[k >> 2] |= encode_fp8<FMT>(decode_reg<IN>(w, k)) << ((k & 3) * 8);
+            for (int k = 0; k < P; k++) code[k >> 2] |= byte_reg<IN, ENC>(w, k) << ((k & 3) * 8);
             const mfh_i64 e0 = c * kChunk + (mfh_i64)(q * 64 + lane) * P;
-            if constexpr (kPair) {
+            if constexpr (PAIR) {
                 if (q & 1) {
                     const mfh_i64 p0 = c * kChunk + (mfh_i64)((q >> 1) * 128 + 2 * lane) * P;
                     store_nt(reinterpret_cast<u32x4*>(out + p0), u32x4{prev[0], prev[1], code[0], code[1]});
@@ -452,7 +487,7 @@ __global__ __launch_bounds__(BS) void k_encode_fp8_wave(const void* __restrict__
     }
     const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
     for (mfh_i64 i = nchunks * kChunk + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride)
-        out[i] = (mfh_u8)encode_fp8<FMT>(decode_at<IN>(in, i));
+        out[i] = (mfh_u8)byte_at<IN, ENC>(in, i);
 }
 
 // Workgroup size of a cast unless the launch config sets one.  Measured at
@@ -468,51 +503,69 @@ int cast_threads(int in_dt, int out_size)
     return src > 0 && out_size >= 4 * src ? 256 : 64;
 }
 
-template <int FMT, int BS>
-int launch_encode_fp8_wave(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, int size,
-                           hipStream_t stream)
+template <int ENC, int BS, bool PAIR>
+int launch_encode_byte_wave(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, int size,
+                            hipStream_t stream)
 {
     const int64_t chunk_elems = 64 * 4 * (16 / size);
     const unsigned grid = grid_for(std::max<int64_t>(n / chunk_elems, 1) * 64, dev, Kern::kConvert, 1, BS);
-    switch (in_dt) {
+    if constexpr (PAIR) {
+        switch (in_dt) {
+        case kFloat16: k_encode_byte_wave<kFloat16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
+        case kBFloat16: k_encode_byte_wave<kBFloat16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
+        case kInt16: k_encode_byte_wave<kInt16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
+        case kUint16: k_encode_byte_wave<kUint16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
+        default: return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: paired encode of %s", dtype_name(in_dt));
+        }
+        return launch_status("k_encode_byte_wave");
+    } else {
+        switch (in_dt) {
 #define MFH_ENCODE_WAVE_CASE(DT) \
-    case DT: k_encode_fp8_wave<DT, FMT, BS><<<grid, BS, 0, stream>>>(in, out, n); break;
-        MFH_ENCODE_WAVE_CASE(kFloat64)
-        MFH_ENCODE_WAVE_CASE(kFloat32)
-        MFH_ENCODE_WAVE_CASE(kFloat16)
-        MFH_ENCODE_WAVE_CASE(kBFloat16)
-        MFH_ENCODE_WAVE_CASE(kInt64)
-        MFH_ENCODE_WAVE_CASE(kInt32)
-        MFH_ENCODE_WAVE_CASE(kInt16)
-        MFH_ENCODE_WAVE_CASE(kInt8)
-        MFH_ENCODE_WAVE_CASE(kUint64)
-        MFH_ENCODE_WAVE_CASE(kUint32)
-        MFH_ENCODE_WAVE_CASE(kUint16)
-        MFH_ENCODE_WAVE_CASE(kUint8)
+    case DT: k_encode_byte_wave<DT, ENC, BS, false><<<grid, BS, 0, stream>>>(in, out, n); break;
+            MFH_ENCODE_WAVE_CASE(kFloat64)
+            MFH_ENCODE_WAVE_CASE(kFloat32)
+            MFH_ENCODE_WAVE_CASE(kFloat16)
+            MFH_ENCODE_WAVE_CASE(kBFloat16)
+            MFH_ENCODE_WAVE_CASE(kInt64)
+            MFH_ENCODE_WAVE_CASE(kInt32)
+            MFH_ENCODE_WAVE_CASE(kInt16)
+            MFH_ENCODE_WAVE_CASE(kInt8)
+            MFH_ENCODE_WAVE_CASE(kUint64)
+            MFH_ENCODE_WAVE_CASE(kUint32)
+            MFH_ENCODE_WAVE_CASE(kUint16)
+            MFH_ENCODE_WAVE_CASE(kUint8)
 #undef MFH_ENCODE_WAVE_CASE
-    default:
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+        default:
+            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+        }
+        return launch_status("k_encode_byte_wave");
     }
-    return launch_status("k_encode_fp8_wave");
 }
 
-template <int FMT>
-int launch_encode_fp8(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
+template <int ENC>
+int launch_encode_byte(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
 {
     // unpacked numeric sources: whole 4 KiB source chunks per wave when the
-    // buffers are aligned for the kernel's loads and stores
+    // source is 16-byte aligned and the output aligned for the kernel's
+    // stores (2-byte sources: 16 bytes for paired pieces, else 8)
     const int size = in_dt == kF8E4M3 || in_dt == kF8E5M2 || in_dt == kInt4 ? 0 : dtype_size(in_dt);
-    // output alignment = the kernel's store width (2-byte sources pair pieces into 16)
-    if (size > 0 && aligned16(in) && (reinterpret_cast<uintptr_t>(out) & (uintptr_t)(size == 2 ? 15 : 16 / size - 1)) == 0)
-        return with_block(cast_threads(in_dt, 1), [&](auto block) {
-            return launch_encode_fp8_wave<FMT, decltype(block)::value>(dev, out, in, in_dt, n, size, stream);
-        });
+    if (size > 0 && aligned16(in)) {
+        const uintptr_t at = reinterpret_cast<uintptr_t>(out);
+        if (size == 2 && (at & 15) == 0)
+            return with_block(cast_threads(in_dt, 1), [&](auto block) {
+                return launch_encode_byte_wave<ENC, decltype(block)::value, true>(dev, out, in, in_dt, n, size, stream);
+            });
+        if ((at & (uintptr_t)(16 / size - 1)) == 0)
+            return with_block(cast_threads(in_dt, 1), [&](auto block) {
+                return launch_encode_byte_wave<ENC, decltype(block)::value, false>(dev, out, in, in_dt, n, size, stream);
+            });
+    }
     const int vec_ok = aligned16(out) && n >= 16;
     const int64_t items = vec_ok ? n / 16 : n;
     const unsigned grid = grid_for(items, dev, Kern::kConvert);
     switch (in_dt) {
 #define MFH_ENCODE_CASE(DT) \
-    case DT: k_encode_fp8<DT, FMT><<<grid, kBlock, 0, stream>>>(in, out, n, vec_ok); break;
+    case DT: k_encode_byte<DT, ENC><<<grid, kBlock, 0, stream>>>(in, out, n, vec_ok); break;
         MFH_ENCODE_CASE(kFloat64)
         MFH_ENCODE_CASE(kFloat32)
         MFH_ENCODE_CASE(kFloat16)
@@ -532,12 +585,135 @@ int launch_encode_fp8(const Device* dev, mfh_u8* out, const void* in, int in_dt,
     default:
         return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
     }
-    return launch_status("k_encode_fp8");
+    return launch_status("k_encode_byte");
+}
+
+// ---------------------------------------------------------------------------
+// Any numeric dtype -> f64 (BytesToFloat64, dtype/convert/convert.go:36-79)
+// ---------------------------------------------------------------------------
+
+// float64(float32) as Go compiles it on amd64 (cvtss2sd), on the bits: exact
+// for every number (denormals renormalised, so no device denormal mode is
+// involved), a NaN quieted with its sign and payload kept.
+MFH_DEV mfh_u64 f64_bits_of_f32(mfh_u32 b)
+{
+    const mfh_u64 sign = (mfh_u64)(b >> 31) << 63;
+    const mfh_u32 e = (b >> 23) & 0xffu, m = b & 0x7fffffu;
+    if (e == 0xffu) return sign | 0x7ff0000000000000ull | (m ? 0x0008000000000000ull : 0ull) | ((mfh_u64)m << 29);
+    if (e != 0u) return sign | ((mfh_u64)(e + 896u) << 52) | ((mfh_u64)m << 29);
+    if (m == 0u) return sign;
+    const int p = 31 - __builtin_clz(m);  // top set bit of the denormal's fraction, 0..22
+    return sign | ((mfh_u64)(p + 874) << 52) | (((mfh_u64)m << (52 - p)) & 0xfffffffffffffull);
+}
+
+// The f64 bits of element k of a register copy of consecutive elements
+// (Int4: nibble k of the copy).  Integers convert with correctly rounded
+// int -> f64 conversions (the 64-bit ones as two exact halves and one add).
+template <int IN>
+MFH_DEV mfh_u64 f64_reg(const mfh_u32* w, int k)
+{
+    if constexpr (IN == kFloat64) return (mfh_u64)w[2 * k] | ((mfh_u64)w[2 * k + 1] << 32);
+    else if constexpr (IN == kInt64)
+        return __builtin_bit_cast(mfh_u64, (double)(long long)((mfh_u64)w[2 * k] | ((mfh_u64)w[2 * k + 1] << 32)));
+    else if constexpr (IN == kUint64)
+        return __builtin_bit_cast(mfh_u64, (double)((mfh_u64)w[2 * k] | ((mfh_u64)w[2 * k + 1] << 32)));
+    else if constexpr (IN == kInt32) return __builtin_bit_cast(mfh_u64, (double)(int)w[k]);
+    else if constexpr (IN == kUint32) return __builtin_bit_cast(mfh_u64, (double)w[k]);
+    else if constexpr (IN == kInt4) return __builtin_bit_cast(mfh_u64, (double)mfh_int4_at(w[k >> 3], (mfh_u32)(k & 7)));
+    else if constexpr (IN == kF8E4M3 || IN == kF8E5M2) {
+        const mfh_u32 code = (w[k >> 2] >> ((k & 3) * 8)) & 0xffu;
+        return f64_bits_of_f32(IN == kF8E4M3 ? mfh_e4m3_bits(code) : mfh_e5m2_bits(code));
+    } else if constexpr (IN == kInt16 || IN == kUint16 || IN == kInt8 || IN == kUint8)
+        return __builtin_bit_cast(mfh_u64, (double)decode_reg<IN>(w, k));  // exact in f32
+    else return f64_bits_of_f32(mfh_bits(decode_reg<IN>(w, k)));          // f32, f16, bf16
+}
+
+// Element i from memory (tails, misaligned buffers).
+template <int IN>
+MFH_DEV mfh_u64 f64_at(const void* in, mfh_i64 i)
+{
+    if constexpr (IN == kInt4) {
+        const mfh_u32 byte = static_cast<const mfh_u8*>(in)[i >> 1];
+        return __builtin_bit_cast(mfh_u64, (double)mfh_int4_at(byte, (mfh_u32)(i & 1)));
+    } else {
+        constexpr int S = IN == kF8E4M3 || IN == kF8E5M2 ? 1 : size_of<IN>();
+        mfh_u32 w[2] = {0u, 0u};
+        const mfh_u8* p = static_cast<const mfh_u8*>(in) + i * S;
+#pragma unroll
+        for (int b = 0; b < S; b++) w[b >> 2] |= (mfh_u32)p[b] << (8 * (b & 3));
+        return f64_reg<IN>(w, 0);
+    }
+}
+
+// Item = 2 elements -> one 16-byte store; the item's 2 * size source bytes
+// (one byte for two Int4 nibbles) are one load.  Elements past the last whole
+// item, and every element when a buffer is not aligned, run the element loop.
+template <int IN, int BS>
+__global__ __launch_bounds__(BS) void k_widen_f64(const void* __restrict__ in, void* __restrict__ out, mfh_i64 n,
+                                                      int vec_ok)
+{
+    constexpr int S = IN == kF8E4M3 || IN == kF8E5M2 ? 1 : IN == kInt4 ? 0 : size_of<IN>();
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    const mfh_i64 nitems = vec_ok ? n / 2 : 0;
+    u32x4* dst = reinterpret_cast<u32x4*>(out);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nitems; v += stride) {
+        mfh_u32 w[4] = {0u, 0u, 0u, 0u};
+        if constexpr (S == 8) {
+            const u32x4 x = load_nt(reinterpret_cast<const u32x4*>(in) + v);
+            w[0] = x[0], w[1] = x[1], w[2] = x[2], w[3] = x[3];
+        } else if constexpr (S == 4) {
+            const u32x2 x = reinterpret_cast<const u32x2*>(in)[v];
+            w[0] = x[0], w[1] = x[1];
+        } else if constexpr (S == 2) {
+            w[0] = reinterpret_cast<const mfh_u32*>(in)[v];
+        } else if constexpr (S == 1) {
+            w[0] = reinterpret_cast<const mfh_u16*>(in)[v];
+        } else {
+            w[0] = static_cast<const mfh_u8*>(in)[v];  // Int4: two nibbles
+        }
+        const mfh_u64 a = f64_reg<IN>(w, 0), b = f64_reg<IN>(w, 1);
+        store_nt(&dst[v], u32x4{(mfh_u32)a, (mfh_u32)(a >> 32), (mfh_u32)b, (mfh_u32)(b >> 32)});
+    }
+    for (mfh_i64 i = nitems * 2 + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride)
+        static_cast<mfh_u64*>(out)[i] = f64_at<IN>(in, i);
+}
+
+int launch_widen_f64(const Device* dev, void* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
+{
+    const int size = in_dt == kF8E4M3 || in_dt == kF8E5M2 ? 1 : in_dt == kInt4 ? 0 : dtype_size(in_dt);
+    if (size == 0 && in_dt != kInt4)
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+    const int vec_ok = aligned16(out) && aligned(in, (unsigned)std::max(1, 2 * size)) && n >= 2;
+    return with_block(cast_threads(in_dt, 8), [&](auto block) {
+        constexpr int BS = decltype(block)::value;
+        const unsigned grid = vec_ok ? grid_for(n / 2, dev, Kern::kConvert, 1, BS) : grid_for(n, dev, Kern::kConvert, 1, BS);
+        switch (in_dt) {
+#define MFH_WIDEN_CASE(DT) \
+    case DT: k_widen_f64<DT, BS><<<grid, BS, 0, stream>>>(in, out, n, vec_ok); break;
+            MFH_WIDEN_CASE(kFloat64)
+            MFH_WIDEN_CASE(kFloat32)
+            MFH_WIDEN_CASE(kFloat16)
+            MFH_WIDEN_CASE(kBFloat16)
+            MFH_WIDEN_CASE(kF8E4M3)
+            MFH_WIDEN_CASE(kF8E5M2)
+            MFH_WIDEN_CASE(kInt64)
+            MFH_WIDEN_CASE(kInt32)
+            MFH_WIDEN_CASE(kInt16)
+            MFH_WIDEN_CASE(kInt8)
+            MFH_WIDEN_CASE(kInt4)
+            MFH_WIDEN_CASE(kUint64)
+            MFH_WIDEN_CASE(kUint32)
+            MFH_WIDEN_CASE(kUint16)
+            MFH_WIDEN_CASE(kUint8)
+#undef MFH_WIDEN_CASE
+        default:
+            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+        }
+        return launch_status("k_widen_f64");
+    });
 }
 
 bool is_out_dtype(int dt) { return dt == kFloat32 || dt == kBFloat16 || dt == kFloat16; }
-
-bool aligned(const void* p, unsigned bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
 
 template <template <int> class F, typename... A>
 int by_out(int out_dt, A... args)
@@ -716,17 +892,18 @@ int mfh_convert(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype, 
     const Device* dev;
     MFH_TRY(bind_device(&dev));
     if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: negative count %lld", (long long)count);
-    const bool to_fp8 = out_dtype == kF8E4M3 || out_dtype == kF8E5M2;
-    if (!is_out_dtype(out_dtype) && !to_fp8)
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: output dtype %s is not f32/bf16/f16/fp8",
+    const bool to_byte = out_dtype == kF8E4M3 || out_dtype == kF8E5M2 || out_dtype == kInt8;
+    if (!is_out_dtype(out_dtype) && !to_byte && out_dtype != kFloat64)
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: output dtype %s is not f64/f32/bf16/f16/fp8/i8",
                     dtype_name(out_dtype));
     if (count == 0) return MFH_OK;
     if (!out || !in) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: NULL buffer");
     hipStream_t s = (hipStream_t)stream;
-    if (to_fp8)
-        return out_dtype == kF8E4M3
-                   ? launch_encode_fp8<kF8E4M3>(dev, static_cast<mfh_u8*>(out), in, in_dtype, count, s)
-                   : launch_encode_fp8<kF8E5M2>(dev, static_cast<mfh_u8*>(out), in, in_dtype, count, s);
+    mfh_u8* bytes = static_cast<mfh_u8*>(out);
+    if (out_dtype == kF8E4M3) return launch_encode_byte<kF8E4M3>(dev, bytes, in, in_dtype, count, s);
+    if (out_dtype == kF8E5M2) return launch_encode_byte<kF8E5M2>(dev, bytes, in, in_dtype, count, s);
+    if (out_dtype == kInt8) return launch_encode_byte<kInt8>(dev, bytes, in, in_dtype, count, s);
+    if (out_dtype == kFloat64) return launch_widen_f64(dev, out, in, in_dtype, count, s);
     if (in_dtype == kF8E4M3 || in_dtype == kF8E5M2)
         return by_out<Fp8Launch>(out_dtype, dev, out, in, (int)in_dtype, count, 1.0f, s);
     if (in_dtype == kInt4)

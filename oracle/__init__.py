@@ -92,7 +92,7 @@ def _declare(L):
     L.orc_int4_hi.restype = c.c_int8
     L.orc_int4_hi.argtypes = [c.c_uint8]
     L.orc_logical_elements.argtypes = [i32, i64, c.POINTER(i64)]
-    for name in ("orc_bytes_to_f64", "orc_bytes_to_f32", "orc_bytes_to_bf16", "orc_bytes_to_f16"):
+    for name in ("orc_bytes_to_f64", "orc_bytes_to_f32", "orc_bytes_to_bf16", "orc_bytes_to_f16", "orc_bytes_to_i8"):
         getattr(L, name).argtypes = [i32, vp, i64, vp]
     L.orc_f32_to_bf16_buf.argtypes = [vp, i64, vp]
     L.orc_f32_to_f16_buf.argtypes = [vp, i64, vp]
@@ -177,6 +177,18 @@ def bytes_to_f64(dtype: int, buf: np.ndarray) -> np.ndarray:
         raise OracleError("bad dtype or byte count")
     out = np.empty(n.value, dtype=np.float64)
     if lib().orc_bytes_to_f64(dtype, _ptr(buf), buf.size, _ptr(out)) != 0:
+        raise OracleError("unsupported dtype")
+    return out
+
+
+def bytes_to_i8(dtype: int, buf: np.ndarray) -> np.ndarray:
+    """BytesToInt8 (dtype/convert/convert.go:235-263); NaN gives 0."""
+    buf = np.ascontiguousarray(buf).view(np.uint8).reshape(-1)
+    n = ctypes.c_int64()
+    if lib().orc_logical_elements(dtype, buf.size, ctypes.byref(n)) != 0:
+        raise OracleError("bad dtype or byte count")
+    out = np.empty(n.value, dtype=np.int8)
+    if lib().orc_bytes_to_i8(dtype, _ptr(buf), buf.size, _ptr(out)) != 0:
         raise OracleError("unsupported dtype")
     return out
 

@@ -274,8 +274,22 @@ static uint32_t rd32(const uint8_t* p)
 }
 static uint64_t rd64(const uint8_t* p) { return (uint64_t)rd32(p) | ((uint64_t)rd32(p + 4) << 32); }
 
+/* float64(float32), as Go compiles it on amd64 (cvtss2sd): exact for every
+ * number, a NaN keeps its sign and payload (shifted into the top of the f64
+ * fraction) and is quieted.  Stated on the bits so the result does not depend
+ * on the host's conversion of signalling NaNs. */
+double orc_f32_to_f64(float value)
+{
+    uint32_t b = f32_bits(value);
+    if ((b & 0x7fffffffu) > 0x7f800000u)
+        return bits_f64(((uint64_t)(b >> 31) << 63) | 0x7ff8000000000000ull | ((uint64_t)(b & 0x7fffffu) << 29));
+    return (double)value;
+}
+
 /* BytesToFloat64, dtype/convert/convert.go:36-79 and the per-dtype decoders in
- * dtype/convert/decoders.go. */
+ * dtype/convert/decoders.go: float64 of the Float32() decode for the 32-, 16-
+ * and 8-bit float dtypes (decoders.go:44-124), float64(int) of the integers
+ * (:126-260), the nibbles of Int4 (:262-289). */
 int orc_bytes_to_f64(int dtype, const uint8_t* buf, int64_t nbytes, double* out)
 {
     int64_t n;
@@ -283,11 +297,11 @@ int orc_bytes_to_f64(int dtype, const uint8_t* buf, int64_t nbytes, double* out)
     for (int64_t i = 0; i < n; i++) {
         switch (dtype) {
         case ORC_FLOAT64: out[i] = bits_f64(rd64(buf + 8 * i)); break;
-        case ORC_FLOAT32: out[i] = (double)bits_f32(rd32(buf + 4 * i)); break;
-        case ORC_FLOAT16: out[i] = (double)orc_f16_to_f32(rd16(buf + 2 * i)); break;
-        case ORC_BFLOAT16: out[i] = (double)orc_bf16_to_f32(rd16(buf + 2 * i)); break;
-        case ORC_F8E4M3: out[i] = (double)orc_e4m3_to_f32(buf[i]); break;
-        case ORC_F8E5M2: out[i] = (double)orc_e5m2_to_f32(buf[i]); break;
+        case ORC_FLOAT32: out[i] = orc_f32_to_f64(bits_f32(rd32(buf + 4 * i))); break;
+        case ORC_FLOAT16: out[i] = orc_f32_to_f64(orc_f16_to_f32(rd16(buf + 2 * i))); break;
+        case ORC_BFLOAT16: out[i] = orc_f32_to_f64(orc_bf16_to_f32(rd16(buf + 2 * i))); break;
+        case ORC_F8E4M3: out[i] = orc_f32_to_f64(orc_e4m3_to_f32(buf[i])); break;
+        case ORC_F8E5M2: out[i] = orc_f32_to_f64(orc_e5m2_to_f32(buf[i])); break;
         case ORC_INT64: out[i] = (double)(int64_t)rd64(buf + 8 * i); break;
         case ORC_INT32: out[i] = (double)(int32_t)rd32(buf + 4 * i); break;
         case ORC_INT16: out[i] = (double)(int16_t)rd16(buf + 2 * i); break;
@@ -342,6 +356,35 @@ int orc_bytes_to_f32(int dtype, const uint8_t* buf, int64_t nbytes, float* out)
         return rc;
     }
     }
+}
+
+/* int8(value) after BytesToInt8's saturation (dtype/convert/convert.go:
+ * 235-263): below -128 gives -128, above 127 gives 127 (so -Inf and +Inf
+ * saturate), everything else truncates toward zero.  A NaN passes both
+ * comparisons; Go leaves int8(NaN) to the platform, and on amd64 (cvttsd2sl,
+ * whose low byte of 0x80000000 is 0) and arm64 (fcvtzs) it is 0, which this
+ * build states as the rule. */
+int8_t orc_f64_to_i8(double value)
+{
+    if (isnan(value)) return 0;
+    if (value < -128.0) return -128;
+    if (value > 127.0) return 127;
+    return (int8_t)value;
+}
+
+/* BytesToInt8, dtype/convert/convert.go:235-263: BytesToFloat64, then
+ * orc_f64_to_i8 per element. */
+int orc_bytes_to_i8(int dtype, const uint8_t* buf, int64_t nbytes, int8_t* out)
+{
+    int64_t n;
+    if (orc_logical_elements(dtype, nbytes, &n) != 0) return -1;
+    double* wide = (double*)malloc((size_t)(n > 0 ? n : 1) * sizeof(double));
+    if (!wide) return -1;
+    int rc = orc_bytes_to_f64(dtype, buf, nbytes, wide);
+    if (rc == 0)
+        for (int64_t i = 0; i < n; i++) out[i] = orc_f64_to_i8(wide[i]);
+    free(wide);
+    return rc;
 }
 
 /* BytesToBFloat16, dtype/convert/convert.go:155-169 (f32 then RNE). */

@@ -54,6 +54,10 @@ int orc_bytes_to_f64(int dtype, const uint8_t* buf, int64_t nbytes, double* out)
 int orc_bytes_to_f32(int dtype, const uint8_t* buf, int64_t nbytes, float* out);
 int orc_bytes_to_bf16(int dtype, const uint8_t* buf, int64_t nbytes, uint16_t* out);
 int orc_bytes_to_f16(int dtype, const uint8_t* buf, int64_t nbytes, uint16_t* out);
+/* BytesToInt8 (dtype/convert/convert.go:235-263); NaN gives 0. */
+int orc_bytes_to_i8(int dtype, const uint8_t* buf, int64_t nbytes, int8_t* out);
+double orc_f32_to_f64(float value);
+int8_t orc_f64_to_i8(double value);
 void orc_f32_to_bf16_buf(const float* in, int64_t n, uint16_t* out);
 void orc_f32_to_f16_buf(const float* in, int64_t n, uint16_t* out);
 

@@ -598,3 +598,85 @@ def test_new_checks_catch_planted_mistakes():
                       for xi, yi in zip(x[ok], y[ok])], dtype=np.float32)
     unfused = (y[ok] + (a * x[ok]).astype(np.float32)).astype(np.float32)
     assert not np.array_equal(_narrow(fused, O.FLOAT16), _narrow(unfused, O.FLOAT16))
+
+
+# --------------------------------------------------------------------------
+# BytesToFloat64 and BytesToInt8 (dtype/convert/convert.go:36-79, 235-263).
+# --------------------------------------------------------------------------
+
+def _f32_probe_bits(rng):
+    r = rng.integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0, 0x80000000, 1, 0x807FFFFF, 0x7F7FFFFF, 0x7F800000, 0xFF800000, 0x7F800001,
+                        0xFFBFFFFF, 0x7FC00000, 0xFFC12345, 0x00800000], dtype=np.uint32)
+    return np.concatenate([r, special])
+
+
+def test_f32_to_f64_matches_the_hardware_widening():
+    # numpy widens with the host's cvtss2sd, the instruction Go's float64(f32)
+    # compiles to on amd64: exact for numbers, NaN quieted with its payload.
+    u = _f32_probe_bits(np.random.default_rng(14))
+    with np.errstate(invalid="ignore"):
+        ref = u.view(np.float32).astype(np.float64).view(np.uint64)
+    got = O.bytes_to_f64(O.FLOAT32, u).view(np.uint64)
+    assert np.array_equal(got, ref)
+    # every 16-bit and FP8 code: the f64 value of the Float32() decode
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    for dt in (O.FLOAT16, O.BFLOAT16):
+        with np.errstate(invalid="ignore"):
+            want = O.bytes_to_f32(dt, h).astype(np.float64).view(np.uint64)
+        assert np.array_equal(O.bytes_to_f64(dt, h).view(np.uint64), want)
+    codes = np.arange(256, dtype=np.uint8)
+    for dt in (O.F8E4M3, O.F8E5M2):
+        with np.errstate(invalid="ignore"):
+            want = O.bytes_to_f32(dt, codes).astype(np.float64).view(np.uint64)
+        assert np.array_equal(O.bytes_to_f64(dt, codes).view(np.uint64), want)
+
+
+def _i8_closed(d):
+    """Saturate then truncate toward zero, NaN to 0, with numpy's own clip and trunc."""
+    d = np.asarray(d, dtype=np.float64)
+    with np.errstate(invalid="ignore"):
+        t = np.clip(np.trunc(np.where(np.isnan(d), 0.0, d)), -128, 127)
+    return t.astype(np.int8)
+
+
+BYTES_TO_I8_EDGES = [0.0, -0.0, 0.999, -0.999, 1.0, -1.0, 1.9999999999, -1.9999999999, 126.9, 127.0, 127.5, 127.999,
+                     128.0, 128.5, 1e30, -127.9, -128.0, -128.5, -128.999, -129.0, -1e30, float("inf"), float("-inf"),
+                     float("nan"), -float("nan")]
+
+
+def test_bytes_to_i8_is_saturate_then_truncate():
+    rng = np.random.default_rng(15)
+    d = np.concatenate([np.array(BYTES_TO_I8_EDGES), rng.uniform(-300, 300, 1 << 16), rng.normal(0, 50, 1 << 16)])
+    assert np.array_equal(O.bytes_to_i8(O.FLOAT64, d), _i8_closed(d))
+    f = d.astype(np.float32)
+    assert np.array_equal(O.bytes_to_i8(O.FLOAT32, f), _i8_closed(f))
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    for dt in (O.FLOAT16, O.BFLOAT16):
+        assert np.array_equal(O.bytes_to_i8(dt, h), _i8_closed(O.bytes_to_f64(dt, h)))
+    codes = np.arange(256, dtype=np.uint8)
+    for dt in (O.F8E4M3, O.F8E5M2, O.INT8, O.UINT8):
+        assert np.array_equal(O.bytes_to_i8(dt, codes), _i8_closed(O.bytes_to_f64(dt, codes)))
+    assert O.bytes_to_i8(O.INT4, codes).tolist() == O.bytes_to_f64(O.INT4, codes).astype(np.int8).tolist()
+    for np_type, dt in ((np.int16, O.INT16), (np.uint16, O.UINT16), (np.int32, O.INT32), (np.uint32, O.UINT32),
+                        (np.int64, O.INT64), (np.uint64, O.UINT64)):
+        v = _wide_int_probe(np_type)
+        v = np.concatenate([v, np.array([np_type(x) for x in (0, 1, 127, 128, 200, 255)], dtype=np_type)])
+        if np.iinfo(np_type).min < 0:
+            v = np.concatenate([v, np.array([-1, -127, -128, -129, -1000], dtype=np_type)])
+        want = np.clip(v.astype(np.float64), -128, 127).astype(np.int8)  # integers: saturation only
+        assert np.array_equal(O.bytes_to_i8(dt, v), want), np_type
+
+
+def test_bytes_to_i8_checks_catch_planted_mistakes():
+    d = np.array(BYTES_TO_I8_EDGES)
+    ok = ~np.isnan(d)
+    want = _i8_closed(d)
+    with np.errstate(invalid="ignore"):
+        # rounding to nearest instead of truncating
+        assert not np.array_equal(np.clip(np.rint(d[ok]), -128, 127).astype(np.int8), want[ok])
+        # wrapping instead of saturating
+        assert not np.array_equal(np.trunc(d[ok & (np.abs(d) < 1e9)]).astype(np.int64).astype(np.int8),
+                                  want[ok & (np.abs(d) < 1e9)])
+        # truncating the f32 value of an f64 input (1.9999999999 becomes 2)
+        assert not np.array_equal(_i8_closed(d.astype(np.float32)), want)

@@ -112,6 +112,13 @@ def test_convert_golden(golden):
         O.bytes_to_f64(16, np.array([1], dtype=np.uint8))  # Bool is rejected (convert_test.go:70-75)
 
 
+def test_bytes_to_int8_golden(golden):
+    g = golden["bytes_to_int8"]
+    for case in (g["truncate"], g["saturate"]):
+        f = np.array(case["f32"], dtype=np.float32)
+        assert O.bytes_to_i8(O.FLOAT32, f).tolist() == case["i8"]
+
+
 def test_evaluator_golden(golden):
     g = golden["evaluator"]
     nodes = O.flatten((O.N_RELU, (O.N_ADD, ("in", 0), ("in", 1))))
