@@ -85,8 +85,10 @@ int mfh_backend_upload_sparse(mfh_backend* backend);
  * like axpyDevice (no counterpart in tensor.Backend): FP8 codes times one f32
  * scale (mfh_dequant_fp8), or Int4 nibbles times per-group scales
  * (mfh_dequant_int4; `group_scales` is host memory of
- * ceil(elements / group) values of `scale_dtype`).  Stored as `out_dtype`
- * (Float32, Float16 or BFloat16). */
+ * ceil(elements / group) values of `scale_dtype`, staged chunk by chunk with
+ * the nibbles they scale through the backend's pinned ring, so the upload
+ * allocates nothing besides the tensor).  Stored as `out_dtype` (Float32,
+ * Float16 or BFloat16). */
 int mfh_backend_upload_fp8(mfh_backend* backend, const int64_t* shape, int32_t rank, uint8_t fp8_dtype,
                            const void* codes, size_t n_bytes, float scale, uint8_t out_dtype, mfh_tensor** tensor);
 int mfh_backend_upload_int4(mfh_backend* backend, const int64_t* shape, int32_t rank, const void* packed,

@@ -63,8 +63,10 @@ int mfh_safetensors_read(const mfh_safetensors* file, const char* name, void* ds
  * (F32 / F16 / BF16 as written, F8_E4M3 / F8_E5M2 / I4 dequantised to BF16).
  * A non-NULL `scale_name` names a companion tensor (one element of F32, F16
  * or BF16) whose value scales an FP8 tensor; for an I4 tensor it names the
- * per-group scales, `group` elements each.  Other dtypes fail with
- * MFH_ERR_DTYPE_UNSUPPORTED. */
+ * per-group scales, `group` elements each, which are read from the file
+ * chunk by chunk beside the nibbles they scale.  A scale for an F32, F16 or
+ * BF16 tensor is MFH_ERR_INVALID_ARGUMENT (those are stored as written);
+ * other dtypes fail with MFH_ERR_DTYPE_UNSUPPORTED. */
 int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_backend* backend,
                          const char* scale_name, int64_t group, mfh_tensor** tensor);
 

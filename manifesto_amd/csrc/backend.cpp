@@ -178,49 +178,63 @@ struct MemorySource : Source {
 
 // Queues the upload of `n_src` source bytes holding `elements` elements into
 // `dst` (already allocated for the stored dtype) on the backend stream.
+// A scaled Int4 chunk holds whole scale groups of nibbles; its scales follow
+// its nibbles in the same staging slot (at a 16-byte aligned offset) and
+// cross PCIe in the same copy.
 int stream_in(BackendState& s, const Plan& p, Source& src, size_t n_src, int64_t elements, Storage& dst)
 {
     if (n_src == 0) return MFH_OK;
     MFH_TRY(ensure_staging(s));
     const bool convert = dequantised(p.src) || p.out != p.src;
-    // Source bytes per chunk: whole Int4 bytes and whole scale groups.
+    const bool scaled4 = p.src == kInt4 && p.scales;
+    const size_t ssize = scaled4 ? (size_t)dtype_size(p.scale_dt) : 0;
+    // Source bytes per chunk: whole Int4 bytes and whole scale groups, with
+    // room for the chunk's scales.
     size_t chunk = kChunk;
-    if (p.src == kInt4 && p.group > 0 && p.scales) {
-        int64_t per = std::max<int64_t>(1, (int64_t)(kChunk * 2) / p.group) * p.group;  // nibbles
-        if (per % 2) per *= 2;
-        if ((size_t)(per / 2) > kChunk) return fail(MFH_ERR_INVALID_ARGUMENT, "upload: group %lld exceeds a staging chunk", (long long)p.group);
-        chunk = (size_t)(per / 2);
+    if (scaled4) {
+        const int64_t unit = p.group % 2 ? 2 * p.group : p.group;  // nibbles: whole groups and whole bytes
+        const double bytes_per_nibble = 0.5 + (double)ssize / (double)p.group;
+        const int64_t units = (int64_t)(((double)kChunk - 16.0) / bytes_per_nibble) / unit;
+        if (units < 1)
+            return fail(MFH_ERR_INVALID_ARGUMENT, "upload: group %lld exceeds a staging chunk", (long long)p.group);
+        chunk = (size_t)(units * unit / 2);
     }
     const int out_size = dtype_size(p.out);
     size_t done = 0;
     for (int c = 0; done < n_src; c++) {
         const int slot = c % kRing;
         const size_t len = std::min(chunk, n_src - done);
+        int64_t first = 0, count = 0;  // elements of this chunk
+        if (p.src == kInt4) {
+            first = (int64_t)done * 2;
+            count = std::min<int64_t>((int64_t)len * 2, elements - first);
+        } else if (convert) {
+            const int in_size = dtype_size(p.src);
+            first = (int64_t)done / in_size;
+            count = (int64_t)len / in_size;
+        }
+        const size_t scale_at = (len + 15) & ~(size_t)15;
+        const size_t scale_len = scaled4 ? (size_t)((count + p.group - 1) / p.group) * ssize : 0;
         MFH_TRY(check_hip(hipEventSynchronize(s.slot_free[slot]), "hipEventSynchronize"));
         MFH_TRY(src.read(s.pinned[slot], done, len));
+        if (scaled4)
+            MFH_TRY(p.scales->read(static_cast<uint8_t*>(s.pinned[slot]) + scale_at, (size_t)(first / p.group) * ssize,
+                                   scale_len));
         if (!convert) {
             MFH_TRY(check_hip(hipMemcpyAsync(static_cast<uint8_t*>(dst.ptr) + done, s.pinned[slot], len,
                                              hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync(H2D)"));
         } else {
-            MFH_TRY(check_hip(hipMemcpyAsync(s.dstage[slot], s.pinned[slot], len, hipMemcpyHostToDevice, s.stream),
+            const size_t copy = scaled4 ? scale_at + scale_len : len;
+            MFH_TRY(check_hip(hipMemcpyAsync(s.dstage[slot], s.pinned[slot], copy, hipMemcpyHostToDevice, s.stream),
                               "hipMemcpyAsync(H2D)"));
-            int64_t first, count;  // elements of this chunk
-            if (p.src == kInt4) {
-                first = (int64_t)done * 2;
-                count = std::min<int64_t>((int64_t)len * 2, elements - first);
-            } else {
-                const int in_size = dtype_size(p.src);
-                first = (int64_t)done / in_size;
-                count = (int64_t)len / in_size;
-            }
             void* out = static_cast<uint8_t*>(dst.ptr) + first * out_size;
             int rc;
             if (p.src == kF8E4M3 || p.src == kF8E5M2)
                 rc = mfh_dequant_fp8(out, (uint8_t)p.out, s.dstage[slot], (uint8_t)p.src, count, p.scale, s.stream);
-            else if (p.src == kInt4 && p.scales)
+            else if (scaled4)
                 rc = mfh_dequant_int4(out, (uint8_t)p.out, s.dstage[slot], count,
-                                      static_cast<const uint8_t*>(p.scales) + (first / p.group) * dtype_size(p.scale_dt),
-                                      (uint8_t)p.scale_dt, p.group, s.stream);
+                                      static_cast<const uint8_t*>(s.dstage[slot]) + scale_at, (uint8_t)p.scale_dt,
+                                      p.group, s.stream);
             else
                 rc = mfh_convert(out, (uint8_t)p.out, s.dstage[slot], (uint8_t)p.src, count, s.stream);
             MFH_TRY(rc);
@@ -436,28 +450,14 @@ int mfh_backend_upload_int4(mfh_backend* backend, const int64_t* shape, int32_t 
     MFH_TRY(make_shape(shape, rank, &dims, &elements));
     const int64_t n_scales = (elements + group - 1) / group;
     if (n_scales > 0 && !group_scales) return fail(MFH_ERR_INVALID_ARGUMENT, "upload_int4: group scales are NULL");
-    void* dscales = nullptr;
-    const size_t scale_bytes = (size_t)n_scales * dtype_size(scale_dtype);
-    if (scale_bytes) {
-        MFH_TRY(check_hip(hipMalloc(&dscales, scale_bytes), "hipMalloc(scales)"));
-        int rc = check_hip(hipMemcpy(dscales, group_scales, scale_bytes, hipMemcpyHostToDevice), "hipMemcpy(scales)");
-        if (rc != MFH_OK) {
-            (void)hipFree(dscales);
-            return rc;
-        }
-    }
+    MemorySource scales(group_scales);
     Plan p;
     p.src = kInt4;
     p.out = out_dtype;
-    p.scales = dscales;
+    p.scales = &scales;
     p.scale_dt = scale_dtype;
     p.group = group;
-    int rc = upload(backend, shape, rank, p, packed, n_bytes, true, tensor);
-    if (dscales) {
-        (void)hipStreamSynchronize(backend->state->stream);
-        (void)hipFree(dscales);
-    }
-    return rc;
+    return upload(backend, shape, rank, p, packed, n_bytes, true, tensor);
 }
 
 int mfh_backend_download(mfh_backend* backend, const mfh_tensor* tensor, uint8_t* dtype, void* dst, size_t dst_bytes,

@@ -538,8 +538,12 @@ int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_back
     src.name = e->name;
     const Entry* se = scale_name ? find(file, scale_name) : nullptr;
     if (scale_name && !se) return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors: missing tensor \"%s\"", scale_name);
+    if (se && as_is)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors: tensor \"%s\" is %s, which is stored as written; a scale "
+                    "(\"%s\") applies only to F8_E4M3, F8_E5M2 and I4 tensors", e->name.c_str(), e->dtype_name.c_str(),
+                    se->name.c_str());
     if (se && fp8) MFH_TRY(read_scalar(*file, *se, &p.scale));
-    void* dscales = nullptr;
+    FileSource scales;
     if (se && e->dtype == kInt4) {
         if (group <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors: group must be positive, got %lld", (long long)group);
         if (se->dtype != kFloat32 && se->dtype != kFloat16 && se->dtype != kBFloat16)
@@ -556,26 +560,15 @@ int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_back
         if (s_len != need)
             return fail(MFH_ERR_SHAPE_MISMATCH, "safetensors: scales \"%s\" hold %zu bytes, %lld elements in groups of "
                         "%lld need %zu", se->name.c_str(), s_len, (long long)elements, (long long)group, need);
-        std::vector<uint8_t> host(s_len);
-        if (s_len && read_full(file->fd, host.data(), s_len, s_at))
-            return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors read \"%s\": unexpected EOF", se->name.c_str());
-        const Device* dev;
-        MFH_TRY(bind_device(&dev));
-        if (s_len) {
-            MFH_TRY(check_hip(hipMalloc(&dscales, s_len), "hipMalloc(scales)"));
-            int rc = check_hip(hipMemcpy(dscales, host.data(), s_len, hipMemcpyHostToDevice), "hipMemcpy(scales)");
-            if (rc != MFH_OK) {
-                (void)hipFree(dscales);
-                return rc;
-            }
-        }
-        p.scales = dscales;
+        // streamed from the file chunk by chunk beside the nibbles they scale
+        scales.fd = file->fd;
+        scales.base = s_at;
+        scales.name = se->name;
+        p.scales = &scales;
         p.scale_dt = se->dtype;
         p.group = group;
     }
-    int rc = upload_from(backend, e->shape.data(), (int32_t)e->shape.size(), p, src, len, true, tensor);
-    if (dscales) (void)hipFree(dscales);  // the upload has completed (wait = true)
-    return rc;
+    return upload_from(backend, e->shape.data(), (int32_t)e->shape.size(), p, src, len, true, tensor);
 }
 
 }  // extern "C"

@@ -4,6 +4,7 @@ FP8 / I4 dequantised there; results are checked bit for bit against the
 oracle on the same bytes."""
 import json
 import struct
+import time
 
 import numpy as np
 import pytest
@@ -107,3 +108,59 @@ def test_load_errors(backend, tmp_path):
     assert e.value.code == -3
     with pytest.raises(M.MFHError, match="missing tensor"):
         f.load("nope", backend)
+
+
+def test_load_many_grouped_int4_tensors(backend, tmp_path):
+    # Int4 weights with their group scales, tensor after tensor: the scales
+    # stream through the pinned ring beside the nibbles, so a load allocates
+    # nothing but its output and runs at the PCIe rate of the packed bytes.
+    rng = np.random.default_rng(2)
+    rows, cols, group = 14336, 4096, 128
+    entries, want = {}, {}
+    for k in range(4):
+        packed = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+        s16 = O.f32_to_f16(rng.uniform(0.005, 0.02, rows * cols // group).astype(np.float32))
+        entries[f"w{k}"] = ("I4", [rows, cols], packed.tobytes())
+        entries[f"w{k}_scales"] = ("F16", [rows, cols // group], s16.tobytes())
+        want[f"w{k}"] = (packed, s16)
+    f = SafeTensorsFile(write(tmp_path / "many.safetensors", entries))
+    f.load("w0", backend, scale="w0_scales", group=group).release()  # staging ring and page cache warm
+    t0 = time.perf_counter()
+    tensors = [f.load(f"w{k}", backend, scale=f"w{k}_scales", group=group) for k in range(4)]
+    dt = time.perf_counter() - t0
+    src_bytes = 4 * (rows * cols // 2 + rows * cols // group * 2)
+    log(f"safetensors: 4 grouped Int4 tensors [{rows},{cols}] in {dt * 1e3:.1f} ms, "
+        f"{src_bytes / dt / 1e9:.1f} GB/s of file bytes")
+    for k, t in enumerate(tensors):
+        packed, s16 = want[f"w{k}"]
+        got = np.frombuffer(backend.download(t)[1], np.uint16)
+        np.testing.assert_array_equal(got, O.dequant_int4(packed, rows * cols, s16, O.FLOAT16, group, O.BFLOAT16))
+        t.release()
+
+
+@pytest.mark.parametrize("group, n", [(7, 40 * (1 << 20) + 5), (1, 14 * (1 << 20) + 1), (96, 33 * (1 << 20) + 2),
+                                      (4096, 3 * (1 << 22) + 77)])
+def test_grouped_int4_across_staging_chunks(backend, tmp_path, group, n):
+    # chunks hold whole groups and whole bytes, odd and tiny groups included,
+    # with a partial last group
+    rng = np.random.default_rng(group)
+    packed = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
+    scales = rng.uniform(-0.05, 0.05, -(-n // group)).astype(np.float32)
+    f = SafeTensorsFile(write(tmp_path / "g.safetensors", {
+        "q": ("I4", [n], packed.tobytes()), "qs": ("F32", [scales.size], scales.tobytes())}))
+    t = f.load("q", backend, scale="qs", group=group)
+    got = np.frombuffer(backend.download(t)[1], np.uint16)
+    np.testing.assert_array_equal(got, O.dequant_int4(packed, n, scales, O.FLOAT32, group, O.BFLOAT16))
+    t.release()
+    t = backend.upload_int4([n], packed, scales, O.FLOAT32, group)
+    np.testing.assert_array_equal(np.frombuffer(backend.download(t)[1], np.uint16), got)
+    t.release()
+
+
+def test_scale_for_a_tensor_stored_as_written_is_refused(backend, tmp_path):
+    f = SafeTensorsFile(write(tmp_path / "a.safetensors", {
+        "w": ("BF16", [4], O.f32_to_bf16(np.ones(4, np.float32)).tobytes()),
+        "s": ("F32", [1], np.array([2.0], np.float32).tobytes())}))
+    with pytest.raises(M.MFHError, match="stored as written") as e:
+        f.load("w", backend, scale="s")
+    assert e.value.code == -1

@@ -136,3 +136,17 @@ def test_load_requires_a_device(tmp_path):
     with pytest.raises(M.MFHError):
         Backend(0)
     assert f.read("a") == b"\0" * 4
+
+
+def test_scale_for_a_tensor_stored_as_written_is_refused(tmp_path):
+    # Checked from the index before any device work, so it needs no GPU: a
+    # scale names nothing to multiply for an F32/F16/BF16 tensor.
+    import ctypes
+    from manifesto_amd import safetensors as S
+    f = SafeTensorsFile(write_raw(tmp_path / "s.safetensors", {
+        "w": {"dtype": "F16", "shape": [2], "data_offsets": [0, 4]},
+        "s": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 8))
+    h = ctypes.c_void_p()
+    rc = S._L().mfh_safetensors_load(f._h, b"w", None, b"s", 0, ctypes.byref(h))
+    assert rc == -1 and "stored as written" in M.last_error()
+    assert not h.value
