@@ -3,16 +3,22 @@
 Headline (BASELINE.json metric, configs[1]): FP8 e4m3 -> bf16 dequantisation of
 a [4096, 14336] byte tensor with a per-tensor f32 scale of 0.0125, reported as
 achieved HBM GB/s (algorithmic bytes / kernel time) and as a fraction of the
-MI355X's 8 TB/s.  One step = one kernel launch over one resident batch.  Buffer
-sets are rotated (at least four, and at least twice the 256 MB Infinity Cache
-in flight), and the
-timed steps are replayed from a captured HIP graph so the clock sees kernel
-time, not Python launch overhead; the W warm-up steps replay the same graph
-first, so the timed replay runs at the settled clock of sustained load.  The other BASELINE configs (axpy, SwiGLU,
-the f16 gelu chain, Int4) are measured the same way and listed under
-"configs".  The CPU baseline is the oracle (a C restatement of the Go loops,
--O2 -ffp-contract=off) timed on this host, single-threaded as the Go loops
-run; "cpu_baseline_all_cores" splits the same sample over the host's threads.
+MI355X's 8 TB/s.  One step = one kernel launch over one resident batch.
+
+Buffer sets are rotated so that every cycle reads at least 1 GiB of distinct
+inputs (four times the 256 MB Infinity Cache) and the footprint is at least
+twice that cache: the kernels' non-temporal stores do not displace cached
+inputs, so a rotation whose inputs alone fit in the cache (four FP8 sets hold
+235 MB of codes) measures cache reads, not HBM (FP8 then reads 7.07 against
+6.2 TB/s, Int4 6.8 against 5.1).  The timed steps are replayed from a
+captured HIP graph so the clock sees kernel time, not Python launch overhead;
+the W warm-up steps replay the same graph first.  After timing, a sample of
+the timed outputs is checked against the oracle ("sample_check").  The other
+BASELINE configs (axpy, SwiGLU, the f16 gelu chain, Int4) are measured the
+same way and listed under "configs".  The CPU baseline is the oracle (a C
+restatement of the Go loops, -O2 -ffp-contract=off) timed on this host,
+single-threaded as the Go loops run; "cpu_baseline_all_cores" splits the same
+sample over the host's threads.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only N] [--sweep] [--profile REPS]
 """
@@ -32,6 +38,8 @@ sys.path.insert(0, ROOT)
 PEAK_GBS = 8000.0
 METRIC = "achieved HBM GB/s (% of MI355X peak) for fused elementwise + FP8/Int4 dequant"
 MALL_BYTES = 256 << 20
+SEED = 0x5EED
+CHECK_ELEMENTS = 1 << 20
 
 
 def log(msg):
@@ -52,11 +60,32 @@ class Workload:
         return self.torch.cuda.current_stream().cuda_stream
 
     def rotations(self):
-        return max(4, -(-2 * MALL_BYTES // self.bytes_per_step))
+        """Sets per rotation: at least four, a footprint of at least twice the
+        Infinity Cache, and at least four caches' worth of distinct inputs."""
+        return max(4, -(-2 * MALL_BYTES // self.bytes_per_step), -(-4 * MALL_BYTES // self.read_bytes_per_step))
 
     def setup(self):
         for _ in range(self.rotations()):
             self.sets.append(self.make_set())
+
+    def generator(self):
+        """Device RNG of the next set: seed 0x5EED + 1000 * config + set."""
+        return self.torch.Generator(device="cuda").manual_seed(SEED + 1000 * self.cfg + len(self.sets))
+
+    @staticmethod
+    def compare(got, want, width=16):
+        """Bit-identical fraction and largest distance in storage ulps."""
+        g, w = got.astype(np.int64) & ((1 << width) - 1), want.astype(np.int64) & ((1 << width) - 1)
+        sign = 1 << (width - 1)
+        key = lambda b: np.where(b & sign, sign - b, b)  # noqa: E731
+        return float(np.mean(g == w)), int(np.abs(key(g) - key(w)).max())
+
+    def host(self, t, m=CHECK_ELEMENTS):
+        """The first m elements of a device tensor as a numpy array of its raw bits."""
+        t = t.reshape(-1)[:m]
+        if t.dtype in (self.torch.bfloat16, self.torch.float16):
+            t = t.view(self.torch.int16)
+        return t.cpu().numpy()
 
     def step(self, i):
         self.launch(self.sets[i % len(self.sets)])
@@ -71,11 +100,12 @@ class Axpy(Workload):
     n = 1 << 24
     bytes_for = staticmethod(lambda n: 12 * n)
     bytes_per_step = 12 * n
+    read_bytes_per_step = 8 * n
     kernel = "k_axpy_f32"
 
     def make_set(self):
         t = self.torch
-        g = t.Generator(device="cuda").manual_seed(1 + len(self.sets))
+        g = self.generator()
         x = t.rand(self.n, device="cuda", generator=g) * 2 - 1
         y = t.rand(self.n, device="cuda", generator=g) * 2 - 1
         return x, y
@@ -83,6 +113,15 @@ class Axpy(Workload):
     def launch(self, s):
         x, y = s
         self.M.axpy(y.data_ptr(), x.data_ptr(), self.n, 0.75, self.M.FLOAT32, self.stream)
+
+    def check(self):
+        """One more launch on set 0 against the oracle's axpy, bit for bit."""
+        x, y = self.sets[0]
+        x0, y0 = self.host(x), self.host(y)
+        self.launch(self.sets[0])
+        self.torch.cuda.synchronize()
+        exact, worst = self.compare(self.host(y).view(np.uint32), self.O.axpy_f32(y0, x0, 0.75).view(np.uint32), 32)
+        return {"elements": CHECK_ELEMENTS, "bit_identical": exact, "max_ulp": worst, "ok": exact == 1.0}
 
     def cpu_sample(self):
         rng = np.random.default_rng(1)
@@ -100,17 +139,24 @@ class Fp8(Workload):
     n = 4096 * 14336
     bytes_for = staticmethod(lambda n: 3 * n + 4)
     bytes_per_step = 3 * n + 4
+    read_bytes_per_step = n + 4
     kernel = "k_dequant_fp8<bf16>"
 
     def make_set(self):
         t = self.torch
-        g = t.Generator(device="cuda").manual_seed(2 + len(self.sets))
+        g = self.generator()
         return _rand_u8(t, self.n, g), t.empty(self.n, dtype=t.int16, device="cuda")
 
     def launch(self, s):
         src, out = s
         M = self.M
         M.dequant_fp8(out.data_ptr(), M.BFLOAT16, src.data_ptr(), M.F8E4M3, self.n, 0.0125, self.stream)
+
+    def check(self):
+        src, out = self.sets[0]
+        want = self.O.dequant_fp8(self.host(src), self.O.F8E4M3, 0.0125, self.O.BFLOAT16)
+        exact, worst = self.compare(self.host(out).view(np.uint16), want)
+        return {"elements": CHECK_ELEMENTS, "bit_identical": exact, "max_ulp": worst, "ok": exact == 1.0}
 
     def cpu_sample(self):
         rng = np.random.default_rng(2)
@@ -129,6 +175,7 @@ class SwiGLU(Workload):
     n = 8192 * 14336
     bytes_for = staticmethod(lambda n: 6 * n)
     bytes_per_step = 6 * n
+    read_bytes_per_step = 4 * n
     kernel = "fused_swiglu"
 
     def setup(self):
@@ -139,7 +186,7 @@ class SwiGLU(Workload):
 
     def make_set(self):
         t = self.torch
-        g = t.Generator(device="cuda").manual_seed(3 + len(self.sets))
+        g = self.generator()
         gate = t.randn(self.n, device="cuda", generator=g).to(t.bfloat16)
         up = t.randn(self.n, device="cuda", generator=g).to(t.bfloat16)
         return gate, up, t.empty(self.n, dtype=t.bfloat16, device="cuda")
@@ -147,6 +194,16 @@ class SwiGLU(Workload):
     def launch(self, s):
         gate, up, out = s
         self.k.launch([gate.data_ptr(), up.data_ptr()], out.data_ptr(), self.n, self.stream)
+
+    def check(self):
+        """Against the oracle's f64 Silu: the fast form may be 1 bf16 ulp off."""
+        O = self.O
+        gate, up, out = self.sets[0]
+        g, u = self.host(gate).view(np.uint16), self.host(up).view(np.uint16)
+        want = O.f32_to_bf16(O.run(self.nodes, [O.decode(g, O.BFLOAT16), O.decode(u, O.BFLOAT16)], g.size))
+        exact, worst = self.compare(self.host(out).view(np.uint16), want)
+        return {"elements": CHECK_ELEMENTS, "bit_identical": exact, "max_ulp": worst,
+                "ok": exact >= 0.999 and worst <= 1}
 
     def cpu_sample(self):
         O = self.O
@@ -167,6 +224,7 @@ class GeluChain(Workload):
     n = 4 * 4096 * 4096
     bytes_for = staticmethod(lambda n: 6 * n + 4096 * 2)
     bytes_per_step = 6 * n + 4096 * 2
+    read_bytes_per_step = 4 * n + 4096 * 2
     kernel = "fused_gelu_chain"
 
     def setup(self):
@@ -180,7 +238,7 @@ class GeluChain(Workload):
 
     def make_set(self):
         t = self.torch
-        g = t.Generator(device="cuda").manual_seed(4 + len(self.sets))
+        g = self.generator()
         x = t.randn(self.n, device="cuda", generator=g).to(t.float16)
         res = t.randn(self.n, device="cuda", generator=g).to(t.float16)
         bias = (t.randn(4096, device="cuda", generator=g) * 0.02).to(t.float16)
@@ -191,6 +249,18 @@ class GeluChain(Workload):
         x, bias, s, res, out = st
         self.k.launch([x.data_ptr(), bias.data_ptr(), s.data_ptr(), res.data_ptr()], out.data_ptr(),
                       self.n, self.stream)
+
+    def check(self):
+        """Against the oracle's f64 Gelu: where the residual add cancels, the
+        fast form's 2 f32 ulps can be several f16 ulps of the sum."""
+        O = self.O
+        x, bias, sc, res, out = self.sets[0]
+        xs, rs = self.host(x).view(np.uint16), self.host(res).view(np.uint16)
+        b = O.decode(self.host(bias, 4096).view(np.uint16), O.FLOAT16)
+        want = O.f32_to_f16(O.run(self.nodes, [O.decode(xs, O.FLOAT16), b, np.array([1.1], np.float32),
+                                               O.decode(rs, O.FLOAT16)], xs.size, [0, 4096, 1, 0]))
+        exact, worst = self.compare(self.host(out).view(np.uint16), want)
+        return {"elements": CHECK_ELEMENTS, "bit_identical": exact, "max_ulp": worst, "ok": exact >= 0.999}
 
     def cpu_sample(self):
         O = self.O
@@ -214,11 +284,12 @@ class Int4(Workload):
     n = 14336 * 4096
     bytes_for = staticmethod(lambda n: n // 2 + (n // 128) * 2 + 2 * n)
     bytes_per_step = n // 2 + (n // 128) * 2 + 2 * n
+    read_bytes_per_step = n // 2 + (n // 128) * 2
     kernel = "k_dequant_int4<bf16,f16>"
 
     def make_set(self):
         t = self.torch
-        g = t.Generator(device="cuda").manual_seed(5 + len(self.sets))
+        g = self.generator()
         packed = _rand_u8(t, self.n // 2, g)
         scales = (t.rand(self.n // 128, device="cuda", generator=g) * 0.015 + 0.005).to(t.float16)
         return packed, scales, t.empty(self.n, dtype=t.int16, device="cuda")
@@ -228,6 +299,15 @@ class Int4(Workload):
         M = self.M
         M.dequant_int4(out.data_ptr(), M.BFLOAT16, packed.data_ptr(), self.n, scales.data_ptr(), M.FLOAT16,
                        128, self.stream)
+
+    def check(self):
+        O = self.O
+        packed, scales, out = self.sets[0]
+        p = self.host(packed, CHECK_ELEMENTS // 2)
+        sc = self.host(scales, CHECK_ELEMENTS // 128).view(np.uint16)
+        want = O.dequant_int4(p, CHECK_ELEMENTS, sc, O.FLOAT16, 128, O.BFLOAT16)
+        exact, worst = self.compare(self.host(out).view(np.uint16), want)
+        return {"elements": CHECK_ELEMENTS, "bit_identical": exact, "max_ulp": worst, "ok": exact == 1.0}
 
     def cpu_sample(self):
         O = self.O
@@ -460,7 +540,8 @@ def main():
              "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
              "elements_per_s": round(w.n / (ms * 1e-3), 1), "bytes_per_step": w.bytes_per_step,
              "steps_timed": n, "warmup_steps_run": warm_steps(w, args), "rotated_sets": len(w.sets),
-             "wall_s": round(wall, 4)}
+             "input_bytes_per_rotation": len(w.sets) * w.read_bytes_per_step, "wall_s": round(wall, 4),
+             "sample_check": w.check()}
         if not args.no_cpu:
             r["cpu_baseline"] = time_cpu(w)
             r["speedup_vs_cpu"] = round(gbs / r["cpu_baseline"]["value"], 1)
@@ -475,10 +556,14 @@ def main():
         "metric": METRIC, "value": head["GB_s"], "unit": "GB/s", "n_gpus": 1,
         "steps": head["steps_timed"], "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (seeded torch RNG on device; uniform bytes over all 256 codes)",
+        "data": ("synthetic: every rotated set from a device torch.Generator seeded 0x5EED + 1000 * config + set; "
+                 "FP8 bytes uniform over all 256 codes"),
         "config": {"workload": "BASELINE config 2: fp8_e4m3 -> bf16 dequant [4096,14336], scale 0.0125",
                    "elements": Fp8.n, "algorithmic_bytes_per_step": Fp8.bytes_per_step,
-                   "timing": "HIP events on the launch stream around one replay of a graph of K launches over rotated buffer sets, after ceil(W/K) untimed replays of the same graph"},
+                   "rotated_sets": head["rotated_sets"],
+                   "timing": ("HIP events on the launch stream around one replay of a graph of K launches over "
+                              "rotated buffer sets (>= 1 GiB of distinct inputs per rotation), after ceil(W/K) "
+                              "untimed replays of the same graph")},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": load_traffic(), "kernel": head["kernel"]},
         "cpu_baseline": head.get("cpu_baseline"),
