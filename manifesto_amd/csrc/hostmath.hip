@@ -30,19 +30,25 @@ MFH_DEV float axpy_step(float y, float x, float alpha)
     return y + product;
 }
 
+// A block of BS threads takes chunks of BS * U consecutive 16-byte items
+// (thread t holds items t, t + BS, ...), one-shot by default, so the launch
+// sweeps x and y in dispatch order: 6.5 TB/s at 64 threads x 1 item against
+// 6.2 for the best grid-stride shape, once x and y outgrow the Infinity Cache.
 template <int U, int BS>
 __global__ __launch_bounds__(BS) void k_axpy_f32(float* __restrict__ y, const float* __restrict__ x,
                                                      mfh_i64 n, float alpha, int vec_ok)
 {
-    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    constexpr mfh_i64 kChunk = (mfh_i64)BS * U;
     const mfh_i64 nvec = vec_ok ? (n >> 2) : 0;
+    const mfh_i64 nchunks = (nvec + kChunk - 1) / kChunk;
     u32x4* yv = reinterpret_cast<u32x4*>(y);
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nvec; v += stride * U) {
+    for (mfh_i64 c = blockIdx.x; c < nchunks; c += gridDim.x) {
+        const mfh_i64 first = c * kChunk + threadIdx.x;
         u32x4 a[U], b[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            mfh_i64 i = v + u * stride;
+            const mfh_i64 i = first + u * BS;
             if (i < nvec) {
                 a[u] = load_nt(&xv[i]);
                 b[u] = load_nt(&yv[i]);
@@ -50,7 +56,7 @@ __global__ __launch_bounds__(BS) void k_axpy_f32(float* __restrict__ y, const fl
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            mfh_i64 i = v + u * stride;
+            const mfh_i64 i = first + u * BS;
             if (i >= nvec) break;
             u32x4 o;
 #pragma unroll
@@ -58,6 +64,7 @@ __global__ __launch_bounds__(BS) void k_axpy_f32(float* __restrict__ y, const fl
             store_nt(&yv[i], o);
         }
     }
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
     for (mfh_i64 i = nvec * 4 + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride)
         y[i] = axpy_step(y[i], x[i], alpha);
 }
@@ -68,15 +75,17 @@ template <int DT, int U, int BS>
 __global__ __launch_bounds__(BS) void k_axpy16(mfh_u16* __restrict__ y, const mfh_u16* __restrict__ x,
                                                    mfh_i64 n, float alpha, int vec_ok)
 {
-    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    constexpr mfh_i64 kChunk = (mfh_i64)BS * U;
     const mfh_i64 nvec = vec_ok ? (n >> 3) : 0;
+    const mfh_i64 nchunks = (nvec + kChunk - 1) / kChunk;
     u32x4* yv = reinterpret_cast<u32x4*>(y);
     const u32x4* xv = reinterpret_cast<const u32x4*>(x);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nvec; v += stride * U) {
+    for (mfh_i64 c = blockIdx.x; c < nchunks; c += gridDim.x) {
+        const mfh_i64 first = c * kChunk + threadIdx.x;
         u32x4 a[U], b[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            mfh_i64 i = v + u * stride;
+            const mfh_i64 i = first + u * BS;
             if (i < nvec) {
                 a[u] = load_nt(&xv[i]);
                 b[u] = load_nt(&yv[i]);
@@ -84,7 +93,7 @@ __global__ __launch_bounds__(BS) void k_axpy16(mfh_u16* __restrict__ y, const mf
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            mfh_i64 i = v + u * stride;
+            const mfh_i64 i = first + u * BS;
             if (i >= nvec) break;
             u32x4 o;
 #pragma unroll
@@ -96,6 +105,7 @@ __global__ __launch_bounds__(BS) void k_axpy16(mfh_u16* __restrict__ y, const mf
             store_nt(&yv[i], o);
         }
     }
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
     for (mfh_i64 i = nvec * 8 + (mfh_i64)blockIdx.x * BS + threadIdx.x; i < n; i += stride) {
         float r = axpy_step(dec16<DT>(y[i]), dec16<DT>(x[i]), alpha);
         y[i] = (mfh_u16)(enc16x2<DT>(r, 0.0f) & 0xffffu);

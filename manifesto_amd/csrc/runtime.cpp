@@ -201,7 +201,7 @@ constexpr unsigned kSizes64To256 = (1u << 6) | (1u << 7) | (1u << 8);
 constexpr unsigned kSizes64To1024 = kSizes64To256 | (1u << 9) | (1u << 10);
 LaunchCfg g_cfg[(int)Kern::kCount] = {
     {"fp8", {kMaxBlocksPerCu}, {2}, {128}, kSizes64To256},
-    {"int4", {kMaxBlocksPerCu}, {2}, {256}, 1u << 8},
+    {"int4", {kMaxBlocksPerCu}, {2}, {256}, kSizes64To256},
     {"axpy", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
     {"axpy16", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
     {"convert", {kMaxBlocksPerCu}, {1}, {0}, kSizes64To256},

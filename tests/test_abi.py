@@ -230,11 +230,13 @@ def test_launch_threads_set_keep_restore_and_limits():
             assert M.get_launch_threads("fp8") == t
         with pytest.raises(M.MFHError, match="workgroups of 64, 128, 256 threads, not 512"):
             M.set_launch_threads("axpy", 512)
-        with pytest.raises(M.MFHError, match="workgroups of 256 threads, not 128"):
-            M.set_launch_threads("int4", 128)
-        M.set_launch_threads("int4", 256)
+        with pytest.raises(M.MFHError, match="workgroups of 64, 128, 256 threads, not 1024"):
+            M.set_launch_threads("int4", 1024)
+        M.set_launch_threads("int4", 128)
+        assert M.get_launch_threads("int4") == 128
     finally:
         M.set_launch_threads("fp8", -1)
+        M.set_launch_threads("int4", -1)
     assert M.get_launch_threads("fp8") == 128
     with pytest.raises(M.MFHError, match="unknown kernel family"):
         M.set_launch_threads("nope", 64)

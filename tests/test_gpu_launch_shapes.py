@@ -17,7 +17,8 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 1), (1, 2), (1, 4), (3, 2), (-1, -1)]  # (workgroups per CU, items per thread); -1: default
 # workgroup sizes each ahead-of-time family runs besides its default
-THREADS = {"fp8": (64, 128, 256), "axpy": (64, 128, 256), "axpy16": (64, 128, 256), "convert": (64, 128, 256)}
+THREADS = {"fp8": (64, 128, 256), "int4": (64, 128, 256), "axpy": (64, 128, 256), "axpy16": (64, 128, 256),
+           "convert": (64, 128, 256)}
 
 
 @pytest.fixture(scope="module", autouse=True)
