@@ -15,6 +15,7 @@
 #define MFH_BACKEND_H
 
 #include "mfh.h"
+#include "mfh_graph.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -151,6 +152,22 @@ int mfh_tensor_release(mfh_tensor* tensor);
  * owners' Download, Sync, Close and shutdown wait for it.  Asynchronous;
  * Sync or Download observes the result. */
 int mfh_axpy_onto_resident(mfh_backend* backend, mfh_tensor* y, const mfh_tensor* x, float alpha);
+
+/* runtime.Backend.CallGraph (runtime/executor.go:22-27, GraphCallRequest and
+ * GraphCallResult at :52-72) over resident tensors: binds inputs[k] to graph
+ * input input_names[k], allocates for each output_keys[j] a flat tensor of
+ * this backend with the dtype and length the call gives that key
+ * (mfh_graph_output_shape), and queues mfh_graph_call on the backend stream.
+ * Inputs may be held by other backends and may still be pending: the call
+ * waits for work queued on them, and their owners' Download, Sync, Close and
+ * shutdown wait for the call.  Returns once the call is queued, with every
+ * output MFH_STATE_PENDING until it has run; Sync or Download observes the
+ * results.  On error no output is returned (outputs[j] == NULL) and nothing
+ * stays allocated.  The graph must not be called from two threads at once
+ * (mfh_graph_call). */
+int mfh_backend_graph_call(mfh_backend* backend, mfh_graph* graph, const char* const* input_names,
+                           const mfh_tensor* const* inputs, int32_t n_inputs, const char* const* output_keys,
+                           int32_t n_outputs, mfh_tensor** outputs);
 
 #ifdef __cplusplus
 }

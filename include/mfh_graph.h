@@ -177,6 +177,17 @@ typedef struct {
 int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
                    int32_t n_outputs, void* stream);
 
+/* The dtype and element count that mfh_graph_call with these inputs gives
+ * output `key` (a key of Graph.Outputs), so that a caller can allocate the
+ * outputs before the call.  Only the inputs' names, dtypes and counts are
+ * read (data may be NULL); nothing is compiled, allocated or queued, and no
+ * device is needed.  The same errors as mfh_graph_call for the same
+ * bindings.  No counterpart in the reference, whose CallGraph returns
+ * outputs it allocates itself (runtime/executor.go:70-72); the backend-level
+ * call, mfh_backend_graph_call (mfh_backend.h), uses it to do the same. */
+int mfh_graph_output_shape(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const char* key,
+                           uint8_t* dtype, int64_t* count);
+
 /* Bytes of the graph's device workspace (0 before the first call). */
 int64_t mfh_graph_workspace_bytes(const mfh_graph* graph);
 

@@ -62,6 +62,8 @@ def _L():
             "mfh_tensor_close": (c.c_int, [vp]),
             "mfh_tensor_release": (c.c_int, [vp]),
             "mfh_axpy_onto_resident": (c.c_int, [vp, vp, vp, c.c_float]),
+            "mfh_backend_graph_call": (c.c_int, [vp, vp, c.POINTER(c.c_char_p), c.POINTER(vp), i32,
+                                                 c.POINTER(c.c_char_p), i32, c.POINTER(vp)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -227,6 +229,20 @@ class Backend:
     def axpy_onto_resident(self, y: Tensor, x: Tensor, alpha: float) -> Tensor:
         check(_L().mfh_axpy_onto_resident(self._h, y._h, x._h, alpha))
         return y
+
+    def graph_call(self, graph, inputs: dict, output_keys) -> dict:
+        """runtime.Backend.CallGraph over resident tensors: `inputs` maps
+        graph input names to Tensors; returns {key: Tensor} with one new flat
+        tensor of this backend per output key, pending until the call has
+        run."""
+        names = list(inputs)
+        keys = list(output_keys)
+        c_names = (ctypes.c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+        c_ins = (ctypes.c_void_p * max(1, len(names)))(*[inputs[n]._h for n in names])
+        c_keys = (ctypes.c_char_p * max(1, len(keys)))(*[k.encode() for k in keys])
+        c_outs = (ctypes.c_void_p * max(1, len(keys)))()
+        check(_L().mfh_backend_graph_call(self._h, graph._h, c_names, c_ins, len(names), c_keys, len(keys), c_outs))
+        return {k: Tensor(self, c_outs[j]) for j, k in enumerate(keys)}
 
     def close(self) -> None:
         check(_L().mfh_backend_close(self._h))

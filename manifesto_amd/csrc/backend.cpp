@@ -668,4 +668,86 @@ int mfh_axpy_onto_resident(mfh_backend* backend, mfh_tensor* y, const mfh_tensor
     return MFH_OK;
 }
 
+int mfh_backend_graph_call(mfh_backend* backend, mfh_graph* graph, const char* const* input_names,
+                           const mfh_tensor* const* inputs, int32_t n_inputs, const char* const* output_keys,
+                           int32_t n_outputs, mfh_tensor** outputs)
+{
+    if (n_outputs < 0 || (n_outputs > 0 && (!outputs || !output_keys)) || n_inputs < 0 ||
+        (n_inputs > 0 && (!inputs || !input_names)))
+        return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: bad input or output list");
+    for (int32_t j = 0; j < n_outputs; j++) outputs[j] = nullptr;
+    if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: graph is required");
+    const Device* dev;
+    MFH_TRY(backend_ok(backend, &dev));
+    std::vector<BackendState*> states{backend->state.get()};
+    for (int32_t k = 0; k < n_inputs; k++) {
+        MFH_TRY(tensor_ok(inputs[k]));
+        states.push_back(inputs[k]->backend.get());
+    }
+    // Inputs may belong to other backends: their owners' state changes
+    // (close, download, shutdown) are held off while the call is queued.
+    StateLocks locks(states);
+    BackendState& s = *backend->state;
+    if (s.closed) return fail(MFH_ERR_CLOSED, "tensor: backend closed");
+    std::vector<mfh_value> ins((size_t)n_inputs);
+    for (int32_t k = 0; k < n_inputs; k++) {
+        MFH_TRY(tensor_ok(inputs[k]));
+        const mfh_tensor& t = *inputs[k];
+        ins[k] = mfh_value{input_names[k], mfh_tensor_dispatch_pointer(&t), t.dtype, {0}, t.elements};
+    }
+    // One flat tensor per output key, of the dtype and length the call gives it.
+    std::vector<std::unique_ptr<mfh_tensor>> made;
+    std::vector<mfh_value> outs((size_t)n_outputs);
+    auto undo = [&](int rc) {
+        (void)hipStreamSynchronize(s.stream);
+        for (auto& t : made) {
+            Storage& st = *t->storage;
+            if (st.done) (void)hipEventDestroy(st.done);
+            if (st.ptr) (void)hipFree(st.ptr);
+            st.done = nullptr;
+            st.ptr = nullptr;
+        }
+        return rc;
+    };
+    for (int32_t j = 0; j < n_outputs; j++) {
+        uint8_t dt = kInvalid;
+        int64_t n = 0;
+        int rc = mfh_graph_output_shape(graph, ins.data(), n_inputs, output_keys[j], &dt, &n);
+        if (rc != MFH_OK) return undo(rc);
+        auto t = std::make_unique<mfh_tensor>();
+        t->backend = backend->state;
+        t->storage = std::make_shared<Storage>();
+        t->dims = {n};
+        t->elements = n;
+        t->dtype = dt;
+        t->storage->bytes = (size_t)n * dtype_size(dt);
+        made.push_back(std::move(t));
+        Storage& st = *made.back()->storage;
+        if (st.bytes && (rc = check_hip(hipMalloc(&st.ptr, st.bytes), "hipMalloc")) != MFH_OK) return undo(rc);
+        outs[j] = mfh_value{output_keys[j], st.ptr, dt, {0}, n};
+    }
+    // Order after work still queued on the inputs (uploads, axpys, earlier
+    // graph calls), on whichever stream it runs.
+    for (int32_t k = 0; k < n_inputs; k++) {
+        Storage& st = *inputs[k]->storage;
+        if (st.pending && st.done) {
+            int rc = check_hip(hipStreamWaitEvent(s.stream, st.done, 0), "hipStreamWaitEvent");
+            if (rc != MFH_OK) return undo(rc);
+        }
+    }
+    int rc = mfh_graph_call(graph, ins.data(), n_inputs, outs.data(), n_outputs, s.stream);
+    if (rc != MFH_OK) return undo(rc);
+    // Later readers of the outputs, and closes of the inputs through their
+    // own backends, wait for the call.
+    for (int32_t k = 0; k < n_inputs; k++)
+        if ((rc = mark_pending(*inputs[k]->storage, s.stream)) != MFH_OK) return undo(rc);
+    for (auto& t : made)
+        if ((rc = mark_pending(*t->storage, s.stream)) != MFH_OK) return undo(rc);
+    for (int32_t j = 0; j < n_outputs; j++) {
+        s.owned.insert(made[j]->storage);
+        outputs[j] = made[j].release();
+    }
+    return MFH_OK;
+}
+
 }  // extern "C"

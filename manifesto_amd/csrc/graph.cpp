@@ -638,7 +638,9 @@ int operand_mode(int64_t c, int64_t n, mfh_operand* op)
 // Binds inputs and outputs and lowers every node to a launch.  With
 // `shapes_only` the values' data pointers are not needed (planning); without
 // `may_compile` an unfused node whose one-node kernel was never generated is
-// an error instead of a compile.
+// an error instead of a compile, except with `shapes_only`, where such a node
+// keeps a null kernel and takes the dtype its kernel would produce (a shape
+// query, which needs no device).
 int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
             bool shapes_only, Prepared* P, bool may_compile = true)
 {
@@ -706,6 +708,10 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
             if (kernel->inputs.size() != node.inputs.size())
                 return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: fused node \"%s\" has %d inputs, its kernel %d",
                             node.id.c_str(), (int)node.inputs.size(), (int)kernel->inputs.size());
+        } else if (int32_t type = elementwise_type(node.op); type && !node.solo && shapes_only && !may_compile) {
+            if ((int)node.inputs.size() != node_arity(type))
+                return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" (%s) has %d inputs, want %d",
+                            node.id.c_str(), node.op.c_str(), (int)node.inputs.size(), node_arity(type));
         } else if (int32_t type = elementwise_type(node.op)) {
             if (!node.solo && !may_compile)
                 return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" has no kernel yet (make one "
@@ -747,7 +753,8 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
                 return fail(MFH_ERR_SHAPE_MISMATCH, "graph call: node \"%s\": operand \"%s\" has %lld elements, "
                             "the node %lld", node.id.c_str(), node.inputs[k].c_str(), (long long)s.count,
                             (long long)st.count);
-            if (k < kernel->declared.size() && kernel->declared[k] != kInvalid && kernel->declared[k] != s.dtype)
+            if (kernel && k < kernel->declared.size() && kernel->declared[k] != kInvalid &&
+                kernel->declared[k] != s.dtype)
                 return fail(MFH_ERR_DTYPE_UNSUPPORTED, "graph call: node \"%s\": operand \"%s\" is %s, declared %s",
                             node.id.c_str(), node.inputs[k].c_str(), dtype_name(s.dtype),
                             dtype_name(kernel->declared[k]));
@@ -755,7 +762,8 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
             s.readers.push_back(t);
         }
         Slot out;
-        out.dtype = kernel->out_dtype;
+        if (kernel) out.dtype = kernel->out_dtype;
+        else MFH_TRY(output_dtype(node.output_type, g.execution_dtype, &out.dtype));
         out.count = st.count;
         out.kind = Slot::kArena;
         out.producer = t;
@@ -1111,6 +1119,27 @@ int graph_call_noalloc(Graph& g, const mfh_value* inputs, int32_t n_inputs, cons
 // compiler.PlanGraph (compiler/plan.go:242-290): buildPlanningTopology
 // (:29-90), PlanWorkspace, attachGraphIOPorts (:179-228), ScheduleStreams.
 // The graph is taken in its own order (graph calls need it topological).
+// The dtype and element count a call with these inputs gives output `key`,
+// by prepare()'s rules, from the inputs' names, dtypes and counts alone.
+int output_shape(Graph& g, const mfh_value* inputs, int32_t n_inputs, const std::string& key, uint8_t* dtype,
+                 int64_t* count)
+{
+    auto it = std::find_if(g.outputs.begin(), g.outputs.end(), [&](const auto& kv) { return kv.first == key; });
+    if (it == g.outputs.end()) return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: unknown output \"%s\"", key.c_str());
+    Prepared P;
+    MFH_TRY(prepare(g, inputs, n_inputs, nullptr, 0, true, &P, false));
+    int slot = -1;
+    for (size_t i = 0; i < g.nodes.size(); i++)
+        if (g.nodes[i]->id == it->second) slot = P.node_slot[i];
+    for (size_t k = 0; slot < 0 && k < g.inputs.size(); k++)
+        if (g.inputs[k] == it->second) slot = P.input_slot[k];
+    if (slot < 0)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: output value \"%s\" is never defined", it->second.c_str());
+    *dtype = P.slots[slot].dtype;
+    *count = P.slots[slot].count;
+    return MFH_OK;
+}
+
 int plan_graph(Graph& g, const mfh_value* inputs, int32_t n_inputs, int64_t align, int32_t max_streams, Topology* t)
 {
     Prepared P;
@@ -1500,6 +1529,14 @@ int mfh_graph_call(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, 
 }
 
 int64_t mfh_graph_workspace_bytes(const mfh_graph* graph) { return graph ? graph->ws_bytes : -1; }
+
+int mfh_graph_output_shape(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const char* key,
+                           uint8_t* dtype, int64_t* count)
+{
+    if (!graph || !key || !dtype || !count)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_output_shape: graph, key, dtype and count are required");
+    return output_shape(*graph, inputs, n_inputs, key, dtype, count);
+}
 
 int mfh_graph_call_noalloc(mfh_graph* graph, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
                            int32_t n_outputs, void* stream)

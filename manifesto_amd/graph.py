@@ -99,6 +99,7 @@ def _L():
             "mfh_graph_kernel": (c.c_int, [vp, i32, i32, c.POINTER(vp)]),
             "mfh_graph_call": (c.c_int, [vp, c.POINTER(Value), i32, c.POINTER(Value), i32, vp]),
             "mfh_graph_call_noalloc": (c.c_int, [vp, c.POINTER(Value), i32, c.POINTER(Value), i32, vp]),
+            "mfh_graph_output_shape": (c.c_int, [vp, c.POINTER(Value), i32, cp, c.POINTER(u8), c.POINTER(i64)]),
             "mfh_graph_workspace_bytes": (i64, [vp]),
             "mfh_graph_set_replay": (c.c_int, [vp, i32]),
             "mfh_graph_replayed_calls": (i64, [vp]),
@@ -306,6 +307,15 @@ class Graph:
         to torch tensors."""
         ins, outs = self._values(inputs), self._values(outputs)
         check(_L().mfh_graph_call(self._h, ins, len(inputs), outs, len(outputs), stream))
+
+    def output_shape(self, inputs: dict, key: str) -> tuple:
+        """(dtype, count) that a call with `inputs` gives output `key`; only
+        the inputs' dtypes and counts are read, (ptr, dtype, count) triples
+        with ptr None included."""
+        ins = self._values(inputs)
+        dt, n = ctypes.c_uint8(), ctypes.c_int64()
+        check(_L().mfh_graph_output_shape(self._h, ins, len(inputs), key.encode(), ctypes.byref(dt), ctypes.byref(n)))
+        return dt.value, n.value
 
     def call_noalloc(self, inputs: dict, outputs: dict, stream: int = 0) -> None:
         """mfh_graph_call_noalloc: the same call with its constants and

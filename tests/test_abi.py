@@ -240,3 +240,39 @@ def test_launch_threads_set_keep_restore_and_limits():
     assert M.get_launch_threads("fp8") == 128
     with pytest.raises(M.MFHError, match="unknown kernel family"):
         M.set_launch_threads("nope", 64)
+
+
+HEADERS = sorted(h for h in os.listdir(INCLUDE) if h.endswith(".h"))
+
+
+@pytest.mark.parametrize("std, compiler", [("c99", "gcc"), ("c11", "gcc"), ("c++17", "g++")])
+def test_headers_compile_as_strict_c_and_cxx(tmp_path, std, compiler):
+    # each header alone (twice, for its include guard), then all together in
+    # both orders, as a cgo or C host would include them
+    orders = [[h, h] for h in HEADERS] + [HEADERS, HEADERS[::-1]]
+    for k, order in enumerate(orders):
+        src = tmp_path / f"h{k}.{'cc' if compiler == 'g++' else 'c'}"
+        src.write_text("".join(f'#include "{h}"\n' for h in order) + "int main(void) { return 0; }\n")
+        r = subprocess.run([compiler, f"-std={std}", "-pedantic-errors", "-Wall", "-Wextra", "-Werror",
+                            "-fsyntax-only", "-I", INCLUDE, str(src)], capture_output=True, text=True)
+        assert r.returncode == 0, (order, r.stderr)
+
+
+def test_c99_program_links_every_declared_function(tmp_path):
+    # a C99 caller that takes the address of every function the headers
+    # declare links against the library and loads it
+    names = declared_symbols()
+    src = tmp_path / "link.c"
+    src.write_text("".join(f'#include "{h}"\n' for h in HEADERS) + "#include <stdio.h>\n"
+                   "typedef void (*fn)(void);\n"
+                   "int main(void)\n{\n    int n = 0;\n"
+                   + "".join(f"    n += (fn)&{s} != 0;\n" for s in names)
+                   + '    printf("%d\\n", n);\n    return 0;\n}\n')
+    exe = tmp_path / "link"
+    lib_dir = os.path.dirname(M.LIB_PATH)
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-Wno-pedantic", "-I", INCLUDE, str(src), "-o", str(exe),
+                        "-L", lib_dir, "-l:" + os.path.basename(M.LIB_PATH), f"-Wl,-rpath,{lib_dir}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0 and out.stdout.strip() == str(len(names)), (out.stdout, out.stderr)

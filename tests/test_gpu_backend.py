@@ -230,3 +230,78 @@ def test_backend_close_invalidates_tensors():
     assert code(e) == -7
     t.release()
     b.release()
+
+
+def _affine_graph():
+    # a = x + bias (also an output, so it stays its own node); y = a * 1.1 + residual, fused
+    from manifesto_amd.graph import Graph, GraphNode
+    f16 = O.FLOAT16
+    return Graph(inputs=["x", "bias", "residual"], outputs={"out": "y", "pre": "a"}, execution_dtype=f16, nodes=[
+        GraphNode("s", "math.constant", [], attributes={"value": 1.1}),
+        GraphNode("a", "math.add", ["x", "bias"], input_types=[f16, f16], output_type=f16),
+        GraphNode("m", "math.mul", ["a", "s"], input_types=[f16, O.FLOAT32], output_type=f16),
+        GraphNode("y", "math.add", ["m", "residual"], input_types=[f16, f16], output_type=f16),
+    ])
+
+
+def _affine_want(xs, bs, rs):
+    f = lambda h: O.bytes_to_f32(O.FLOAT16, h.view(np.uint8))  # noqa: E731
+    rows = xs.size // bs.size
+    a = O.f32_to_f16(f(xs) + np.tile(f(bs), rows))
+    y = O.f32_to_f16(f(a) * np.float32(1.1) + f(rs))
+    return a, y
+
+
+def test_graph_call_over_resident_tensors():
+    # runtime.Backend.CallGraph (runtime/executor.go:22-27): inputs are tensors
+    # of two backends, some still pending; outputs are allocated by the call.
+    from manifesto_amd import graph as G
+    a, b = Backend(0), Backend(0)
+    try:
+        graph = _affine_graph()
+        G.run(graph)
+        assert [n.op for n in graph.nodes] == ["math.constant", "math.add", G.FUSE_OP]
+        G.attach_kernels(graph)
+        rng = np.random.default_rng(3)
+        n, period = 4096 * 1031, 4096
+        xs = O.f32_to_f16(rng.standard_normal(n).astype(np.float32))
+        bs = O.f32_to_f16((rng.standard_normal(period) * 0.02).astype(np.float32))
+        rs = O.f32_to_f16(rng.standard_normal(n).astype(np.float32))
+        tx = a.upload_async([n], O.FLOAT16, xs)
+        tb = a.upload([period], O.FLOAT16, bs)
+        tr = b.upload_async([n], O.FLOAT16, rs)  # another backend's tensor
+        outs = a.graph_call(graph, {"x": tx, "bias": tb, "residual": tr}, ["out", "pre", "out"])
+        assert sorted(outs) == ["out", "pre"]
+        out, pre = outs["out"], outs["pre"]
+        assert out.dtype() == O.FLOAT16 and out.len() == n and out.shape() == [n]
+        assert out.state() in (STATE_PENDING, STATE_READY)
+        want_a, want_y = _affine_want(xs, bs, rs)
+        out.sync()
+        assert out.state() == STATE_READY
+        np.testing.assert_array_equal(np.frombuffer(a.download(out)[1], np.uint16), want_y)
+        np.testing.assert_array_equal(np.frombuffer(a.download(pre)[1], np.uint16), want_a)
+        log(f"graph call over resident tensors: {n} elements bit-exact, inputs from two backends")
+        # a second call reads the first one's output (ordered on the stream)
+        outs2 = b.graph_call(graph, {"x": out, "bias": tb, "residual": tr}, ["out"])
+        _, want2 = _affine_want(want_y, bs, rs)
+        np.testing.assert_array_equal(np.frombuffer(b.download(outs2["out"])[1], np.uint16), want2)
+        # errors come back before anything is queued, with no outputs
+        with pytest.raises(M.MFHError) as e:
+            a.graph_call(graph, {"x": tx, "bias": tx.slice(0, 4095), "residual": tr}, ["out"])
+        assert code(e) == -3 and "operand \"bias\" has 4095 elements" in str(e.value)
+        with pytest.raises(M.MFHError, match="unknown output \"nope\""):
+            a.graph_call(graph, {"x": tx, "bias": tb, "residual": tr}, ["nope"])
+        for t in (out, pre, outs2["out"]):
+            t.release()
+        tr.close()
+        b.close()
+        with pytest.raises(M.MFHError) as e:
+            a.graph_call(graph, {"x": tx, "bias": tb, "residual": tr}, ["out"])
+        assert code(e) == ERR_TENSOR_CLOSED
+        a.close()
+        with pytest.raises(M.MFHError) as e:
+            a.graph_call(graph, {"x": tx, "bias": tb}, ["out"])
+        assert code(e) == -7
+    finally:
+        b.release()
+        a.release()

@@ -511,3 +511,51 @@ def test_graph_call_requires_init():
     with pytest.raises(M.MFHError) as e:
         graph.call({"x": (0, M.FLOAT32, 0)}, {})
     assert e.value.code == -6
+
+
+# ---- mfh_graph_output_shape: outputs sized before a call, with no device -----------
+
+def _shape_inputs(n=16384, period=4096, dt=M.FLOAT16):
+    return {"x": (None, dt, n), "bias": (None, dt, period), "residual": (None, dt, n)}
+
+
+def test_output_shape_of_unfused_and_fused_graph():
+    graph = gelu_chain_graph()
+    assert graph.output_shape(_shape_inputs(), "out") == (M.FLOAT16, 16384)
+    G.run(graph)
+    G.attach_kernels(graph)
+    assert graph.output_shape(_shape_inputs(), "out") == (M.FLOAT16, 16384)
+    # a repeating row and a scalar broadcast to the node's length
+    assert graph.output_shape(_shape_inputs(n=4096 * 3), "out") == (M.FLOAT16, 4096 * 3)
+
+
+def test_output_shape_dtype_fallbacks_and_input_outputs():
+    def g(exec_dt, out_t):
+        return Graph(inputs=["a", "b"], outputs={"y": "s", "a_again": "a", "c": "k"}, execution_dtype=exec_dt,
+                     nodes=[GraphNode("k", "math.constant", [], attributes={"value": 2.0}),
+                            GraphNode("s", "math.add", ["a", "b"], output_type=out_t)])
+    ins = {"a": (None, M.BFLOAT16, 10), "b": (None, M.BFLOAT16, 1)}
+    # OutputType, else ExecutionDType, else Float32 (the graph call's rule)
+    assert g(M.FLOAT16, M.BFLOAT16).output_shape(ins, "y") == (M.BFLOAT16, 10)
+    assert g(M.FLOAT16, 0).output_shape(ins, "y") == (M.FLOAT16, 10)
+    assert g(0, 0).output_shape(ins, "y") == (M.FLOAT32, 10)
+    assert g(0, 0).output_shape(ins, "a_again") == (M.BFLOAT16, 10)
+    assert g(0, 0).output_shape(ins, "c") == (M.FLOAT32, 1)
+
+
+def test_output_shape_errors_match_the_call():
+    graph = gelu_chain_graph()
+    with pytest.raises(M.MFHError) as e:
+        graph.output_shape(_shape_inputs(period=4095), "out")
+    assert e.value.code == -3 and "operand \"bias\" has 4095 elements" in str(e.value)  # SHAPE_MISMATCH
+    with pytest.raises(M.MFHError) as e:
+        graph.output_shape(_shape_inputs(), "nope")
+    assert "unknown output \"nope\"" in str(e.value)
+    ins = _shape_inputs()
+    del ins["residual"]
+    with pytest.raises(M.MFHError) as e:
+        graph.output_shape(ins, "out")
+    assert "neither a bound input nor an earlier node" in str(e.value)
+    with pytest.raises(M.MFHError) as e:
+        graph.output_shape({**_shape_inputs(), "x": (None, M.F8E4M3, 16384)}, "out")
+    assert e.value.code == -2  # MFH_ERR_DTYPE_UNSUPPORTED
