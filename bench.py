@@ -15,12 +15,15 @@ captured HIP graph so the clock sees kernel time, not Python launch overhead;
 the W warm-up steps replay the same graph first.  After timing, a sample of
 the timed outputs is checked against the oracle ("sample_check").  The other
 BASELINE configs (axpy, SwiGLU, the f16 gelu chain, Int4) are measured the
-same way and listed under "configs".  The CPU baseline is the oracle (a C
+same way and listed under "configs".  Each config also carries
+"torch_same_mix": PyTorch-ROCm's own elementwise kernel moving the same bytes
+in the same read:write mix, rotated and timed the same way, as the stock
+stack's rate on that stream.  The CPU baseline is the oracle (a C
 restatement of the Go loops, -O2 -ffp-contract=off) timed on this host,
 single-threaded as the Go loops run; "cpu_baseline_all_cores" splits the same
 sample over the host's threads.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only N] [--sweep] [--profile REPS]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-torch] [--only N] [--sweep] [--profile REPS]
 """
 from __future__ import annotations
 
@@ -325,6 +328,73 @@ class Int4(Workload):
 WORKLOADS = [Axpy, Fp8, SwiGLU, GeluChain, Int4]
 
 
+class SameMix(Workload):
+    """PyTorch-ROCm's own elementwise kernel moving the bytes of a config's
+    step in the same read:write mix, rotated and timed the same way: the rate
+    the stock ROCm stack reaches on that stream, beside the config's kernel.
+    axpy -> y.add_(x, alpha=0.75) (the same op); FP8 -> uint8 to bf16 copy
+    (1 B read, 2 B written per element); SwiGLU -> bf16 mul(gate, up); gelu
+    chain -> f16 add(x, residual) (the 8 KiB bias row aside); Int4 -> uint8 to
+    f32 copy of n/2 bytes (0.5 B read, 2 B written per element; the group
+    scales, 1.6% of the bytes, aside)."""
+    OPS = {1: "torch y.add_(x, alpha=0.75), f32", 2: "torch copy_ uint8 -> bf16",
+           3: "torch mul(gate, up, out=), bf16", 4: "torch add(x, residual, out=), f16",
+           5: "torch copy_ uint8 -> f32 (n/2 bytes)"}
+
+    def __init__(self, base, torch, M, O):
+        super().__init__(torch, M, O)
+        self.cfg = base.cfg
+        n = base.n
+        torch_ = torch
+        if base.cfg == 1:
+            shape = [("x", torch_.float32, n), ("y", torch_.float32, n)]
+            self.bytes_per_step, self.read_bytes_per_step = 12 * n, 8 * n
+        elif base.cfg == 2:
+            shape = [("in", torch_.uint8, n), ("out", torch_.bfloat16, n)]
+            self.bytes_per_step, self.read_bytes_per_step = 3 * n, n
+        elif base.cfg in (3, 4):
+            dt = torch_.bfloat16 if base.cfg == 3 else torch_.float16
+            shape = [("a", dt, n), ("b", dt, n), ("out", dt, n)]
+            self.bytes_per_step, self.read_bytes_per_step = 6 * n, 4 * n
+        else:
+            shape = [("in", torch_.uint8, n // 2), ("out", torch_.float32, n // 2)]
+            self.bytes_per_step, self.read_bytes_per_step = n // 2 + 2 * n, n // 2
+        self.shape = shape
+        self.op = self.OPS[base.cfg]
+
+    def make_set(self):
+        t = self.torch
+        g = self.generator()
+        out = []
+        for _, dt, n in self.shape:
+            if dt == t.uint8:
+                out.append(t.randint(0, 256, (n,), dtype=t.uint8, device="cuda", generator=g))
+            else:
+                out.append(t.randn(n, device="cuda", generator=g).to(dt))
+        return out
+
+    def launch(self, st):
+        t = self.torch
+        if self.cfg == 1:
+            st[1].add_(st[0], alpha=0.75)
+        elif self.cfg in (2, 5):
+            st[1].copy_(st[0])
+        elif self.cfg == 3:
+            t.mul(st[0], st[1], out=st[2])
+        else:
+            t.add(st[0], st[1], out=st[2])
+
+
+def time_same_mix(base, torch, M, O, args):
+    w = SameMix(base, torch, M, O)
+    w.setup()
+    ms, _, _ = time_gpu(w, args.steps, args.warmup, use_graph=not args.no_graph)
+    gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
+    del w
+    torch.cuda.empty_cache()
+    return {"op": SameMix.OPS[base.cfg], "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+
+
 def warm_steps(w, args):
     """Untimed launches time_gpu makes before the timed region."""
     if args.no_graph:
@@ -502,6 +572,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-torch", action="store_true", help="skip the torch same-mix stream of each config")
     ap.add_argument("--only", type=int, default=0, help="measure only this BASELINE config")
     ap.add_argument("--sweep", action="store_true",
                     help="each BASELINE kernel at 1/64 to 4x its config's launch size (one JSON line each)")
@@ -542,6 +613,9 @@ def main():
              "steps_timed": n, "warmup_steps_run": warm_steps(w, args), "rotated_sets": len(w.sets),
              "input_bytes_per_rotation": len(w.sets) * w.read_bytes_per_step, "wall_s": round(wall, 4),
              "sample_check": w.check()}
+        if not args.no_torch:  # after the config's own timing, which it leaves as it was
+            r["torch_same_mix"] = time_same_mix(cls, torch, M, O, args)
+            r["vs_torch_same_mix"] = round(gbs / r["torch_same_mix"]["GB_s"], 3)
         if not args.no_cpu:
             r["cpu_baseline"] = time_cpu(w)
             r["speedup_vs_cpu"] = round(gbs / r["cpu_baseline"]["value"], 1)
@@ -566,6 +640,7 @@ def main():
                               "untimed replays of the same graph")},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": load_traffic(), "kernel": head["kernel"]},
+        "torch_same_mix": head.get("torch_same_mix"),
         "cpu_baseline": head.get("cpu_baseline"),
         "cpu_baseline_all_cores": head.get("cpu_baseline_all_cores"),
         "elements_per_s": head["elements_per_s"],
