@@ -23,7 +23,8 @@ restatement of the Go loops, -O2 -ffp-contract=off) timed on this host,
 single-threaded as the Go loops run; "cpu_baseline_all_cores" splits the same
 sample over the host's threads.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-torch] [--only N] [--sweep] [--profile REPS]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-torch] [--only N] [--sets S]
+                [--sweep] [--footprint] [--profile REPS]
 """
 from __future__ import annotations
 
@@ -62,9 +63,13 @@ class Workload:
     def stream(self):
         return self.torch.cuda.current_stream().cuda_stream
 
+    sets_override = 0  # --sets: a fixed rotation, for footprint studies
+
     def rotations(self):
         """Sets per rotation: at least four, a footprint of at least twice the
         Infinity Cache, and at least four caches' worth of distinct inputs."""
+        if self.sets_override:
+            return self.sets_override
         return max(4, -(-2 * MALL_BYTES // self.bytes_per_step), -(-4 * MALL_BYTES // self.read_bytes_per_step))
 
     def setup(self):
@@ -510,11 +515,14 @@ def time_cpu(w, budget_s=3.0, threads=1):
     return out
 
 
-def profile_run(torch, M, O, reps):
-    """Eager launches for rocprofv3: every workload kernel `reps` times, then a
-    plain f32 copy of 64 MiB (mfh_convert f32->f32, the k_convert_vec kernel) whose
-    FETCH_SIZE / WRITE_SIZE calibrate the counters against known bytes."""
+def profile_run(torch, M, O, reps, only=0):
+    """Eager launches for rocprofv3: every workload kernel (or config `only`'s)
+    `reps` times over its rotated sets, then a plain f32 copy of 64 MiB
+    (mfh_convert f32->f32, the k_convert_vec kernel) whose FETCH_SIZE /
+    WRITE_SIZE calibrate the counters against known bytes."""
     for cls in WORKLOADS:
+        if only and cls.cfg != only:
+            continue
         w = cls(torch, M, O)
         w.setup()
         for i in range(reps):
@@ -554,6 +562,31 @@ def sweep_run(torch, M, O, steps, warmup):
             torch.cuda.empty_cache()
 
 
+def footprint_run(torch, M, O, steps, warmup, only=0):
+    """--footprint: each BASELINE kernel over 1 to 32 rotated buffer sets,
+    timed as the bench times a step.  One JSON line per kernel and rotation:
+    the rate against the distinct input bytes per cycle shows where the
+    Infinity Cache (256 MB) stops serving the inputs."""
+    for cls in WORKLOADS:
+        if only and cls.cfg != only:
+            continue
+        for sets in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32):
+            if sets > 1 and (sets - 1) * cls.read_bytes_per_step > 8 * MALL_BYTES:
+                break
+            sized = type(cls.__name__, (cls,), {"sets_override": sets})
+            w = sized(torch, M, O)
+            w.setup()
+            ms, _, _ = time_gpu(w, steps, warmup)
+            gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
+            print(json.dumps({"config": cls.cfg, "kernel": cls.kernel, "sets": sets,
+                              "input_MB_per_cycle": round(sets * w.read_bytes_per_step / 1e6, 1),
+                              "footprint_MB": round(sets * w.bytes_per_step / 1e6, 1),
+                              "us_per_step": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
+                              "frac_of_peak": round(gbs / PEAK_GBS, 4)}), flush=True)
+            del w
+            torch.cuda.empty_cache()
+
+
 def load_traffic():
     """HBM bytes per dispatch of the headline kernel from the committed
     rocprofv3 PMC summary (profiles/pmc_traffic.json), or None."""
@@ -578,6 +611,10 @@ def main():
                     help="each BASELINE kernel at 1/64 to 4x its config's launch size (one JSON line each)")
     ap.add_argument("--profile", type=int, default=0, metavar="REPS",
                     help="eager launches of every kernel REPS times (for rocprofv3), no timing")
+    ap.add_argument("--sets", type=int, default=0,
+                    help="rotate exactly this many buffer sets (default: >= 1 GiB of distinct inputs per cycle)")
+    ap.add_argument("--footprint", action="store_true",
+                    help="each BASELINE kernel over 1 to 32 rotated sets (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -592,8 +629,13 @@ def main():
     M.init(0)
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} ({props.multi_processor_count} CUs)")
+    if args.sets:
+        Workload.sets_override = args.sets
     if args.profile:
-        profile_run(torch, M, O, args.profile)
+        profile_run(torch, M, O, args.profile, args.only)
+        return
+    if args.footprint:
+        footprint_run(torch, M, O, args.steps, args.warmup, args.only)
         return
     if args.sweep:
         sweep_run(torch, M, O, args.steps, args.warmup)

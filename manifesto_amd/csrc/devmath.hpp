@@ -39,6 +39,7 @@
 #ifdef MFH_HOST_MATH
 #include <cmath>
 #define MFH_MATH inline
+#define MFH_RARE inline
 #define mfh_fmaf(a, b, c) std::fma((float)(a), (float)(b), (float)(c))
 #define mfh_fma(a, b, c) std::fma((double)(a), (double)(b), (double)(c))
 #define mfh_rintf(x) std::nearbyint((float)(x))
@@ -66,6 +67,11 @@ extern "C" __device__ double __ocml_tanh_f64(double);
 extern "C" __device__ double __ocml_exp_f64(double);
 extern "C" __device__ double __ocml_log_f64(double);
 #define MFH_MATH __device__ inline __attribute__((always_inline))
+// The reference forms behind the fast ones' rare branches are real calls: the
+// constants of the f64 tanh / exp they inline were otherwise hoisted into
+// every thread's prologue (about 3 VALU instructions per element of a
+// one-item-per-thread launch) although no wave takes the branch.
+#define MFH_RARE __device__ __attribute__((noinline))
 #define mfh_fmaf(a, b, c) __builtin_fmaf((a), (b), (c))
 #define mfh_fma(a, b, c) __builtin_fma((a), (b), (c))
 #define mfh_rintf(x) __builtin_rintf(x)
@@ -242,14 +248,15 @@ MFH_MATH float mfh_gelu_fast(float v, bool& rare)
     return mfh_div_one_plus(v, mfh_ldexpf(p, mfh_low_int(tk)));
 }
 
-#define MFH_FAST_OR_REF(name)               \
-    MFH_MATH float mfh_##name(float v)       \
-    {                                       \
-        bool rare = false;                  \
-        float s = mfh_##name##_fast(v, rare); \
-        MFH_KEEP(s);                        \
-        if (rare) s = mfh_##name##_ref(v);  \
-        return s;                           \
+#define MFH_FAST_OR_REF(name)                                           \
+    MFH_RARE float mfh_##name##_rare(float v) { return mfh_##name##_ref(v); } \
+    MFH_MATH float mfh_##name(float v)                                   \
+    {                                                                   \
+        bool rare = false;                                              \
+        float s = mfh_##name##_fast(v, rare);                           \
+        MFH_KEEP(s);                                                    \
+        if (rare) s = mfh_##name##_rare(v);                             \
+        return s;                                                       \
     }
 MFH_FAST_OR_REF(sigmoid)
 MFH_FAST_OR_REF(silu)
