@@ -16,15 +16,16 @@ the W warm-up steps replay the same graph first.  After timing, a sample of
 the timed outputs is checked against the oracle ("sample_check").  The other
 BASELINE configs (axpy, SwiGLU, the f16 gelu chain, Int4) are measured the
 same way and listed under "configs".  Each config also carries
-"torch_same_mix": PyTorch-ROCm's own elementwise kernel moving the same bytes
-in the same read:write mix, rotated and timed the same way, as the stock
-stack's rate on that stream.  The CPU baseline is the oracle (a C
+"cast_same_mix" and "torch_same_mix": the library's own dtype cast and
+PyTorch-ROCm's own elementwise kernel moving the same bytes in the same
+read:write mix, rotated and timed the same way: that access pattern's
+practical ceiling on the box, and the stock stack's rate on it.  The CPU baseline is the oracle (a C
 restatement of the Go loops, -O2 -ffp-contract=off) timed on this host,
 single-threaded as the Go loops run; "cpu_baseline_all_cores" splits the same
 sample over the host's threads.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-torch] [--only N] [--sets S]
-                [--sweep] [--footprint] [--profile REPS]
+                [--sweep] [--footprint] [--transient] [--profile REPS]
 """
 from __future__ import annotations
 
@@ -366,6 +367,7 @@ class SameMix(Workload):
             self.bytes_per_step, self.read_bytes_per_step = n // 2 + 2 * n, n // 2
         self.shape = shape
         self.op = self.OPS[base.cfg]
+        self.n = shape[0][2]
 
     def make_set(self):
         t = self.torch
@@ -390,14 +392,53 @@ class SameMix(Workload):
             t.add(st[0], st[1], out=st[2])
 
 
-def time_same_mix(base, torch, M, O, args):
-    w = SameMix(base, torch, M, O)
+class CastMix(Workload):
+    """The library's own dtype cast (mfh_convert, one-shot, non-temporal
+    stores) moving exactly the bytes of a config's step in the same
+    read:write mix, with next to no arithmetic: what this access pattern
+    reaches on the box, the config kernel's practical ceiling.  axpy (8 : 4
+    bytes per element) and the fused chains (4 : 2) -> f32 to bf16 over 2n and
+    n elements; FP8 (1 : 2) -> bf16 to f32 over n/2; Int4 (0.5 : 2) -> int8 to
+    f32 over n/2.  The casts read one stream where axpy and the chains read
+    two."""
+    CASTS = {1: ("f32", "bf16", 2.0), 2: ("bf16", "f32", 0.5), 3: ("f32", "bf16", 1.0), 4: ("f32", "bf16", 1.0),
+             5: ("i8", "f32", 0.5)}
+
+    def __init__(self, base, torch, M, O):
+        super().__init__(torch, M, O)
+        self.cfg = base.cfg
+        src, dst, f = self.CASTS[base.cfg]
+        self.n = int(base.n * f)
+        dts = {"f32": (torch.float32, M.FLOAT32, 4), "bf16": (torch.bfloat16, M.BFLOAT16, 2),
+               "i8": (torch.int8, M.INT8, 1)}
+        self.src, self.dst = dts[src], dts[dst]
+        self.read_bytes_per_step = self.n * self.src[2]
+        self.bytes_per_step = self.n * (self.src[2] + self.dst[2])
+        self.op = f"mfh_convert {src} -> {dst}, {self.n} elements"
+
+    def make_set(self):
+        t = self.torch
+        g = self.generator()
+        if self.src[0] == t.int8:
+            x = t.randint(-128, 128, (self.n,), dtype=t.int8, device="cuda", generator=g)
+        else:
+            x = t.randn(self.n, device="cuda", generator=g).to(self.src[0])
+        return x, t.empty(self.n, dtype=self.dst[0], device="cuda")
+
+    def launch(self, st):
+        x, y = st
+        self.M.convert(y.data_ptr(), self.dst[1], x.data_ptr(), self.src[1], self.n, self.stream)
+
+
+def time_same_mix(kind, base, torch, M, O, args):
+    w = kind(base, torch, M, O)
     w.setup()
     ms, _, _ = time_gpu(w, args.steps, args.warmup, use_graph=not args.no_graph)
     gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
+    op = w.op
     del w
     torch.cuda.empty_cache()
-    return {"op": SameMix.OPS[base.cfg], "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+    return {"op": op, "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}
 
 
 def warm_steps(w, args):
@@ -562,6 +603,45 @@ def sweep_run(torch, M, O, steps, warmup):
             torch.cuda.empty_cache()
 
 
+class GeluChainAs(GeluChain):
+    """The gelu chain's operands and output with another activation in the
+    gelu node's place (silu, or none): the same bytes and access pattern, a
+    different compute load."""
+    act = None
+
+    def setup(self):
+        O, M = self.O, self.M
+        inner = (O.N_MUL, (O.N_ADD, ("in", 0), ("in", 1)), ("in", 2))
+        self.nodes = O.flatten((O.N_ADD, (self.act, inner) if self.act else inner, ("in", 3)))
+        ops = [(M.FLOAT16, M.OPERAND_FULL, 0), (M.FLOAT16, M.OPERAND_PERIODIC, 4096),
+               (M.FLOAT32, M.OPERAND_SCALAR, 0), (M.FLOAT16, M.OPERAND_FULL, 0)]
+        self.kernel = "fused_" + self.ident
+        self.k = M.FusedKernel(self.nodes, ops, M.FLOAT16, self.ident)
+        Workload.setup(self)
+
+
+def transient_run(torch, M, O, steps, warmup):
+    """--transient: every BASELINE kernel, then the gelu chain with silu and
+    with no activation in the gelu node's place, each from an idle GPU (4 s
+    asleep) through the bench's warm-up and timed replays.  Run under
+    rocprofv3 --kernel-trace, the dispatch durations show how each kernel
+    rides the clock's dip after idle."""
+    variants = list(WORKLOADS) + [
+        type("GeluChainSilu", (GeluChainAs,), {"act": O.N_SILU, "ident": "gelu_chain_silu"}),
+        type("GeluChainPlain", (GeluChainAs,), {"act": None, "ident": "gelu_chain_plain"})]
+    for cls in variants:
+        w = cls(torch, M, O)
+        w.setup()
+        torch.cuda.synchronize()
+        time.sleep(4.0)
+        ms, _, _ = time_gpu(w, steps, warmup)
+        gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
+        print(json.dumps({"workload": cls.__name__, "kernel": w.kernel, "us_per_step": round(ms * 1e3, 2),
+                          "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}), flush=True)
+        del w
+        torch.cuda.empty_cache()
+
+
 def footprint_run(torch, M, O, steps, warmup, only=0):
     """--footprint: each BASELINE kernel over 1 to 32 rotated buffer sets,
     timed as the bench times a step.  One JSON line per kernel and rotation:
@@ -605,7 +685,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--no-torch", action="store_true", help="skip the torch same-mix stream of each config")
+    ap.add_argument("--no-torch", action="store_true",
+                    help="skip the same-mix streams (library cast, torch) of each config")
     ap.add_argument("--only", type=int, default=0, help="measure only this BASELINE config")
     ap.add_argument("--sweep", action="store_true",
                     help="each BASELINE kernel at 1/64 to 4x its config's launch size (one JSON line each)")
@@ -613,6 +694,8 @@ def main():
                     help="eager launches of every kernel REPS times (for rocprofv3), no timing")
     ap.add_argument("--sets", type=int, default=0,
                     help="rotate exactly this many buffer sets (default: >= 1 GiB of distinct inputs per cycle)")
+    ap.add_argument("--transient", action="store_true",
+                    help="each kernel (and two variants of the gelu chain) from an idle GPU, for a kernel trace")
     ap.add_argument("--footprint", action="store_true",
                     help="each BASELINE kernel over 1 to 32 rotated sets (one JSON line each)")
     args = ap.parse_args()
@@ -637,6 +720,9 @@ def main():
     if args.footprint:
         footprint_run(torch, M, O, args.steps, args.warmup, args.only)
         return
+    if args.transient:
+        transient_run(torch, M, O, args.steps, args.warmup)
+        return
     if args.sweep:
         sweep_run(torch, M, O, args.steps, args.warmup)
         return
@@ -656,7 +742,9 @@ def main():
              "input_bytes_per_rotation": len(w.sets) * w.read_bytes_per_step, "wall_s": round(wall, 4),
              "sample_check": w.check()}
         if not args.no_torch:  # after the config's own timing, which it leaves as it was
-            r["torch_same_mix"] = time_same_mix(cls, torch, M, O, args)
+            r["cast_same_mix"] = time_same_mix(CastMix, cls, torch, M, O, args)
+            r["vs_cast_same_mix"] = round(gbs / r["cast_same_mix"]["GB_s"], 3)
+            r["torch_same_mix"] = time_same_mix(SameMix, cls, torch, M, O, args)
             r["vs_torch_same_mix"] = round(gbs / r["torch_same_mix"]["GB_s"], 3)
         if not args.no_cpu:
             r["cpu_baseline"] = time_cpu(w)
