@@ -25,7 +25,7 @@ single-threaded as the Go loops run; "cpu_baseline_all_cores" splits the same
 sample over the host's threads.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-torch] [--only N] [--sets S]
-                [--sweep] [--footprint] [--transient] [--profile REPS]
+                [--sweep] [--footprint] [--transient] [--pcie] [--profile REPS]
 """
 from __future__ import annotations
 
@@ -591,7 +591,8 @@ def sweep_run(torch, M, O, steps, warmup):
     for cls in WORKLOADS:
         for f in (1 / 64, 1 / 16, 1 / 4, 1, 4):
             n = max(4096, int(cls.n * f) // 4096 * 4096)
-            sized = type(cls.__name__, (cls,), {"n": n, "bytes_per_step": cls.bytes_for(n)})
+            sized = type(cls.__name__, (cls,), {"n": n, "bytes_per_step": cls.bytes_for(n),
+                                                "read_bytes_per_step": cls.read_bytes_per_step * n // cls.n})
             w = sized(torch, M, O)
             w.setup()
             ms, _, _ = time_gpu(w, steps, warmup)
@@ -640,6 +641,80 @@ def transient_run(torch, M, O, steps, warmup):
                           "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4)}), flush=True)
         del w
         torch.cuda.empty_cache()
+
+
+def pcie_run(M, O):
+    """--pcie: host-buffer rates through the HIP backend (never `value`,
+    which has its inputs resident in HBM).  Uploads of config 2's FP8 tensor
+    and config 5's Int4 tensor with its f16 group scales (dequantised on the
+    device while the next chunk crosses PCIe), a 134 MB f32 upload and
+    download, and the same FP8 / Int4 tensors loaded from a SafeTensors
+    file.  Best of three passes over four tensors each, source bytes per
+    second."""
+    import struct
+    import tempfile
+    from manifesto_amd.backend import Backend
+    from manifesto_amd.safetensors import SafeTensorsFile
+    b = Backend(0)
+    rng = np.random.default_rng(SEED)
+    rows, cols, group = 14336, 4096, 128
+    packed = [rng.integers(0, 256, rows * cols // 2, dtype=np.uint8) for _ in range(4)]
+    s16 = [O.f32_to_f16(rng.uniform(0.005, 0.02, rows * cols // group).astype(np.float32)) for _ in range(4)]
+    codes = [rng.integers(0, 256, 4096 * 14336, dtype=np.uint8) for _ in range(4)]
+    f32 = rng.standard_normal(1 << 25).astype(np.float32)
+    int4_bytes = 4 * (packed[0].nbytes + s16[0].nbytes)
+
+    def rate(fn, nbytes, what):
+        for t in fn():
+            t.release()
+        best = 1e9
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ts = fn()
+            best = min(best, time.perf_counter() - t0)
+            for t in ts:
+                t.release()
+        print(json.dumps({"what": what, "ms": round(best * 1e3, 2), "GB_s": round(nbytes / best / 1e9, 2)}),
+              flush=True)
+
+    rate(lambda: [b.upload_fp8([4096, 14336], O.F8E4M3, codes[k], 0.0125) for k in range(4)], 4 * codes[0].nbytes,
+         "upload_fp8 e4m3 -> bf16, 4 x [4096,14336] from host memory")
+    rate(lambda: [b.upload_int4([rows, cols], packed[k], s16[k], O.FLOAT16, group) for k in range(4)], int4_bytes,
+         "upload_int4 + f16 scales -> bf16, 4 x [14336,4096] from host memory")
+    rate(lambda: [b.upload([f32.size], O.FLOAT32, f32)], f32.nbytes, "upload f32, 134 MB")
+    t = b.upload([f32.size], O.FLOAT32, f32)
+    out = bytearray(f32.nbytes)
+    b.download(t, out)
+    best = 1e9
+    for _ in range(3):
+        t0 = time.perf_counter()
+        b.download(t, out)
+        best = min(best, time.perf_counter() - t0)
+    print(json.dumps({"what": "download f32, 134 MB, into a reused host buffer", "ms": round(best * 1e3, 2),
+                      "GB_s": round(f32.nbytes / best / 1e9, 2)}), flush=True)
+    t.release()
+    with tempfile.TemporaryDirectory() as d:
+        header, blobs, at = {}, [], 0
+        for k in range(4):
+            for name, dt, shape, raw in ((f"w{k}", "I4", [rows, cols], packed[k].tobytes()),
+                                         (f"w{k}_s", "F16", [rows, cols // group], s16[k].tobytes()),
+                                         (f"q{k}", "F8_E4M3", [4096, 14336], codes[k].tobytes())):
+                header[name] = {"dtype": dt, "shape": shape, "data_offsets": [at, at + len(raw)]}
+                blobs.append(raw)
+                at += len(raw)
+        path = os.path.join(d, "weights.safetensors")
+        with open(path, "wb") as f:
+            text = json.dumps(header).encode()
+            f.write(struct.pack("<Q", len(text)) + text)
+            for raw in blobs:
+                f.write(raw)
+        sf = SafeTensorsFile(path)
+        rate(lambda: [sf.load(f"q{k}", b) for k in range(4)], 4 * codes[0].nbytes,
+             "SafeTensors F8_E4M3 -> bf16, 4 tensors (page cache warm)")
+        rate(lambda: [sf.load(f"w{k}", b, scale=f"w{k}_s", group=group) for k in range(4)], int4_bytes,
+             "SafeTensors I4 + F16 scales -> bf16, 4 tensors (page cache warm)")
+        del sf
+    b.release()
 
 
 def footprint_run(torch, M, O, steps, warmup, only=0):
@@ -694,6 +769,7 @@ def main():
                     help="eager launches of every kernel REPS times (for rocprofv3), no timing")
     ap.add_argument("--sets", type=int, default=0,
                     help="rotate exactly this many buffer sets (default: >= 1 GiB of distinct inputs per cycle)")
+    ap.add_argument("--pcie", action="store_true", help="host-buffer upload / download / SafeTensors rates")
     ap.add_argument("--transient", action="store_true",
                     help="each kernel (and two variants of the gelu chain) from an idle GPU, for a kernel trace")
     ap.add_argument("--footprint", action="store_true",
@@ -722,6 +798,9 @@ def main():
         return
     if args.transient:
         transient_run(torch, M, O, args.steps, args.warmup)
+        return
+    if args.pcie:
+        pcie_run(M, O)
         return
     if args.sweep:
         sweep_run(torch, M, O, args.steps, args.warmup)
