@@ -132,8 +132,8 @@ int mfh_linspace(void* out, uint8_t out_dtype, int64_t count, float start, float
 /* ---- dtype conversion and dequantisation -------------------------------- */
 
 /* Element-wise conversion of `count` logical elements from `in_dtype` to
- * `out_dtype` (Float64, Float32, Float16, BFloat16, Float8E4M3, Float8E5M2 or
- * Int8) with the reference's exact bit rules: BytesToFloat32
+ * `out_dtype` (Float64, Float32, Float16, BFloat16, Float8E4M3, Float8E5M2,
+ * Int8 or Int4) with the reference's exact bit rules: BytesToFloat32
  * (dtype/convert/convert.go:85-146) followed, for 16-bit outputs, by
  * BytesToBFloat16 / BytesToFloat16 narrowing (:155-188) and, for FP8 outputs,
  * by BytesToFloat8E4M3 / BytesToFloat8E5M2 (:194-232: NewF8E4M3FromFloat32 /
@@ -142,8 +142,10 @@ int mfh_linspace(void* out, uint8_t out_dtype, int64_t count, float start, float
  * (:36-79: float64 of each dtype's decode, a NaN quieted with its payload as
  * amd64's cvtss2sd does); BytesToInt8 (:235-263: the f64 value saturated to
  * [-128, 127], then truncated toward zero; NaN, which Go leaves to the
- * platform, gives 0 as on amd64 and arm64).  in_dtype may be any numeric
- * code including Int4 (count nibbles). */
+ * platform, gives 0 as on amd64 and arm64); Int4: that int8 value through
+ * int4Encode (dtype/int4.go:60-70, clamped to [-8, 7]) packed low nibble
+ * first into (count + 1) / 2 bytes, an odd count's last high nibble 0.
+ * in_dtype may be any numeric code including Int4 (count nibbles). */
 int mfh_convert(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype,
                 int64_t count, void* stream);
 

@@ -616,6 +616,78 @@ int launch_encode_byte(const Device* dev, mfh_u8* out, const void* in, int in_dt
 }
 
 // ---------------------------------------------------------------------------
+// Any numeric dtype -> packed Int4: BytesToInt8's value (saturated to
+// [-128, 127], truncated, NaN -> 0), then int4Encode (dtype/int4.go:60-70):
+// clamped to [-8, 7], low nibble first.  An odd count leaves the last byte's
+// high nibble 0, as a fresh Int4Vector holds it (tensor/int4vector.go:74-87).
+// ---------------------------------------------------------------------------
+
+template <int IN>
+MFH_DEV mfh_u32 nibble_at(const void* in, mfh_i64 i)
+{
+    const int v = (int)(signed char)byte_at<IN, kInt8>(in, i);
+    return (mfh_u32)(v < -8 ? -8 : (v > 7 ? 7 : v)) & 0xfu;
+}
+
+// Item = 32 elements -> one 16-byte store of nibbles (16-byte aligned
+// output), then the byte loop for the rest.
+template <int IN>
+__global__ __launch_bounds__(kBlock) void k_encode_int4(const void* __restrict__ in, mfh_u8* __restrict__ out,
+                                                        mfh_i64 n, int vec_ok)
+{
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 nitems = vec_ok ? n / 32 : 0;
+    u32x4* dst = reinterpret_cast<u32x4*>(out);
+    for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            mfh_u32 word = 0u;
+#pragma unroll
+            for (int k = 0; k < 8; k++) word |= nibble_at<IN>(in, v * 32 + 8 * q + k) << (4 * k);
+            o[q] = word;
+        }
+        store_nt(&dst[v], o);
+    }
+    const mfh_i64 nbytes = (n + 1) / 2;
+    for (mfh_i64 b = nitems * 16 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; b < nbytes; b += stride) {
+        const mfh_u32 lo = nibble_at<IN>(in, 2 * b);
+        const mfh_u32 hi = 2 * b + 1 < n ? nibble_at<IN>(in, 2 * b + 1) : 0u;
+        out[b] = (mfh_u8)(lo | (hi << 4));
+    }
+}
+
+int launch_encode_int4(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
+{
+    const int vec_ok = aligned16(out) && n >= 32;
+    const int64_t items = vec_ok ? n / 32 : (n + 1) / 2;
+    const unsigned grid = grid_for(items, dev, Kern::kConvert);
+    switch (in_dt) {
+#define MFH_ENCODE_I4_CASE(DT) \
+    case DT: k_encode_int4<DT><<<grid, kBlock, 0, stream>>>(in, out, n, vec_ok); break;
+        MFH_ENCODE_I4_CASE(kFloat64)
+        MFH_ENCODE_I4_CASE(kFloat32)
+        MFH_ENCODE_I4_CASE(kFloat16)
+        MFH_ENCODE_I4_CASE(kBFloat16)
+        MFH_ENCODE_I4_CASE(kF8E4M3)
+        MFH_ENCODE_I4_CASE(kF8E5M2)
+        MFH_ENCODE_I4_CASE(kInt64)
+        MFH_ENCODE_I4_CASE(kInt32)
+        MFH_ENCODE_I4_CASE(kInt16)
+        MFH_ENCODE_I4_CASE(kInt8)
+        MFH_ENCODE_I4_CASE(kInt4)
+        MFH_ENCODE_I4_CASE(kUint64)
+        MFH_ENCODE_I4_CASE(kUint32)
+        MFH_ENCODE_I4_CASE(kUint16)
+        MFH_ENCODE_I4_CASE(kUint8)
+#undef MFH_ENCODE_I4_CASE
+    default:
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+    }
+    return launch_status("k_encode_int4");
+}
+
+// ---------------------------------------------------------------------------
 // Any numeric dtype -> f64 (BytesToFloat64, dtype/convert/convert.go:36-79)
 // ---------------------------------------------------------------------------
 
@@ -923,8 +995,8 @@ int mfh_convert(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype, 
     MFH_TRY(bind_device(&dev));
     if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: negative count %lld", (long long)count);
     const bool to_byte = out_dtype == kF8E4M3 || out_dtype == kF8E5M2 || out_dtype == kInt8;
-    if (!is_out_dtype(out_dtype) && !to_byte && out_dtype != kFloat64)
-        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: output dtype %s is not f64/f32/bf16/f16/fp8/i8",
+    if (!is_out_dtype(out_dtype) && !to_byte && out_dtype != kFloat64 && out_dtype != kInt4)
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: output dtype %s is not f64/f32/bf16/f16/fp8/i8/i4",
                     dtype_name(out_dtype));
     if (count == 0) return MFH_OK;
     if (!out || !in) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: NULL buffer");
@@ -933,6 +1005,7 @@ int mfh_convert(void* out, uint8_t out_dtype, const void* in, uint8_t in_dtype, 
     if (out_dtype == kF8E4M3) return launch_encode_byte<kF8E4M3>(dev, bytes, in, in_dtype, count, s);
     if (out_dtype == kF8E5M2) return launch_encode_byte<kF8E5M2>(dev, bytes, in, in_dtype, count, s);
     if (out_dtype == kInt8) return launch_encode_byte<kInt8>(dev, bytes, in, in_dtype, count, s);
+    if (out_dtype == kInt4) return launch_encode_int4(dev, bytes, in, in_dtype, count, s);
     if (out_dtype == kFloat64) return launch_widen_f64(dev, out, in, in_dtype, count, s);
     if (in_dtype == kF8E4M3 || in_dtype == kF8E5M2)
         return by_out<Fp8Launch>(out_dtype, dev, out, in, (int)in_dtype, count, 1.0f, s);

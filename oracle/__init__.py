@@ -193,6 +193,25 @@ def bytes_to_i8(dtype: int, buf: np.ndarray) -> np.ndarray:
     return out
 
 
+def int4_encode(values: np.ndarray) -> np.ndarray:
+    """Packs int8 values as Int4Pair bytes: int4Encode (dtype/int4.go:60-70)
+    clamps each to [-8, 7] and keeps its low nibble; element 2k is the low
+    nibble of byte k (dtype/int4.go:12-22).  An odd count leaves the last
+    byte's high nibble 0, as a fresh Int4Vector holds it
+    (tensor/int4vector.go:74-87)."""
+    v = np.asarray(values, dtype=np.int8).reshape(-1)
+    nib = (np.clip(v.astype(np.int16), -8, 7) & 0xF).astype(np.uint8)
+    if nib.size % 2:
+        nib = np.append(nib, np.uint8(0))
+    return (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+
+
+def bytes_to_i4(dtype: int, buf: np.ndarray, count: int) -> np.ndarray:
+    """BytesToInt8's values of the first `count` elements, packed by
+    int4_encode: what mfh_convert writes for an Int4 output."""
+    return int4_encode(bytes_to_i8(dtype, buf)[:count])
+
+
 def bytes_to_bf16(dtype: int, buf: np.ndarray) -> np.ndarray:
     buf = np.ascontiguousarray(buf).view(np.uint8).reshape(-1)
     n = ctypes.c_int64()

@@ -1,5 +1,6 @@
-"""GPU parity of mfh_convert's f64 and i8 outputs: BytesToFloat64
-(dtype/convert/convert.go:36-79, decoders.go) and BytesToInt8 (:235-263),
+"""GPU parity of mfh_convert's f64, i8 and i4 outputs: BytesToFloat64
+(dtype/convert/convert.go:36-79, decoders.go), BytesToInt8 (:235-263) and
+BytesToInt8 through int4Encode (dtype/int4.go:60-70),
 bit for bit against the CPU oracle on every 16-bit, FP8, Int4 and byte code,
 random wide sources with their edge values, tails and misaligned buffers, and
 over every f32 input against closed forms evaluated with torch on the device.
@@ -155,6 +156,46 @@ def test_every_f32_input_to_f64_and_i8():
 def test_rejects_unsupported_outputs():
     src, sp = to_dev(np.zeros(64, np.uint8))
     out, op = empty_dev(256)
-    for bad in (O.INT16, O.INT32, O.UINT8, O.INT4, 16):
-        with pytest.raises(M.MFHError, match="is not f64/f32/bf16/f16/fp8/i8"):
+    for bad in (O.INT16, O.INT32, O.UINT8, 16):
+        with pytest.raises(M.MFHError, match="is not f64/f32/bf16/f16/fp8/i8/i4"):
             M.convert(op, bad, sp, O.FLOAT32, 16, stream())
+
+
+# ---- Int4 output: BytesToInt8's value through int4Encode (dtype/int4.go:60-70) ----
+
+def convert_i4(a, in_dt, n, pad_in=0, pad_out=0):
+    src, sp = to_dev(a, pad=pad_in)
+    out, op = empty_dev((n + 1) // 2, pad=pad_out)
+    M.convert(op, O.INT4, sp, in_dt, n, stream())
+    return to_host(out, np.uint8, pad=pad_out)
+
+
+@pytest.mark.parametrize("in_dt", [O.FLOAT16, O.BFLOAT16, O.F8E4M3, O.F8E5M2, O.INT8, O.UINT8, O.INT16, O.UINT16,
+                                   O.INT4])
+def test_int4_from_every_code(in_dt):
+    if in_dt in (O.FLOAT16, O.BFLOAT16, O.INT16, O.UINT16):
+        a = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(NP_OF[in_dt])
+        n = a.size
+    else:
+        a = np.tile(np.arange(256, dtype=np.uint8), 3)
+        n = a.size * (2 if in_dt == O.INT4 else 1)
+    check(convert_i4(a, in_dt, n), O.bytes_to_i4(in_dt, a, n), f"{in_dt}->i4")
+
+
+@pytest.mark.parametrize("in_dt", [O.FLOAT64, O.FLOAT32, O.INT64, O.INT32, O.UINT64, O.UINT32])
+@pytest.mark.parametrize("n, pad", [(50001, 0), (50001, 1), (50000, 16), (7, 0), (1, 2), (33, 0)])
+def test_int4_wide_sources_odd_counts_misaligned(in_dt, n, pad):
+    # 32-element items into 16-byte stores when the output is 16-byte
+    # aligned, the byte loop otherwise and for the tail; an odd count's last
+    # high nibble is 0
+    a = wide_source(in_dt, n, np.random.default_rng(in_dt * 13 + n + pad))
+    for m in (a.size, a.size - 1):  # both parities of the count
+        got = convert_i4(a, in_dt, m, pad_in=pad, pad_out=pad % 3)
+        check(got, O.bytes_to_i4(in_dt, a, m), f"{in_dt}->i4 n={m} pad={pad}")
+
+
+def test_golden_int4_pairs(golden):
+    g = golden["int4_pair"]
+    vals = np.array([v for pair in g["pairs"] for v in pair], np.int8)
+    got = convert_i4(vals, O.INT8, vals.size)
+    assert O.bytes_to_i8(O.INT4, got).reshape(-1, 2).tolist() == g["lo_hi"]

@@ -680,3 +680,34 @@ def test_bytes_to_i8_checks_catch_planted_mistakes():
                                   want[ok & (np.abs(d) < 1e9)])
         # truncating the f32 value of an f64 input (1.9999999999 becomes 2)
         assert not np.array_equal(_i8_closed(d.astype(np.float32)), want)
+
+
+# --------------------------------------------------------------------------
+# Int4 encode (dtype/int4.go:60-70): int8 -> clamp to [-8, 7] -> nibble,
+# low nibble first.  Pinned by decoding the packed bytes with the oracle's
+# Int4 decode (itself pinned by the golden pair vectors above) and checking
+# the clamp against plain integer bounds, for every int8 value in both
+# nibble positions.
+# --------------------------------------------------------------------------
+
+def test_int4_encode_every_int8_value():
+    v = np.arange(-128, 128, dtype=np.int16).astype(np.int8)
+    want = np.minimum(np.maximum(v.astype(np.int16), -8), 7)
+    zero = np.zeros_like(v)
+    for slot, pairs in ((0, np.stack([v, zero], axis=1)), (1, np.stack([zero, v], axis=1))):
+        back = O.bytes_to_i8(O.INT4, O.int4_encode(pairs.reshape(-1))).astype(np.int16).reshape(-1, 2)
+        np.testing.assert_array_equal(back[:, slot], want)  # every value as the low, then the high nibble
+        np.testing.assert_array_equal(back[:, 1 - slot], 0)
+    # an odd count: the last byte's high nibble is 0
+    assert O.int4_encode(np.array([3, -2, 7], np.int8)).tolist() == [0xE3, 0x07]
+    # planted: wrapping instead of clamping (v & 0xF) decodes -100 as -4, not -8
+    wrapped = (np.array([-100], np.int16) & 0xF).astype(np.uint8)
+    assert O.bytes_to_i8(O.INT4, wrapped).tolist() != [-8]
+
+
+def test_bytes_to_i4_follows_bytes_to_i8():
+    # the float path: BytesToInt8's saturate-then-truncate, then the clamp
+    f = np.array([0.0, -0.0, 0.9, -0.9, 7.99, -8.99, 8.0, -9.0, 1e9, -1e9, np.nan, np.inf, -np.inf, 3.5],
+                 dtype=np.float32)
+    got = O.bytes_to_i8(O.INT4, O.bytes_to_i4(O.FLOAT32, f, f.size))[:f.size].tolist()
+    assert got == [0, 0, 0, 0, 7, -8, 7, -8, 7, -8, 0, 7, -8, 3]

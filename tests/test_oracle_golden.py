@@ -170,3 +170,19 @@ def test_linspace_scalar_broadcast_golden(golden):
         O.scalar_broadcast(sig, 0.0, "div")
     with pytest.raises(O.OracleError):
         O.linspace(0.0, 1.0, 0)
+
+
+def test_int4_pair_golden(golden):
+    # NewInt4Pair packs the clamped low and high nibbles; Lo/Hi sign-extend
+    # them back (the oracle's Int4 decode), so each pair's byte decodes to
+    # the reference's expected values.
+    g = golden["int4_pair"]
+    for (lo, hi), want in zip(g["pairs"], g["lo_hi"]):
+        packed = O.int4_encode(np.array([lo, hi], np.int8))
+        assert packed.size == 1
+        assert O.bytes_to_i8(O.INT4, packed).tolist() == want
+    for key, slot in (("with_lo", 0), ("with_hi", 1)):
+        case = g[key]
+        vals = list(case["pair"])
+        vals[slot] = case["value"]  # WithLo/WithHi replace one nibble of the pair
+        assert O.bytes_to_i8(O.INT4, O.int4_encode(np.array(vals, np.int8))).tolist() == case["lo_hi"]
