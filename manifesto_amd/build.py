@@ -23,6 +23,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = ["runtime.cpp", "dequant.hip", "hostmath.hip", "scratch.hip", "fusion.cpp", "graph.cpp", "plan.cpp",
+           "hostcopy.cpp",
            "backend.cpp", "safetensors.cpp"]
 PRELUDE_PARTS = ["codec.hpp", "devmath.hpp", "fusion_io.hpp"]
 

@@ -5,9 +5,10 @@
 // (runtime/axpy.go:44-93).
 //
 // A backend owns one HIP stream, a ring of two pinned host chunks and two
-// device staging chunks.  An upload copies chunk i into a pinned slot while
-// the DMA (and dequant kernel) of chunk i-1 runs from the other slot; a slot
-// is reused once the event recorded after its last reader has fired.
+// device staging chunks.  An upload copies chunk i into a pinned slot (split
+// over the host copy threads of hostcopy.cpp) while the DMA (and dequant
+// kernel) of chunk i-1 runs from the other slot; a slot is reused once the
+// event recorded after its last reader has fired.
 // Tensors share their storage with their views; the storage and the backend
 // state outlive a released backend handle until the last tensor handle goes,
 // so a stale tensor reports closed instead of touching freed memory.
@@ -21,6 +22,7 @@
 #include "../../include/mfh_backend.h"
 #include "backend_internal.hpp"
 #include "common.hpp"
+#include "hostcopy.hpp"
 
 namespace mfh {
 namespace {
@@ -216,7 +218,8 @@ int stream_in(BackendState& s, const Plan& p, Source& src, size_t n_src, int64_t
         const size_t scale_at = (len + 15) & ~(size_t)15;
         const size_t scale_len = scaled4 ? (size_t)((count + p.group - 1) / p.group) * ssize : 0;
         MFH_TRY(check_hip(hipEventSynchronize(s.slot_free[slot]), "hipEventSynchronize"));
-        MFH_TRY(src.read(s.pinned[slot], done, len));
+        uint8_t* slot_at = static_cast<uint8_t*>(s.pinned[slot]);
+        MFH_TRY(for_each_piece(len, [&](size_t lo, size_t hi) { return src.read(slot_at + lo, done + lo, hi - lo); }));
         if (scaled4)
             MFH_TRY(p.scales->read(static_cast<uint8_t*>(s.pinned[slot]) + scale_at, (size_t)(first / p.group) * ssize,
                                    scale_len));
@@ -491,7 +494,7 @@ int mfh_backend_download(mfh_backend* backend, const mfh_tensor* tensor, uint8_t
         }
         if (prev_slot >= 0) {
             MFH_TRY(check_hip(hipEventSynchronize(s.slot_free[prev_slot]), "hipEventSynchronize"));
-            std::memcpy(static_cast<uint8_t*>(dst) + prev_at, s.pinned[prev_slot], prev_len);
+            MFH_TRY(copy_parallel(static_cast<uint8_t*>(dst) + prev_at, s.pinned[prev_slot], prev_len));
         }
         prev_slot = len ? slot : -1;
         prev_at = at;

@@ -164,3 +164,23 @@ def test_scale_for_a_tensor_stored_as_written_is_refused(backend, tmp_path):
     with pytest.raises(M.MFHError, match="stored as written") as e:
         f.load("w", backend, scale="s")
     assert e.value.code == -1
+
+
+def test_truncated_tensor_fails_from_a_copy_thread(backend, tmp_path):
+    # A tensor whose bytes end early: the staging chunk that crosses the end
+    # of the file is read in pieces by several host threads, and the piece
+    # that hits EOF reports it on the calling thread.  A whole tensor loads
+    # after it from the same backend.
+    n = (40 << 20) // 4
+    body = np.arange(n, dtype=np.float32).tobytes()
+    header = {"w": {"dtype": "F32", "shape": [n], "data_offsets": [0, len(body)]}}
+    text = json.dumps(header).encode()
+    path = tmp_path / "cut.safetensors"
+    path.write_bytes(struct.pack("<Q", len(text)) + text + body[:30 << 20])
+    f = SafeTensorsFile(path)
+    with pytest.raises(M.MFHError, match='safetensors read "w": unexpected EOF'):
+        f.load("w", backend)
+    good = SafeTensorsFile(write(tmp_path / "whole.safetensors", {"w": ("F32", [n], body)}))
+    t = good.load("w", backend)
+    assert backend.download(t)[1] == body
+    t.release()
