@@ -25,7 +25,7 @@ single-threaded as the Go loops run; "cpu_baseline_all_cores" splits the same
 sample over the host's threads.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-torch] [--only N] [--sets S]
-                [--sweep] [--footprint] [--transient] [--pcie] [--profile REPS]
+                [--sweep] [--footprint] [--transient] [--pcie] [--graph-calls] [--profile REPS]
 """
 from __future__ import annotations
 
@@ -717,6 +717,53 @@ def pcie_run(M, O):
     b.release()
 
 
+def graph_calls_run(torch, M):
+    """--graph-calls: mfh_graph_call (runtime.Backend.CallGraph) on a graph
+    of 4 independent chains of 8 unfused f32 nodes, per call, at 16 K, 256 K
+    and 4 M elements, with MaxStreams 1 and 4, each plain and replayed from a
+    captured HIP graph.  Device time per call from 200 back-to-back calls
+    between a synchronize on each side; host time = until the call returns."""
+    from manifesto_amd.graph import Graph, GraphNode
+    from manifesto_amd import plan as P
+    ops = ["math.neg", "math.abs", "math.add", "math.mul", "activation.relu", "math.sub", "math.max", "math.neg"]
+    stream = torch.cuda.current_stream().cuda_stream
+    for n in (16 << 10, 256 << 10, 4 << 20):
+        x = torch.randn(n, device="cuda")
+        y = torch.randn(n, device="cuda")
+        outs = {f"o{c}": torch.empty(n, device="cuda") for c in range(4)}
+        for streams in (1, 4):
+            for replay in (False, True):
+                nodes, outputs = [], {}
+                for c in range(4):
+                    prev = "x" if c % 2 == 0 else "y"
+                    for k, op in enumerate(ops):
+                        binary = op in ("math.add", "math.mul", "math.sub", "math.max")
+                        node = f"c{c}n{k}"
+                        nodes.append(GraphNode(node, op, [prev, "y" if c % 2 == 0 else "x"] if binary else [prev]))
+                        prev = node
+                    outputs[f"o{c}"] = prev
+                g = Graph(inputs=["x", "y"], outputs=outputs, execution_dtype=M.FLOAT32, nodes=nodes)
+                P.set_max_streams(g, streams)
+                g.set_replay(replay)
+                for _ in range(3):
+                    g.call({"x": x, "y": y}, outs, stream)
+                torch.cuda.synchronize()
+                reps = 200
+                host = 0.0
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    h0 = time.perf_counter()
+                    g.call({"x": x, "y": y}, outs, stream)
+                    host += time.perf_counter() - h0
+                torch.cuda.synchronize()
+                wall = (time.perf_counter() - t0) / reps
+                print(json.dumps({"elements": n, "max_streams": streams, "replay": replay,
+                                  "us_per_call": round(wall * 1e6, 1), "host_us_per_call": round(host / reps * 1e6, 1),
+                                  "replayed_calls": g.replayed_calls(), "streams_used": P.streams_used(g)}),
+                      flush=True)
+                del g
+
+
 def footprint_run(torch, M, O, steps, warmup, only=0):
     """--footprint: each BASELINE kernel over 1 to 32 rotated buffer sets,
     timed as the bench times a step.  One JSON line per kernel and rotation:
@@ -770,6 +817,7 @@ def main():
     ap.add_argument("--sets", type=int, default=0,
                     help="rotate exactly this many buffer sets (default: >= 1 GiB of distinct inputs per cycle)")
     ap.add_argument("--pcie", action="store_true", help="host-buffer upload / download / SafeTensors rates")
+    ap.add_argument("--graph-calls", action="store_true", help="mfh_graph_call time per call, streams and replay")
     ap.add_argument("--transient", action="store_true",
                     help="each kernel (and two variants of the gelu chain) from an idle GPU, for a kernel trace")
     ap.add_argument("--footprint", action="store_true",
@@ -801,6 +849,9 @@ def main():
         return
     if args.pcie:
         pcie_run(M, O)
+        return
+    if args.graph_calls:
+        graph_calls_run(torch, M)
         return
     if args.sweep:
         sweep_run(torch, M, O, args.steps, args.warmup)
