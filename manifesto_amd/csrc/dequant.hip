@@ -55,8 +55,8 @@ MFH_DEV void store_one(void* out, mfh_i64 i, mfh_u32 enc)
 // loops only when there are more chunks than the largest grid.  A block
 // issues its first chunk's loads before building the table, so the load
 // latency covers the build; stores are streaming (StreamOut: non-temporal).
-// Measured at [4096, 14336] on MI355X: 7.0 TB/s against 5.4 for plain
-// stores in a grid-stride loop at 6 blocks per CU.
+// Measured at [4096, 14336] on MI355X with the codes coming from HBM:
+// 6.1-6.2 TB/s, within 3% of a bf16 -> f32 cast moving the same bytes.
 template <int OUT, int U, int BS>
 __global__ __launch_bounds__(BS) void k_dequant_fp8(const mfh_u8* __restrict__ in,
                                                         void* __restrict__ out, mfh_i64 n,

@@ -4,8 +4,8 @@
 // Every streaming kernel here is written so that each store instruction of a
 // wave writes one contiguous 1 KiB span (64 lanes x 16 bytes): on MI355X a
 // wave that interleaves two 16-byte stores per lane (lane j writing bytes
-// 32j..32j+15 and then 32j+16..32j+31) reaches ~4.5-5.0 TB/s on a 1:2
-// read:write stream, the contiguous form ~5.6-5.8 TB/s.
+// 32j..32j+15 and then 32j+16..32j+31) ran 15-20% slower on a 1:2
+// read:write stream than the contiguous form.
 #ifndef MFH_LAUNCH_HPP
 #define MFH_LAUNCH_HPP
 
@@ -54,10 +54,10 @@ int launch_status(const char* what);
 // Streaming 16-byte stores of a chunk: buffer stores with the non-temporal
 // (nt) and sc1 cache-policy bits, addressed from the chunk's first item (the
 // base is uniform across the block, so the descriptor lives in SGPRs).  On
-// MI355X, non-temporal stores in short-lived blocks lift a 1:2 read:write
-// stream from 5.6 to 7.0 TB/s and a 1:4 one from 5.4 to 7.0 (no-compute
-// probes at the BASELINE sizes); plain-address nontemporal stores are within
-// 1%.  The descriptor's record count is the chunk's remaining bytes, so the
+// MI355X, with the inputs coming from HBM, nt|sc1 stores run the FP8 dequant
+// (1:2 read:write) at 6.1-6.2 TB/s and the Int4 dequant (1:4) at 6.0-6.1,
+// against 5.8 and 5.5 with plain stores; nt alone is 1-2% slower, sc1 alone
+// 4-6%.  The descriptor's record count is the chunk's remaining bytes, so the
 // hardware drops anything past the end of the output.
 struct StreamOut {
     __amdgpu_buffer_rsrc_t rsrc;
