@@ -54,7 +54,9 @@ MFH_DEV void store_one(void* out, mfh_i64 i, mfh_u32 enc)
 // block outlives its chunk, so the blocks sweep memory in dispatch order) and
 // loops only when there are more chunks than the largest grid.  A block
 // issues its first chunk's loads before building the table, so the load
-// latency covers the build; stores are streaming (StreamOut: non-temporal).
+// latency covers the build; stores are streaming (StreamOut: non-temporal)
+// and so are the code loads (+0.6% against plain loads; Int4's nibbles lose
+// 0.8% that way and stay plain).
 // Measured at [4096, 14336] on MI355X with the codes coming from HBM:
 // 6.1-6.2 TB/s, within 3% of a bf16 -> f32 cast moving the same bytes.
 template <int OUT, int U, int BS>
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(BS) void k_dequant_fp8(const mfh_u8* __restrict__ i
         for (int u = 0; u < U; u++) {
             const mfh_i64 i = c * kChunk + u * BS + t;
             if (i < nitems) {
-                if constexpr (kCodes == 8) w[u] = reinterpret_cast<const u32x2*>(in)[i];
+                if constexpr (kCodes == 8) w[u] = load_nt(&reinterpret_cast<const u32x2*>(in)[i]);
                 else w[u] = u32x2{reinterpret_cast<const mfh_u32*>(in)[i], 0u};
             }
         }

@@ -84,9 +84,9 @@ __device__ inline void store_nt(T* p, T v)
 }
 
 // Streaming load (global_load ... nt).  Used where a kernel reads at least as
-// many bytes as it writes: non-temporal loads measured +4% on a 1:1 stream
-// and +8% on 2:1, but -10% on a 1:2 stream, so write-heavy kernels (FP8 and
-// Int4 dequant, widening casts) keep plain loads.
+// many bytes as it writes (non-temporal loads measured +4% on a 1:1 stream
+// and +8% on 2:1), and by the FP8 dequant (+0.6% with its codes coming from
+// HBM); the Int4 dequant (-0.8%) and the widening casts keep plain loads.
 template <typename T>
 __device__ inline T load_nt(const T* p)
 {
