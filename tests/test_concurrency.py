@@ -226,3 +226,34 @@ def test_one_backend_from_many_threads():
         assert got_y == want_y, f"thread {k}: axpy"
         assert got_8 == want_fp8, f"thread {k}: fp8 upload"
         assert got_4 == want_int4, f"thread {k}: int4 upload"
+
+
+@pytest.mark.gpu
+def test_backend_per_thread_uploads_and_downloads():
+    # One backend per thread (one stream and staging ring each); every
+    # staging copy goes through the library's shared pool of host copy
+    # threads, so uploads and downloads of different backends interleave
+    # there.  Every tensor keeps its bytes, and a SafeTensors-sized FP8 load
+    # crosses several staging chunks per thread.
+    from manifesto_amd.backend import Backend
+    M.init(0)
+    n = (36 << 20) + 5
+    codes = np.random.default_rng(31).integers(0, 256, n, dtype=np.uint8)
+    want_fp8 = O.dequant_fp8(codes, O.F8E5M2, 2.0, O.FLOAT16).tobytes()
+    results = {}
+
+    def work(k):
+        b = Backend(0)
+        try:
+            f = np.random.default_rng(200 + k).standard_normal(n // 4).astype(np.float32)
+            tf = b.upload_async([f.size], O.FLOAT32, f)
+            t8 = b.upload_fp8([n], O.F8E5M2, codes, 2.0, O.FLOAT16)
+            results[k] = (bytes(b.download(tf)[1]) == f.tobytes(), bytes(b.download(t8)[1]) == want_fp8)
+            for t in (tf, t8):
+                t.release()
+        finally:
+            b.release()
+
+    run_threads(work)
+    for k in range(THREADS):
+        assert results[k] == (True, True), f"thread {k}: {results[k]}"
