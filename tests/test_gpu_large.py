@@ -101,3 +101,21 @@ def test_fused_chain_past_2_31(torch):
         product = a[lo:hi].float() * b[lo:hi].float()
         want = (product + c[lo:hi].float()).to(torch.bfloat16)
         assert torch.equal(out[lo:hi].view(torch.int16), want.view(torch.int16)), f"chain mismatch in [{lo}, {hi})"
+
+
+def test_int4_encode_round_trip_past_2_31(torch):
+    # int8 -> Int4 (int4Encode's clamp) -> int8 again over an odd count past
+    # 2^31: the round trip must give every value clamped to [-8, 7] and the
+    # last byte's high nibble must stay 0
+    n = (1 << 31) + 7
+    log(f"int8 -> int4 -> int8, n = {n}")
+    g = torch.Generator(device="cuda").manual_seed(35)
+    v = torch.randint(-128, 128, (n,), dtype=torch.int8, device="cuda", generator=g)
+    packed = torch.empty((n + 1) // 2, dtype=torch.uint8, device="cuda")
+    back = torch.empty(n, dtype=torch.int8, device="cuda")
+    M.convert(packed.data_ptr(), M.INT4, v.data_ptr(), M.INT8, n, stream())
+    M.convert(back.data_ptr(), M.INT8, packed.data_ptr(), M.INT4, n, stream())
+    for lo, hi in chunks(n):
+        want = torch.clamp(v[lo:hi], -8, 7)
+        assert torch.equal(back[lo:hi], want), f"int4 round trip mismatch in [{lo}, {hi})"
+    assert int(packed[-1]) >> 4 == 0
