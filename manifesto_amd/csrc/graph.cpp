@@ -202,6 +202,11 @@ struct Replay {
 };
 constexpr int kMaxReplays = 8;
 
+// A call's launches, placement and streams for one signature of bindings
+// (defined with the execution code below).
+struct PlannedCall;
+constexpr int kMaxPlans = 8;
+
 }  // namespace
 }  // namespace mfh
 
@@ -236,6 +241,10 @@ struct mfh_graph {
     uint64_t replay_generation = 0;
     int64_t replayed = 0;
     hipStream_t capture = nullptr;
+    // calls planned before, keyed by their bindings without the pointers;
+    // cleared by any change to the graph
+    std::vector<std::unique_ptr<mfh::PlannedCall>> plans;
+    uint64_t plan_clock = 0;
 };
 
 namespace mfh {
@@ -597,6 +606,7 @@ struct Slot {
     int producer = -1;          // step that writes it
     std::vector<int> readers;   // steps that read it
     bool pinned = false;        // read by the output copies after the last step
+    int out_index = -1;         // kBound: the output binding written in place
 };
 
 struct Step {
@@ -611,6 +621,7 @@ struct Step {
 struct Copy {
     int slot;
     const mfh_value* to;
+    int to_index;  // of `to` in the call's output bindings
 };
 
 // A call's values and launches, before placement and streams.
@@ -775,6 +786,7 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
             if (b->dtype == out.dtype && b->count == out.count && b->data) {
                 out.kind = Slot::kBound;
                 out.ptr = b->data;
+                out.out_index = (int)(b - outputs);
             }
         }
         st.result = (int)slots.size();
@@ -798,7 +810,7 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
             return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: output \"%s\" has no data", b->name);
         if (s.kind == Slot::kBound && s.ptr == b->data) continue;
         s.pinned = true;
-        P->copies.push_back(Copy{it->second, b});
+        P->copies.push_back(Copy{it->second, b, (int)(b - outputs)});
     }
     return MFH_OK;
 }
@@ -935,6 +947,89 @@ std::string call_key(const Graph& g, const mfh_value* inputs, int32_t n_inputs, 
     return key + buf;
 }
 
+struct PlannedCall {
+    std::string key;
+    Prepared P;
+    Topology topo;
+    int n_streams = 1, n_events = 0;
+    int64_t need = 0;
+    uint64_t tick = 0;
+};
+
+// What a call's plan depends on besides the graph: value names, dtypes and
+// counts, which bindings have data, which output bindings share a buffer,
+// the stream budget.  Not the pointers: a call on new buffers of the same
+// shapes reuses the plan with its pointers rebound.
+std::string plan_key(const Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
+                     int32_t n_outputs)
+{
+    std::string key;
+    char buf[64];
+    for (int32_t i = 0; i < n_inputs; i++) {
+        key += inputs[i].name ? inputs[i].name : "";
+        snprintf(buf, sizeof buf, "|%u|%lld|%d;", (unsigned)inputs[i].dtype, (long long)inputs[i].count,
+                 inputs[i].data != nullptr);
+        key += buf;
+    }
+    key += "->";
+    for (int32_t i = 0; i < n_outputs; i++) {
+        int alias = i;  // the first binding with the same buffer
+        for (int32_t j = 0; j < i; j++)
+            if (outputs[j].data == outputs[i].data) {
+                alias = j;
+                break;
+            }
+        key += outputs[i].name ? outputs[i].name : "";
+        snprintf(buf, sizeof buf, "|%u|%lld|%d|%d;", (unsigned)outputs[i].dtype, (long long)outputs[i].count,
+                 outputs[i].data != nullptr, alias);
+        key += buf;
+    }
+    snprintf(buf, sizeof buf, "s=%d", (int)g.max_streams);
+    return key + buf;
+}
+
+// Points a cached plan at this call's buffers.
+void rebind(Prepared& P, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs)
+{
+    for (int32_t i = 0; i < n_inputs; i++) P.slots[i].ptr = inputs[i].data;  // prepare() puts inputs first
+    for (Slot& s : P.slots)
+        if (s.kind == Slot::kBound) s.ptr = outputs[s.out_index].data;
+    for (Copy& c : P.copies) c.to = &outputs[c.to_index];
+}
+
+// The plan of a call: prepared, scheduled and laid out on its signature's
+// first call, rebound to the call's buffers after that.  Prepare, stream
+// scheduling and placement took about a third of a plain call's host time.
+int plan_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
+              PlannedCall** out)
+{
+    const std::string key = plan_key(g, inputs, n_inputs, outputs, n_outputs);
+    for (auto& p : g.plans)
+        if (p->key == key) {
+            rebind(p->P, inputs, n_inputs, outputs);
+            p->tick = ++g.plan_clock;
+            *out = p.get();
+            return MFH_OK;
+        }
+    auto p = std::make_unique<PlannedCall>();
+    MFH_TRY(prepare(g, inputs, n_inputs, outputs, n_outputs, false, &p->P));
+    p->topo = launch_topology(g, p->P);
+    MFH_TRY(schedule_streams(p->topo, g.max_streams));
+    for (const PlanNode& n : p->topo.nodes) {
+        p->n_streams = std::max(p->n_streams, n.stream + 1);
+        for (const mfh_sync_event& e : n.barriers) p->n_events = std::max(p->n_events, e.event_id + 1);
+    }
+    p->need = lay_out(p->P, p->topo);
+    p->key = key;
+    p->tick = ++g.plan_clock;
+    if ((int)g.plans.size() >= kMaxPlans)
+        g.plans.erase(std::min_element(g.plans.begin(), g.plans.end(),
+                                       [](const auto& a, const auto& b) { return a->tick < b->tick; }));
+    g.plans.push_back(std::move(p));
+    *out = g.plans.back().get();
+    return MFH_OK;
+}
+
 // Waits for the last call, then drops every captured call.
 void drop_replays(Graph& g)
 {
@@ -944,6 +1039,13 @@ void drop_replays(Graph& g)
     for (Replay& r : g.replays)
         if (r.exec) (void)hipGraphExecDestroy(r.exec);
     g.replays.clear();
+}
+
+// A change to the graph: every captured call and every plan goes.
+void forget_calls(Graph& g)
+{
+    drop_replays(g);
+    g.plans.clear();
 }
 
 int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs, int32_t n_outputs,
@@ -978,19 +1080,14 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         }
     }
 
-    Prepared P;
-    MFH_TRY(prepare(g, inputs, n_inputs, outputs, n_outputs, false, &P));
-
-    // Streams: ScheduleStreams over the launches (ir/stream_scheduler.go:56).
-    Topology topo = launch_topology(g, P);
-    MFH_TRY(schedule_streams(topo, g.max_streams));
-    int n_streams = 1, n_events = 0;
-    for (const PlanNode& n : topo.nodes) {
-        n_streams = std::max(n_streams, n.stream + 1);
-        for (const mfh_sync_event& e : n.barriers) n_events = std::max(n_events, e.event_id + 1);
-    }
-
-    const int64_t need = lay_out(P, topo);
+    // Launches, streams (ScheduleStreams over the launches,
+    // ir/stream_scheduler.go:56) and placement, planned once per signature.
+    PlannedCall* plan = nullptr;
+    MFH_TRY(plan_call(g, inputs, n_inputs, outputs, n_outputs, &plan));
+    Prepared& P = plan->P;
+    const Topology& topo = plan->topo;
+    const int n_streams = plan->n_streams, n_events = plan->n_events;
+    const int64_t need = plan->need;
     const bool captured = capturing != hipStreamCaptureStatusNone;
     if (need > g.ws_bytes && captured)
         return fail(MFH_ERR_INVALID_ARGUMENT,
@@ -1278,7 +1375,7 @@ int mfh_graph_release(mfh_graph* graph)
 
 int mfh_graph_add_input(mfh_graph* graph, const char* name)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (!graph || !name) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_input: graph and name are required");
     graph->inputs.push_back(name);
     return MFH_OK;
@@ -1286,7 +1383,7 @@ int mfh_graph_add_input(mfh_graph* graph, const char* name)
 
 int mfh_graph_set_output(mfh_graph* graph, const char* key, const char* value)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (!graph || !key || !value)
         return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_output: graph, key and value are required");
     for (auto& kv : graph->outputs)
@@ -1300,7 +1397,7 @@ int mfh_graph_set_output(mfh_graph* graph, const char* key, const char* value)
 
 int mfh_graph_add_node(mfh_graph* graph, const char* id, const char* op, const char* const* inputs, int32_t n_inputs)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (!graph || !id || !op) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_node: graph, id and op are required");
     if (n_inputs < 0 || (n_inputs > 0 && !inputs))
         return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_add_node: bad input list");
@@ -1317,7 +1414,7 @@ int mfh_graph_add_node(mfh_graph* graph, const char* id, const char* op, const c
 
 int mfh_graph_set_attribute(mfh_graph* graph, int32_t node, const char* key, double value)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     GraphNode* n = node_at(graph, node);
     if (!n) return bad_node("mfh_graph_set_attribute", node);
     if (!key) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_attribute: key is NULL");
@@ -1328,7 +1425,7 @@ int mfh_graph_set_attribute(mfh_graph* graph, int32_t node, const char* key, dou
 int mfh_graph_set_types(mfh_graph* graph, int32_t node, const uint8_t* input_types, int32_t n_input_types,
                         uint8_t output_type)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     GraphNode* n = node_at(graph, node);
     if (!n) return bad_node("mfh_graph_set_types", node);
     if (n_input_types < 0 || (n_input_types > 0 && !input_types))
@@ -1342,7 +1439,7 @@ int mfh_graph_set_fusion(mfh_graph* graph, int32_t node, const mfh_ast_node* nod
                          int32_t n_nodes, const char* const* input_ports, int32_t n_input_ports,
                          const char* output_port, uint8_t dtype)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     GraphNode* n = node_at(graph, node);
     if (!n) return bad_node("mfh_graph_set_fusion", node);
     if (!nodes || n_nodes <= 0) return fail(MFH_ERR_INVALID_ARGUMENT, "fusion: root is required");
@@ -1478,21 +1575,21 @@ int32_t mfh_optimizer_elementwise_ops(const char** ops, int32_t cap)
 
 int mfh_optimizer_constant_fold(mfh_graph* graph, int32_t* nodes_folded)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
     return constant_fold(*graph, nodes_folded);
 }
 
 int mfh_optimizer_fuse(mfh_graph* graph, mfh_fusion_stats* stats)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
     return fuse(*graph, stats);
 }
 
 int mfh_optimizer_run(mfh_graph* graph, uint32_t options, int32_t* nodes_folded, mfh_fusion_stats* stats)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "optimizer: graph is required");
     if (nodes_folded) *nodes_folded = 0;
     if (stats) *stats = mfh_fusion_stats{0, 0, 0};
@@ -1504,7 +1601,7 @@ int mfh_optimizer_run(mfh_graph* graph, uint32_t options, int32_t* nodes_folded,
 int mfh_codegen_attach_kernels(mfh_graph* graph, const int32_t* targets, int32_t n_targets, uint32_t flags,
                                int32_t* attached)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (attached) *attached = 0;
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen: graph is required");
     return attach_kernels(*graph, targets, n_targets, flags, attached);
@@ -1547,7 +1644,7 @@ int mfh_graph_call_noalloc(mfh_graph* graph, const mfh_value* inputs, int32_t n_
 
 int mfh_graph_set_max_streams(mfh_graph* graph, int32_t max_streams)
 {
-    if (graph) drop_replays(*graph);
+    if (graph) forget_calls(*graph);
     if (!graph) return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_max_streams: graph is required");
     if (max_streams < 1 || max_streams > 64)
         return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_graph_set_max_streams: %d streams; 1 to 64 are supported", (int)max_streams);

@@ -189,3 +189,37 @@ def test_call_inside_a_caller_capture():
     with pytest.raises(M.MFHError, match="must grow"):
         with torch.cuda.graph(tg2):
             big.call(g, torch.cuda.current_stream().cuda_stream)
+
+
+def test_plans_follow_new_buffers_and_output_aliasing():
+    # With replay off every call runs as plain launches from the plan of its
+    # signature (names, dtypes, counts, which outputs share a buffer): new
+    # buffers of the same shapes reuse the plan with their pointers rebound,
+    # and an output bound twice to one buffer, then to two, is planned apart.
+    torch = torch_mod()
+    rng = np.random.default_rng(27)
+    g = Graph(inputs=["x", "y"], outputs={"e": "e", "e2": "e", "c": "c"}, execution_dtype=F32, nodes=[
+        GraphNode("k", "math.constant", [], attributes={"value": 0.75}),
+        GraphNode("a", "math.mul", ["x", "k"]), GraphNode("b", "math.add", ["a", "y"]),
+        GraphNode("c", "activation.relu", ["b"]), GraphNode("d", "math.neg", ["c"]),
+        GraphNode("e", "math.max", ["d", "x"])])
+    g.set_replay(False)
+    n = (1 << 18) + 3
+    for call in range(6):
+        x = rng.normal(0, 1, n).astype(np.float32)
+        y = rng.normal(0, 1, n).astype(np.float32)
+        tx, ty = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()  # new buffers every call
+        e = torch.full((n,), float("nan"), device="cuda")
+        c = torch.full((n,), float("nan"), device="cuda")
+        shared = call % 3 == 1
+        e2 = e if shared else torch.full((n,), float("nan"), device="cuda")
+        g.call({"x": tx, "y": ty}, {"e": e, "e2": e2, "c": c}, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        want = chain_expected(x, y)
+        for name, t in (("e", e), ("e2", e2), ("c", c)):
+            got = t.cpu().numpy()
+            key = "c" if name == "c" else "e"
+            bad = np.flatnonzero(got.view(np.uint32) != want[key].view(np.uint32))
+            assert bad.size == 0, f"call {call} ({'shared' if shared else 'separate'}) output {name}: {bad.size} bad"
+        log(f"plan reuse call {call}: {'shared' if shared else 'separate'} e/e2 ok")
+    assert g.replayed_calls() == 0
