@@ -611,6 +611,7 @@ struct Slot {
 
 struct Step {
     HIPKernel* kernel = nullptr;
+    const mfh_kernel* resolved = nullptr;  // kernel's variant for `ops`, once looked up
     int node = -1;  // graph node index
     std::vector<int> operands;
     std::vector<mfh_operand> ops;
@@ -871,16 +872,19 @@ int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipSt
     auto on = [&](int32_t id) { return id == 0 ? ls : g.aux[id - 1]; };
     std::vector<const void*> ptrs;
     for (size_t t = 0; t < P.steps.size(); t++) {
-        const Step& st = P.steps[t];
+        Step& st = P.steps[t];
         const PlanNode& pn = topo.nodes[t];
         hipStream_t s = on(pn.stream);
         for (const mfh_sync_event& e : pn.barriers)
             if (e.wait) MFH_TRY(check_hip(hipStreamWaitEvent(s, g.events[e.event_id], 0), "hipStreamWaitEvent(barrier)"));
-        const mfh_kernel* k = nullptr;
-        if (may_load) MFH_TRY(st.kernel->variant(st.ops, &k));
-        else if (!(k = st.kernel->find(st.ops)))
-            return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" has no kernel for these operands yet "
-                        "(make one mfh_graph_call with these values first)", g.nodes[st.node]->id.c_str());
+        const mfh_kernel* k = st.resolved;
+        if (!k) {
+            if (may_load) MFH_TRY(st.kernel->variant(st.ops, &k));
+            else if (!(k = st.kernel->find(st.ops)))
+                return fail(MFH_ERR_INVALID_ARGUMENT, "graph call: node \"%s\" has no kernel for these operands "
+                            "yet (make one mfh_graph_call with these values first)", g.nodes[st.node]->id.c_str());
+            st.resolved = k;  // variants are never dropped while the graph keeps this plan
+        }
         ptrs.clear();
         for (int o : st.operands) ptrs.push_back(addr(slots[o]));
         MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, s, may_load));
