@@ -25,7 +25,7 @@ single-threaded as the Go loops run; "cpu_baseline_all_cores" splits the same
 sample over the host's threads.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-torch] [--only N] [--sets S]
-                [--sweep] [--footprint] [--transient] [--pcie] [--graph-calls] [--profile REPS]
+                [--sweep] [--footprint] [--transient] [--pcie] [--graph-calls] [--rows] [--profile REPS]
 """
 from __future__ import annotations
 
@@ -764,6 +764,116 @@ def graph_calls_run(torch, M):
                 del g
 
 
+class Row(Workload):
+    """One kernel row outside the BASELINE configs, timed the bench's way:
+    a cast, FP8 / Int4 / int8 encode, f64 widening, scalar broadcast,
+    linspace or bf16 axpy over 2^26 elements."""
+    n = 1 << 26
+
+    def __init__(self, torch, M, O, label, in_dt, out_dt, kind="convert"):
+        super().__init__(torch, M, O)
+        self.label, self.in_dt, self.out_dt, self.kind = label, in_dt, out_dt, kind
+        size = {M.FLOAT64: 8, M.FLOAT32: 4, M.FLOAT16: 2, M.BFLOAT16: 2, M.INT32: 4, M.INT8: 1, M.UINT8: 1,
+                M.F8E4M3: 1, M.F8E5M2: 1}
+        self.in_size = size.get(in_dt, 0)
+        out_bytes = self.n // 2 if out_dt == M.INT4 else self.n * size[out_dt]
+        reads = self.n * self.in_size * (2 if kind == "axpy" else 1)
+        self.bytes_per_step = reads + out_bytes
+        self.read_bytes_per_step = reads or self.bytes_per_step  # write-only rows rotate by their writes
+        self.out_bytes = out_bytes
+
+    def make_set(self):
+        t, M = self.torch, self.M
+        g = self.generator()
+        dt = {M.FLOAT64: t.float64, M.FLOAT32: t.float32, M.FLOAT16: t.float16, M.BFLOAT16: t.bfloat16}
+        if self.kind == "linspace":
+            src = None
+        elif self.in_dt in dt:
+            src = (t.randn(self.n, device="cuda", generator=g) * 8).to(dt[self.in_dt])
+        elif self.in_dt == M.INT32:
+            src = t.randint(-(1 << 30), 1 << 30, (self.n,), dtype=t.int32, device="cuda", generator=g)
+        else:
+            src = t.randint(0, 256, (self.n,), dtype=t.uint8, device="cuda", generator=g)
+        other = (t.randn(self.n, device="cuda", generator=g)).to(dt[self.in_dt]) if self.kind == "axpy" else None
+        return src, other, t.empty(self.out_bytes, dtype=t.uint8, device="cuda")
+
+    def launch(self, st):
+        src, other, out = st
+        M, s = self.M, self.stream
+        if self.kind == "convert":
+            M.convert(out.data_ptr(), self.out_dt, src.data_ptr(), self.in_dt, self.n, s)
+        elif self.kind == "broadcast":
+            M.scalar_broadcast(out.data_ptr(), self.out_dt, src.data_ptr(), self.in_dt, self.n, 1.5, "mul", s)
+        elif self.kind == "linspace":
+            M.linspace(out.data_ptr(), self.out_dt, self.n, -1.0, 1.0, True, s)
+        else:  # axpy in 16-bit storage: y = src, x = other (y is rewritten in place)
+            M.axpy(src.data_ptr(), other.data_ptr(), self.n, 0.75, self.in_dt, s)
+
+    def cpu_sample(self):
+        """The oracle's restatement of the row on 2^22 elements."""
+        O, M = self.O, self.M
+        m = 1 << 22
+        rng = np.random.default_rng(7)
+        raw = rng.integers(0, 256, m * max(self.in_size, 1), dtype=np.uint8)
+        if self.in_dt in (M.FLOAT64, M.FLOAT32, M.FLOAT16, M.BFLOAT16):
+            f = (rng.standard_normal(m) * 8).astype(np.float32)
+            raw = {M.FLOAT64: f.astype(np.float64).view(np.uint8), M.FLOAT32: f.view(np.uint8),
+                   M.FLOAT16: O.f32_to_f16(f).view(np.uint8), M.BFLOAT16: O.f32_to_bf16(f).view(np.uint8)}[self.in_dt]
+        out = self.out_dt
+        conv = {M.FLOAT32: lambda b: O.bytes_to_f32(self.in_dt, b), M.BFLOAT16: lambda b: O.bytes_to_bf16(self.in_dt, b),
+                M.FLOAT16: lambda b: O.bytes_to_f16(self.in_dt, b), M.FLOAT64: lambda b: O.bytes_to_f64(self.in_dt, b),
+                M.INT8: lambda b: O.bytes_to_i8(self.in_dt, b),
+                M.INT4: lambda b: O.bytes_to_i4(self.in_dt, b, b.size // max(self.in_size, 1)),
+                M.F8E4M3: lambda b: O.f32_to_fp8(O.bytes_to_f32(self.in_dt, b), M.F8E4M3),
+                M.F8E5M2: lambda b: O.f32_to_fp8(O.bytes_to_f32(self.in_dt, b), M.F8E5M2)}
+        if self.kind == "convert":
+            fn = conv[out]
+            part = lambda lo, hi: fn(raw[lo * self.in_size:hi * self.in_size])  # noqa: E731
+        elif self.kind == "broadcast":
+            f32 = O.bytes_to_f32(self.in_dt, raw)
+            part = lambda lo, hi: O.scalar_broadcast(f32[lo:hi], 1.5, "mul")  # noqa: E731
+        elif self.kind == "linspace":
+            part = lambda lo, hi: O.linspace(-1.0, 1.0, hi - lo, True)  # noqa: E731
+        else:
+            y = raw.view(np.uint16)
+            x = y[::-1].copy()
+            part = lambda lo, hi: O.axpy_storage(y[lo:hi], x[lo:hi], 0.75, self.in_dt)  # noqa: E731
+        return m, 4096, part, f"2^22 elements through the oracle's restatement"
+
+
+def rows_run(torch, M, O, args):
+    """--rows: every kernel row outside the BASELINE configs over 2^26
+    elements, timed the bench's way (inputs rotated past the Infinity Cache),
+    beside the oracle's single-threaded restatement on a 2^22 sample."""
+    rows = [("cast f32 -> bf16", M.FLOAT32, M.BFLOAT16, "convert"), ("cast f32 -> f16", M.FLOAT32, M.FLOAT16, "convert"),
+            ("cast bf16 -> f32", M.BFLOAT16, M.FLOAT32, "convert"), ("cast f16 -> f32", M.FLOAT16, M.FLOAT32, "convert"),
+            ("cast f32 -> f32", M.FLOAT32, M.FLOAT32, "convert"), ("cast f64 -> f32", M.FLOAT64, M.FLOAT32, "convert"),
+            ("cast int32 -> f32", M.INT32, M.FLOAT32, "convert"), ("cast int8 -> f32", M.INT8, M.FLOAT32, "convert"),
+            ("cast uint8 -> bf16", M.UINT8, M.BFLOAT16, "convert"),
+            ("BytesToFloat64 f32 -> f64", M.FLOAT32, M.FLOAT64, "convert"),
+            ("BytesToInt8 f32 -> i8", M.FLOAT32, M.INT8, "convert"),
+            ("Int4 encode int8 -> i4", M.INT8, M.INT4, "convert"), ("Int4 encode f32 -> i4", M.FLOAT32, M.INT4, "convert"),
+            ("FP8 encode f32 -> e4m3", M.FLOAT32, M.F8E4M3, "convert"),
+            ("FP8 encode bf16 -> e4m3", M.BFLOAT16, M.F8E4M3, "convert"),
+            ("FP8 encode f32 -> e5m2", M.FLOAT32, M.F8E5M2, "convert"),
+            ("scalar broadcast f32 * 1.5", M.FLOAT32, M.FLOAT32, "broadcast"),
+            ("linspace f32", 0, M.FLOAT32, "linspace"), ("axpy bf16", M.BFLOAT16, M.BFLOAT16, "axpy")]
+    for label, in_dt, out_dt, kind in rows:
+        w = Row(torch, M, O, label, in_dt, out_dt, kind)
+        if kind == "axpy":  # in place: y is read and written, x read
+            w.out_bytes = 0
+            w.bytes_per_step = 3 * w.n * 2
+        w.setup()
+        ms, _, _ = time_gpu(w, args.steps, args.warmup)
+        gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
+        cpu = time_cpu(w, budget_s=1.0)
+        print(json.dumps({"row": label, "elements": w.n, "bytes_per_step": w.bytes_per_step, "us_per_step":
+                          round(ms * 1e3, 2), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+                          "rotated_sets": len(w.sets), "cpu_GB_s": cpu["value"]}), flush=True)
+        del w
+        torch.cuda.empty_cache()
+
+
 def footprint_run(torch, M, O, steps, warmup, only=0):
     """--footprint: each BASELINE kernel over 1 to 32 rotated buffer sets,
     timed as the bench times a step.  One JSON line per kernel and rotation:
@@ -818,6 +928,7 @@ def main():
                     help="rotate exactly this many buffer sets (default: >= 1 GiB of distinct inputs per cycle)")
     ap.add_argument("--pcie", action="store_true", help="host-buffer upload / download / SafeTensors rates")
     ap.add_argument("--graph-calls", action="store_true", help="mfh_graph_call time per call, streams and replay")
+    ap.add_argument("--rows", action="store_true", help="every kernel outside the BASELINE configs (casts, encodes, ...)")
     ap.add_argument("--transient", action="store_true",
                     help="each kernel (and two variants of the gelu chain) from an idle GPU, for a kernel trace")
     ap.add_argument("--footprint", action="store_true",
@@ -852,6 +963,9 @@ def main():
         return
     if args.graph_calls:
         graph_calls_run(torch, M)
+        return
+    if args.rows:
+        rows_run(torch, M, O, args)
         return
     if args.sweep:
         sweep_run(torch, M, O, args.steps, args.warmup)

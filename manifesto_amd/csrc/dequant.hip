@@ -659,8 +659,88 @@ __global__ __launch_bounds__(kBlock) void k_encode_int4(const void* __restrict__
     }
 }
 
+// Unpacked numeric sources, laid out as k_encode_byte_wave: a wave takes 4 KiB
+// of source, lane l its 16-byte pieces l, l + 64, l + 128 and l + 192, so
+// every load instruction reads 1 KiB contiguously; the 16 / size elements of
+// a piece leave as 8 / size bytes of nibbles next to the neighbours' ones.
+// Elements past the last whole chunk run the byte loop.
+template <int IN, int BS>
+__global__ __launch_bounds__(BS) void k_encode_int4_wave(const void* __restrict__ in, mfh_u8* __restrict__ out,
+                                                             mfh_i64 n)
+{
+    constexpr int S = size_of<IN>();
+    constexpr int P = 16 / S;  // elements per 16-byte piece
+    constexpr int kPieces = 4;
+    constexpr mfh_i64 kChunk = 64 * kPieces * P;
+    const int lane = (int)threadIdx.x & 63;
+    const mfh_i64 waves = (mfh_i64)gridDim.x * (BS / 64);
+    const mfh_i64 nchunks = n / kChunk;
+    for (mfh_i64 c = (mfh_i64)blockIdx.x * (BS / 64) + (threadIdx.x >> 6); c < nchunks; c += waves) {
+        u32x4 x[kPieces];
+#pragma unroll
+        for (int q = 0; q < kPieces; q++) x[q] = load_nt(reinterpret_cast<const u32x4*>(in) + c * (64 * kPieces) + q * 64 + lane);
+#pragma unroll
+        for (int q = 0; q < kPieces; q++) {
+            const mfh_u32 w[4] = {x[q][0], x[q][1], x[q][2], x[q][3]};
+            mfh_u32 code[2] = {0u, 0u};
+#pragma unroll
+            for (int k = 0; k < P; k++) {
+                const int v = (int)(signed char)byte_reg<IN, kInt8>(w, k);
+                code[k >> 3] |= ((mfh_u32)(v < -8 ? -8 : (v > 7 ? 7 : v)) & 0xfu) << (4 * (k & 7));
+            }
+            mfh_u8* o = out + (c * kChunk + (mfh_i64)(q * 64 + lane) * P) / 2;
+            if constexpr (P == 16) store_nt(reinterpret_cast<u32x2*>(o), u32x2{code[0], code[1]});
+            else if constexpr (P == 8) store_nt(reinterpret_cast<mfh_u32*>(o), code[0]);
+            else if constexpr (P == 4) store_nt(reinterpret_cast<mfh_u16*>(o), (mfh_u16)code[0]);
+            else *o = (mfh_u8)code[0];
+        }
+    }
+    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    const mfh_i64 nbytes = (n + 1) / 2;
+    for (mfh_i64 b = nchunks * kChunk / 2 + (mfh_i64)blockIdx.x * BS + threadIdx.x; b < nbytes; b += stride) {
+        const mfh_u32 lo = nibble_at<IN>(in, 2 * b);
+        const mfh_u32 hi = 2 * b + 1 < n ? nibble_at<IN>(in, 2 * b + 1) : 0u;
+        out[b] = (mfh_u8)(lo | (hi << 4));
+    }
+}
+
+template <int BS>
+int launch_encode_int4_wave(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, int size,
+                            hipStream_t stream)
+{
+    const int64_t chunk_elems = 64 * 4 * (16 / size);
+    const unsigned grid = grid_for(std::max<int64_t>(n / chunk_elems, 1) * 64, dev, Kern::kConvert, 1, BS);
+    switch (in_dt) {
+#define MFH_ENCODE_I4_WAVE_CASE(DT) \
+    case DT: k_encode_int4_wave<DT, BS><<<grid, BS, 0, stream>>>(in, out, n); break;
+        MFH_ENCODE_I4_WAVE_CASE(kFloat64)
+        MFH_ENCODE_I4_WAVE_CASE(kFloat32)
+        MFH_ENCODE_I4_WAVE_CASE(kFloat16)
+        MFH_ENCODE_I4_WAVE_CASE(kBFloat16)
+        MFH_ENCODE_I4_WAVE_CASE(kInt64)
+        MFH_ENCODE_I4_WAVE_CASE(kInt32)
+        MFH_ENCODE_I4_WAVE_CASE(kInt16)
+        MFH_ENCODE_I4_WAVE_CASE(kInt8)
+        MFH_ENCODE_I4_WAVE_CASE(kUint64)
+        MFH_ENCODE_I4_WAVE_CASE(kUint32)
+        MFH_ENCODE_I4_WAVE_CASE(kUint16)
+        MFH_ENCODE_I4_WAVE_CASE(kUint8)
+#undef MFH_ENCODE_I4_WAVE_CASE
+    default:
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
+    }
+    return launch_status("k_encode_int4_wave");
+}
+
 int launch_encode_int4(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, hipStream_t stream)
 {
+    // unpacked numeric sources aligned to 16 bytes, the output aligned to one
+    // piece's bytes of nibbles (8 / size), take the wave layout
+    const int size = in_dt == kF8E4M3 || in_dt == kF8E5M2 || in_dt == kInt4 ? 0 : dtype_size(in_dt);
+    if (size > 0 && aligned16(in) && (reinterpret_cast<uintptr_t>(out) & (uintptr_t)(std::max(1, 8 / size) - 1)) == 0)
+        return with_block(cast_threads(in_dt, 1), [&](auto block) {
+            return launch_encode_int4_wave<decltype(block)::value>(dev, out, in, in_dt, n, size, stream);
+        });
     const int vec_ok = aligned16(out) && n >= 32;
     const int64_t items = vec_ok ? n / 32 : (n + 1) / 2;
     const unsigned grid = grid_for(items, dev, Kern::kConvert);

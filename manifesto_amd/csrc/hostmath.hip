@@ -168,16 +168,130 @@ __global__ __launch_bounds__(kBlock) void k_linspace(void* __restrict__ out, mfh
     }
 }
 
+template <int OP>
+MFH_DEV float apply(float v, float s)
+{
+    if constexpr (OP == 0) return v + s;
+    else if constexpr (OP == 1) return v - s;
+    else if constexpr (OP == 2) return v * s;
+    else return v / s;
+}
+
+// E consecutive elements of a 16-byte-aligned item row as f32: E = 4 or 8.
+template <int DT, int E, bool NT>
+MFH_DEV void load_item(const void* p, mfh_i64 item, float (&v)[E])
+{
+    auto ld = [](const auto* q) { return NT ? load_nt(q) : *q; };
+    if constexpr (DT == kFloat32) {
+        const u32x4* q = reinterpret_cast<const u32x4*>(p) + item * (E / 4);
+#pragma unroll
+        for (int h = 0; h < E / 4; h++) {
+            const u32x4 w = ld(q + h);
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[4 * h + k] = mfh_f32(w[k]);
+        }
+    } else if constexpr (E == 4) {
+        const u32x2 w = ld(reinterpret_cast<const u32x2*>(p) + item);
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = dec16<DT>((w[k >> 1] >> (16 * (k & 1))) & 0xffffu);
+    } else {
+        const u32x4 w = ld(reinterpret_cast<const u32x4*>(p) + item);
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = dec16<DT>((w[k >> 1] >> (16 * (k & 1))) & 0xffffu);
+    }
+}
+
+// The 16-byte output item of E elements (4 f32, or 8 bf16/f16 with RNE).
+template <int DT, int E>
+MFH_DEV u32x4 pack_item(const float (&v)[E])
+{
+    if constexpr (DT == kFloat32) return u32x4{mfh_bits(v[0]), mfh_bits(v[1]), mfh_bits(v[2]), mfh_bits(v[3])};
+    else return u32x4{enc16x2<DT>(v[0], v[1]), enc16x2<DT>(v[2], v[3]), enc16x2<DT>(v[4], v[5]),
+                      enc16x2<DT>(v[6], v[7])};
+}
+
+// Vector forms: one 16-byte output item per thread (4 f32 or 8 16-bit
+// elements), one-shot grid, streaming stores; loads non-temporal when the
+// input is at least as wide as the output.  The element kernels above keep
+// misaligned buffers and the tails.  The element form stored 2 or 4 bytes
+// per lane: 3.6 TB/s for an f32 broadcast and 4.5 for an f32 linspace.
+template <int IN, int OUT, int OP>
+__global__ __launch_bounds__(kBlock) void k_scalar_broadcast_vec(void* __restrict__ out, const void* __restrict__ in,
+                                                                 mfh_i64 n, float s)
+{
+    constexpr int E = OUT == kFloat32 ? 4 : 8;
+    constexpr bool kNt = (IN == kFloat32) || (OUT != kFloat32);
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 nitems = n / E;
+    for (mfh_i64 it = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; it < nitems; it += stride) {
+        float v[E];
+        load_item<IN, E, kNt>(in, it, v);
+#pragma unroll
+        for (int k = 0; k < E; k++) v[k] = apply<OP>(v[k], s);
+        store_nt(reinterpret_cast<u32x4*>(out) + it, pack_item<OUT, E>(v));
+    }
+    for (mfh_i64 i = nitems * E + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        store_f<OUT>(out, i, apply<OP>(load_f<IN>(in, i), s));
+}
+
+template <int OUT>
+__global__ __launch_bounds__(kBlock) void k_linspace_vec(void* __restrict__ out, mfh_i64 n, float start, float stop,
+                                                         float step, int pin_first, int pin_last)
+{
+    constexpr int E = OUT == kFloat32 ? 4 : 8;
+    const mfh_i64 stride = (mfh_i64)gridDim.x * kBlock;
+    const mfh_i64 nitems = n / E;
+    auto at = [&](mfh_i64 i) {
+        float v = start + (float)i * step;
+        if (pin_first && i == 0) v = start;
+        if (pin_last && i == n - 1) v = stop;
+        return v;
+    };
+    for (mfh_i64 it = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; it < nitems; it += stride) {
+        float v[E];
+#pragma unroll
+        for (int k = 0; k < E; k++) v[k] = at(it * E + k);
+        store_nt(reinterpret_cast<u32x4*>(out) + it, pack_item<OUT, E>(v));
+    }
+    for (mfh_i64 i = nitems * E + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        store_f<OUT>(out, i, at(i));
+}
+
 int check_float_dtype(int dt, const char* what)
 {
     if (dt == kFloat32 || dt == kBFloat16 || dt == kFloat16) return MFH_OK;
     return fail(MFH_ERR_DTYPE_UNSUPPORTED, "%s: dtype %s is not f32/bf16/f16", what, dtype_name(dt));
 }
 
+template <int IN, int OUT>
+void launch_broadcast_vec(unsigned grid, hipStream_t s, void* out, const void* in, int64_t n, float scalar, int op)
+{
+    switch (op) {
+    case 0: k_scalar_broadcast_vec<IN, OUT, 0><<<grid, kBlock, 0, s>>>(out, in, n, scalar); break;
+    case 1: k_scalar_broadcast_vec<IN, OUT, 1><<<grid, kBlock, 0, s>>>(out, in, n, scalar); break;
+    case 2: k_scalar_broadcast_vec<IN, OUT, 2><<<grid, kBlock, 0, s>>>(out, in, n, scalar); break;
+    default: k_scalar_broadcast_vec<IN, OUT, 3><<<grid, kBlock, 0, s>>>(out, in, n, scalar); break;
+    }
+}
+
 template <int IN>
-int launch_broadcast(int out_dt, unsigned grid, hipStream_t s, void* out, const void* in, int64_t n,
+int launch_broadcast(int out_dt, const Device* dev, hipStream_t s, void* out, const void* in, int64_t n,
                      float scalar, int op)
 {
+    // vector items need the output 16-byte aligned and the input aligned to
+    // the item's bytes (16 for f32 sources, 8 or 16 for 16-bit ones)
+    const int e = out_dt == kFloat32 ? 4 : 8;
+    const uintptr_t in_align = IN == kFloat32 ? 16 : (uintptr_t)e * 2;
+    if (n >= e && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (reinterpret_cast<uintptr_t>(in) & (in_align - 1)) == 0) {
+        const unsigned grid = grid_for(n / e, dev, Kern::kConvert);
+        switch (out_dt) {
+        case kFloat32: launch_broadcast_vec<IN, kFloat32>(grid, s, out, in, n, scalar, op); break;
+        case kBFloat16: launch_broadcast_vec<IN, kBFloat16>(grid, s, out, in, n, scalar, op); break;
+        default: launch_broadcast_vec<IN, kFloat16>(grid, s, out, in, n, scalar, op); break;
+        }
+        return launch_status("k_scalar_broadcast_vec");
+    }
+    const unsigned grid = grid_for(n, dev, Kern::kConvert);
     switch (out_dt) {
     case kFloat32: k_scalar_broadcast<IN, kFloat32><<<grid, kBlock, 0, s>>>(out, in, n, scalar, op); break;
     case kBFloat16: k_scalar_broadcast<IN, kBFloat16><<<grid, kBlock, 0, s>>>(out, in, n, scalar, op); break;
@@ -263,12 +377,11 @@ int mfh_scalar_broadcast(void* out, uint8_t out_dtype, const void* in, uint8_t i
     if (count < 0) return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: negative count");
     if (count == 0) return MFH_OK;
     if (!out || !in) return fail(MFH_ERR_INVALID_ARGUMENT, "math.scalar_broadcast: NULL buffer");
-    unsigned grid = grid_for(count, dev, Kern::kConvert);
     hipStream_t s = (hipStream_t)stream;
     switch (in_dtype) {
-    case kFloat32: return launch_broadcast<kFloat32>(out_dtype, grid, s, out, in, count, scalar, op);
-    case kBFloat16: return launch_broadcast<kBFloat16>(out_dtype, grid, s, out, in, count, scalar, op);
-    default: return launch_broadcast<kFloat16>(out_dtype, grid, s, out, in, count, scalar, op);
+    case kFloat32: return launch_broadcast<kFloat32>(out_dtype, dev, s, out, in, count, scalar, op);
+    case kBFloat16: return launch_broadcast<kBFloat16>(out_dtype, dev, s, out, in, count, scalar, op);
+    default: return launch_broadcast<kFloat16>(out_dtype, dev, s, out, in, count, scalar, op);
     }
 }
 
@@ -286,8 +399,18 @@ int mfh_linspace(void* out, uint8_t out_dtype, int64_t count, float start, float
     // count == 1 returns start itself; with the endpoint both ends are pinned.
     int pin_first = (count == 1 || endpoint) ? 1 : 0;
     int pin_last = (count > 1 && endpoint) ? 1 : 0;
-    unsigned grid = grid_for(count, dev, Kern::kConvert);
     hipStream_t s = (hipStream_t)stream;
+    const int e = out_dtype == kFloat32 ? 4 : 8;
+    if (count >= e && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+        const unsigned grid = grid_for(count / e, dev, Kern::kConvert);
+        switch (out_dtype) {
+        case kFloat32: k_linspace_vec<kFloat32><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;
+        case kBFloat16: k_linspace_vec<kBFloat16><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;
+        default: k_linspace_vec<kFloat16><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;
+        }
+        return launch_status("k_linspace_vec");
+    }
+    unsigned grid = grid_for(count, dev, Kern::kConvert);
     switch (out_dtype) {
     case kFloat32: k_linspace<kFloat32><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;
     case kBFloat16: k_linspace<kBFloat16><<<grid, kBlock, 0, s>>>(out, count, start, stop, step, pin_first, pin_last); break;

@@ -111,17 +111,25 @@ def test_linspace_scalar_broadcast_golden(golden):
         assert t[i] == v
 
 
+FLOATS = [O.FLOAT32, O.BFLOAT16, O.FLOAT16]
+
+
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
-@pytest.mark.parametrize("in_dt, out_dt", [(O.FLOAT32, O.FLOAT32), (O.BFLOAT16, O.FLOAT32),
-                                           (O.FLOAT16, O.BFLOAT16)])
-def test_scalar_broadcast_vs_oracle(op, in_dt, out_dt):
-    rng = np.random.default_rng(5)
-    src = O.encode(rng.normal(0, 10, 10007).astype(np.float32), in_dt)
-    st, sp = to_dev(src)
+@pytest.mark.parametrize("in_dt", FLOATS)
+@pytest.mark.parametrize("out_dt", FLOATS)
+@pytest.mark.parametrize("n, pad_in, pad_out", [(10007, 0, 0), (8, 0, 0), (3, 0, 0), (4099, 2, 0), (4099, 0, 4),
+                                                (4104, 8, 0)])
+def test_scalar_broadcast_vs_oracle(op, in_dt, out_dt, n, pad_in, pad_out):
+    # 16-byte output items where the buffers allow (an f32 source aligned to
+    # 16 bytes, a 16-bit one to the item's 8 or 16), the element loop
+    # otherwise and for the tail
+    rng = np.random.default_rng(5 + n + pad_in)
+    src = O.encode(rng.normal(0, 10, n).astype(np.float32), in_dt)
+    st, sp = to_dev(src, pad=pad_in)
     size = 4 if out_dt == O.FLOAT32 else 2
-    ot, opp = empty_dev(src.size * size)
+    ot, opp = empty_dev(src.size * size, pad=pad_out)
     M.scalar_broadcast(opp, out_dt, sp, in_dt, src.size, 0.37, op, stream())
-    got = to_host(ot, np.float32 if out_dt == O.FLOAT32 else np.uint16)
+    got = to_host(ot, np.float32 if out_dt == O.FLOAT32 else np.uint16, pad=pad_out)
     want = O.encode(O.scalar_broadcast(O.decode(src, in_dt), 0.37, op), out_dt)
     assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
 
@@ -144,3 +152,14 @@ def test_linspace_vs_oracle(count, endpoint):
     got = to_host(ot, np.float32)
     want = O.linspace(-0.0, 7.25, count, endpoint)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("dt", FLOATS)
+@pytest.mark.parametrize("count, pad", [(9, 0), (100003, 0), (100003, 2), (16, 4)])
+def test_linspace_every_dtype_and_alignment(dt, count, pad):
+    size = 4 if dt == O.FLOAT32 else 2
+    ot, opp = empty_dev(count * size, pad=pad)
+    M.linspace(opp, dt, count, -3.5, 11.0, True, stream())
+    got = to_host(ot, np.float32 if dt == O.FLOAT32 else np.uint16, pad=pad)
+    want = O.encode(O.linspace(-3.5, 11.0, count, True), dt)
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
