@@ -170,7 +170,13 @@ typedef struct {
  * node's OutputType, else the graph's ExecutionDType, else Float32.
  * Intermediates live in one device workspace per graph, laid out by value
  * lifetime and kept across calls.  Every bound output receives its value; an
- * output with no binding is computed and dropped.  Calls on one graph must
+ * output with no binding is computed and dropped.  An output may share its
+ * buffer with an input (an update in place): it is written in place when the
+ * input is the same buffer with the same element size and count and only
+ * the launch that computes the output reads that input; otherwise it is
+ * computed in the workspace and copied out after the last launch, so every
+ * launch reads the input as it was.  Outputs of different values must not
+ * share or overlap buffers.  Calls on one graph must
  * not overlap in host threads (they share its workspace, streams and replay
  * cache); different graphs may be called from different threads.  Work
  * queued on different caller streams is ordered by the graph itself. */

@@ -1,7 +1,10 @@
 """Builds manifesto_amd/libmfh.so for gfx950 with hipcc.
 
 Every source is compiled with -ffp-contract=off (the reference's Go code never
-contracts a*b+c) and with packed-FP32 instructions disabled.  The JIT prelude
+contracts a*b+c) and with packed-FP32 instructions disabled.  Kernel arguments
+are preloaded into SGPRs (gfx950 firmware loads them at wave launch; the code
+object keeps a prologue that loads them itself for firmware that does not),
+which takes a scalar load off the start of every wave.  The JIT prelude
 (codec.hpp + devmath.hpp + fusion_io.hpp) is embedded into the library as a
 string so that generated kernels see exactly the code the ahead-of-time
 kernels use.
@@ -31,6 +34,7 @@ COMMON_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I", BUILD, "-I", os.path.join(os.path.dirname(HERE), "include"),
 ]
 

@@ -208,7 +208,7 @@ int compile_source(const std::string& source, const std::string& kernel_name, st
         return fail(MFH_ERR_COMPILE, "codegen hip: hiprtcCreateProgram failed");
     const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
                           "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature",
-                          "-Xclang", "-packed-fp32-ops"};
+                          "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-kernarg-preload-count=16"};
     hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
     if (rc != HIPRTC_SUCCESS) {
         size_t log_size = 0;

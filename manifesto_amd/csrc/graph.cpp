@@ -795,6 +795,35 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
         slots.push_back(out);
         P->steps.push_back(std::move(st));
     }
+    // An output buffer that overlaps an input's is written in place only
+    // where nothing can read a changed input: the input is the same buffer
+    // with the same element size and count, and its one reader is the
+    // launch that writes the output, element for element.  Otherwise the
+    // output goes through the workspace and is copied out after every
+    // launch.
+    std::set<int> passed_through;  // input slots copied straight to an output
+    for (const auto& kv : bound) {
+        auto it = named.find(kv.first);
+        if (it != named.end() && slots[it->second].kind == Slot::kInput) passed_through.insert(it->second);
+    }
+    for (Slot& s : slots) {
+        if (s.kind != Slot::kBound) continue;
+        const uintptr_t lo = (uintptr_t)s.ptr, hi = lo + (uintptr_t)s.count * dtype_size(s.dtype);
+        for (int j = 0; j < n_inputs; j++) {
+            const Slot& in = slots[j];  // inputs come first
+            const uintptr_t l = (uintptr_t)in.ptr, h = l + (uintptr_t)in.count * dtype_size(in.dtype);
+            if (!in.ptr || in.count <= 0 || h <= lo || hi <= l) continue;
+            const bool same = in.ptr == s.ptr && dtype_size(in.dtype) == dtype_size(s.dtype) && in.count == s.count &&
+                              !passed_through.count(j) &&
+                              std::all_of(in.readers.begin(), in.readers.end(), [&](int r) { return r == s.producer; });
+            if (!same) {
+                s.kind = Slot::kArena;
+                s.ptr = nullptr;
+                s.out_index = -1;
+                break;
+            }
+        }
+    }
     // Bound outputs not written in place are copied at the end.
     for (const auto& kv : bound) {
         auto it = named.find(kv.first);
@@ -813,6 +842,10 @@ int prepare(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value
         s.pinned = true;
         P->copies.push_back(Copy{it->second, b, (int)(b - outputs)});
     }
+    // inputs passed straight through are copied before anything else is
+    // written into an output buffer
+    std::stable_partition(P->copies.begin(), P->copies.end(),
+                          [&](const Copy& c) { return slots[c.slot].kind == Slot::kInput; });
     return MFH_OK;
 }
 
@@ -962,8 +995,9 @@ struct PlannedCall {
 
 // What a call's plan depends on besides the graph: value names, dtypes and
 // counts, which bindings have data, which output bindings share a buffer,
-// the stream budget.  Not the pointers: a call on new buffers of the same
-// shapes reuses the plan with its pointers rebound.
+// which inputs each output's buffer overlaps, the stream budget.  Not the
+// pointers: a call on new buffers of the same shapes reuses the plan with
+// its pointers rebound.
 std::string plan_key(const Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
                      int32_t n_outputs)
 {
@@ -984,9 +1018,21 @@ std::string plan_key(const Graph& g, const mfh_value* inputs, int32_t n_inputs, 
                 break;
             }
         key += outputs[i].name ? outputs[i].name : "";
-        snprintf(buf, sizeof buf, "|%u|%lld|%d|%d;", (unsigned)outputs[i].dtype, (long long)outputs[i].count,
+        snprintf(buf, sizeof buf, "|%u|%lld|%d|%d", (unsigned)outputs[i].dtype, (long long)outputs[i].count,
                  outputs[i].data != nullptr, alias);
         key += buf;
+        // the inputs whose buffers it overlaps, and whether exactly
+        const mfh_value& o = outputs[i];
+        const uintptr_t lo = (uintptr_t)o.data, hi = lo + (uintptr_t)std::max<int64_t>(0, o.count) * dtype_size(o.dtype);
+        for (int32_t j = 0; j < n_inputs; j++) {
+            const mfh_value& v = inputs[j];
+            const uintptr_t l = (uintptr_t)v.data, h = l + (uintptr_t)std::max<int64_t>(0, v.count) * dtype_size(v.dtype);
+            if (!o.data || !v.data || h <= lo || hi <= l) continue;
+            const bool same = v.data == o.data && v.count == o.count && dtype_size(v.dtype) == dtype_size(o.dtype);
+            snprintf(buf, sizeof buf, "/%d%c", (int)j, same ? '=' : '~');
+            key += buf;
+        }
+        key += ";";
     }
     snprintf(buf, sizeof buf, "s=%d", (int)g.max_streams);
     return key + buf;

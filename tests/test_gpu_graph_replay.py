@@ -223,3 +223,82 @@ def test_plans_follow_new_buffers_and_output_aliasing():
             assert bad.size == 0, f"call {call} ({'shared' if shared else 'separate'}) output {name}: {bad.size} bad"
         log(f"plan reuse call {call}: {'shared' if shared else 'separate'} e/e2 ok")
     assert g.replayed_calls() == 0
+
+
+def test_outputs_bound_over_inputs():
+    # An output may be bound to an input's buffer.  It is written in place
+    # only where the launch computing it is that input's one reader, element
+    # for element; otherwise it is computed in the workspace and copied out
+    # after the last launch, so that every launch reads the input as it was.
+    torch = torch_mod()
+    rng = np.random.default_rng(28)
+    n = (1 << 16) + 7
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def fresh():
+        return rng.normal(0, 1, n).astype(np.float32), rng.normal(0, 1, n).astype(np.float32)
+
+    def same(got, want, what):
+        got = got.cpu().numpy()
+        bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+        assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[:4]}"
+
+    # unfused chain with c bound over x: x is read by the first launch and
+    # the last; four calls on the same buffers (launch, capture, 2 replays)
+    g = chain_graph(fuse=False)
+    tx, ty = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
+    e = torch.empty(n, device="cuda")
+    for call in range(4):
+        x, y = fresh()
+        tx.copy_(torch.from_numpy(x))
+        ty.copy_(torch.from_numpy(y))
+        e.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.call({"x": tx, "y": ty}, {"e": e, "c": tx}, stream())
+        torch.cuda.synchronize()
+        want = chain_expected(x, y)
+        same(e, want["e"], f"chain call {call}: e")
+        same(tx, want["c"], f"chain call {call}: c over x")
+        log(f"in-place chain call {call} ok")
+    assert g.replayed_calls() == 2
+
+    # one fused launch reading x and y element for element: written in place
+    k = np.float32(0.75)
+    g = Graph(inputs=["x", "y"], outputs={"s": "s"}, execution_dtype=F32, nodes=[
+        GraphNode("k", "math.constant", [], attributes={"value": 0.75}),
+        GraphNode("a", "math.mul", ["x", "k"]), GraphNode("s", "math.add", ["a", "y"])])
+    G.run(g)
+    G.attach_kernels(g)
+    g.set_replay(False)
+    for call, target in enumerate(["x", "y", None, "x"]):
+        x, y = fresh()
+        tx, ty = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+        out = {"x": tx, "y": ty, None: torch.full((n,), float("nan"), device="cuda")}[target]
+        g.call({"x": tx, "y": ty}, {"s": out}, stream())
+        torch.cuda.synchronize()
+        same(out, x * k + y, f"fused call {call} (s over {target})")
+        if target:
+            assert g.workspace_bytes() < 4 * n, "written in place: no room for s in the workspace"
+        log(f"in-place fused call {call} over {target} ok")
+
+    # s bound one element into x's buffer: computed aside, copied out
+    store = torch.empty(n + 1, device="cuda")
+    x, y = fresh()
+    store[:n].copy_(torch.from_numpy(x))
+    ty = torch.from_numpy(y).cuda()
+    g.call({"x": store[:n], "y": ty}, {"s": store[1:]}, stream())
+    torch.cuda.synchronize()
+    same(store[1:], x * k + y, "s overlapping x by all but one element")
+    assert g.workspace_bytes() >= 4 * n
+
+    # x passed straight through to xc while s is bound over x: xc gets x as
+    # it was
+    g = Graph(inputs=["x", "y"], outputs={"s": "s", "xc": "x"}, execution_dtype=F32, nodes=[
+        GraphNode("s", "math.add", ["x", "y"])])
+    x, y = fresh()
+    tx, ty = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+    xc = torch.full((n,), float("nan"), device="cuda")
+    g.call({"x": tx, "y": ty}, {"s": tx, "xc": xc}, stream())
+    torch.cuda.synchronize()
+    same(xc, x, "x passed through")
+    same(tx, x + y, "s over x")
