@@ -6,6 +6,7 @@
 // Each function reproduces the bit rules of manifesto's Go codecs:
 //   F8E4M3.Float32   dtype/fp8.go:39-70
 //   F8E5M2.Float32   dtype/fp8.go:149-183
+//   NewF8E4M3FromFloat32 / NewF8E5M2FromFloat32  dtype/fp8.go:77-136,190-249
 //   NewBfloat16FromFloat32  dtype/bfloat16.go:41-55
 //   f16bitsToF32bits / f32bitsToF16bits  dtype/float16.go:222-315
 //   int4 nibbles     dtype/convert/decoders.go:262-289
@@ -14,6 +15,8 @@
 // the Go rules bit for bit on every input, NaN payloads and denormals
 // included (checked over all 2^32 f32 and all 2^16 f16 inputs on MI355X;
 // tests/test_gpu_dequant.py keeps that check), so no fix-up code is needed.
+// FP8 encode runs through v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 between an
+// input map and a NaN fix-up that make its codes the reference's.
 #ifndef MFH_CODEC_HPP
 #define MFH_CODEC_HPP
 
@@ -81,42 +84,84 @@ MFH_DEV mfh_u32 mfh_e5m2_bits(mfh_u32 code)
 //     rounded; a result that reaches the hidden-bit position becomes the
 //     smallest normal (so E4M3 [2^-7, 2^-6) all give 0x08); biased e below
 //     -3 (E4M3) / -1 (E5M2) gives signed zero.
-// MB = mantissa bits, BIAS = exponent bias, EMAX = top exponent field value,
-// SAT = saturation code, MAXF = bits of the largest finite value.
-template <int MB, int BIAS, int EMAX, int MINSUB, mfh_u32 SAT, mfh_u32 MAXF>
-MFH_DEV mfh_u32 mfh_fp8_encode(float value)
+//
+// gfx950's v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32 encode two f32 values into
+// OCP E4M3 / E5M2 with round-to-nearest-even.  Outside NaN they give the
+// reference's code for every input once the input is first moved to a value
+// whose hardware code is the reference's (mfh_fp8_prep; checked over all
+// 2^32 f32 inputs on MI355X, and tests/test_gpu_encode.py keeps the check):
+//   * |x| below 2^-10 (E4M3) / 2^-16 (E5M2) -> 0: there the reference's
+//     shifted mantissa rounds to zero, where the hardware would round the top
+//     of the range up to the smallest subnormal;
+//   * |x| below the smallest normal 2^-6 / 2^-14 -> min(2|x|, smallest
+//     normal): the reference's subnormal shift is one bit short, so its code
+//     for |x| is the IEEE code of 2|x|, and whatever reaches the normal range
+//     stops at the smallest normal's code 0x08 / 0x04;
+//   * |x| >= 248 (E4M3: what rounds into the top binade) or > 57344 (E5M2),
+//     Inf included -> 448 / Inf, whose codes are the saturation codes
+//     0x7e / 0x7c;
+//   * the sign is put back; NaN passes through.
+// The hardware writes every NaN as 0xff (E4M3) / 0xfe (E5M2), bytes that no
+// other input gives, and mfh_fp8_nan_fix turns them into 0x7f.
+template <bool E5>
+MFH_DEV float mfh_fp8_prep(float v)
 {
-    // The same cases, computed for every element without a branch (the
-    // per-case branches of a direct transcription diverge within a wave):
-    constexpr mfh_u32 drop = 23 - MB;                  // 20 (E4M3) or 21 (E5M2)
-    constexpr mfh_u32 kNormal = (128u - BIAS) << 23;   // |x| from here on has biased e >= 1
-    const mfh_u32 u = mfh_bits(value);
+    constexpr mfh_u32 kZero = E5 ? 0x37800000u : 0x3a800000u;  // 2^-16 / 2^-10
+    constexpr mfh_u32 kMinN = E5 ? 0x38800000u : 0x3c800000u;  // 2^-14 / 2^-6
+    constexpr float kSatAt = E5 ? 57344.0f : 248.0f;
+    constexpr mfh_u32 kSatTo = E5 ? 0x7f800000u : 0x43e00000u;  // Inf / 448
+    const mfh_u32 u = mfh_bits(v);
     const mfh_u32 a = u & 0x7fffffffu;
-    // e >= 1: the exponent and top MB mantissa bits rounded to nearest even
-    // by one integer add; a carry out of the mantissa bumps the exponent,
-    // which is the reference's "m >= 1 << MB: m = 0, e++" step
-    const mfh_u32 r = a + ((1u << (drop - 1u)) - 1u) + ((a >> drop) & 1u);
-    const mfh_u32 normal = (r >> drop) - ((127u - BIAS) << MB);
-    // e <= 0: the hidden-bit mantissa shifted right by drop - e and rounded
-    // to nearest even is |x| * 2^(BIAS + MB) rounded to an integer (exact
-    // scaling, then the 2^23 round-to-integer add); below biased e = MINSUB
-    // zero; a result reaching 1 << MB stays there
-    constexpr float kScale = (float)(1u << (BIAS + MB));
-    constexpr float kZeroBelow = MINSUB + MB >= 0 ? (float)(1u << (MINSUB + MB >= 0 ? MINSUB + MB : 0))
-                                                  : 1.0f / (float)(1u << (MINSUB + MB < 0 ? -(MINSUB + MB) : 0));
-    const float y = mfh_f32(a) * kScale;
-    const mfh_u32 t = mfh_bits((y < kZeroBelow ? 0.0f : y) + 8388608.0f) - 0x4b000000u;
-    const mfh_u32 sub = t < (1u << MB) ? t : (1u << MB);
-    mfh_u32 code = a < kNormal ? sub : normal;
-    // above the largest finite value, Inf, and a rounded biased exponent at
-    // the top field value saturate
-    code = (a > MAXF || r >= ((mfh_u32)(EMAX + 127 - BIAS) << 23)) ? SAT : code;
-    code |= (u >> 24) & 0x80u;
-    return a > 0x7f800000u ? 0x7fu : code;             // NaN, whatever its sign
+    // 2|x| is a + 1 << 23 for the normal |x| that get here; the median of
+    // a, 2a and the smallest normal is min(2a, smallest normal) below it and
+    // a from it on (a NaN's a stays the median)
+    const mfh_u32 d = a + 0x00800000u;
+    const mfh_u32 lo = d < kMinN ? d : kMinN;
+    mfh_u32 m = a > lo ? a : lo;
+    m = a < kZero ? 0u : m;
+    const float af = mfh_f32(a);
+    m = (E5 ? af > kSatAt : af >= kSatAt) ? kSatTo : m;  // false for NaN
+    return mfh_f32(m | (u & 0x80000000u));
 }
 
-MFH_DEV mfh_u32 mfh_e4m3_encode(float v) { return mfh_fp8_encode<3, 7, 15, -3, 0x7eu, 0x43e00000u>(v); }
-MFH_DEV mfh_u32 mfh_e5m2_encode(float v) { return mfh_fp8_encode<2, 15, 31, -1, 0x7cu, 0x47600000u>(v); }
+// The hardware's NaN bytes of a word of codes -> 0x7f.  E4M3: a byte whose
+// low 7 bits are all set is 0xff from a NaN (0x7f is never produced);
+// E5M2: a byte whose low 7 bits are 0x7d..0x7f is 0xfe from a NaN.
+template <bool E5>
+MFH_DEV mfh_u32 mfh_fp8_nan_fix(mfh_u32 w)
+{
+    const mfh_u32 hit = ((w & 0x7f7f7f7fu) + (E5 ? 0x03030303u : 0x01010101u)) & 0x80808080u;
+    if constexpr (E5) return (w | (hit >> 7)) & ~hit;  // 0xfe -> 0x7f
+    else return w & ~hit;                              // 0xff -> 0x7f
+}
+
+// Four values -> four codes, value k in byte k.
+template <bool E5>
+MFH_DEV mfh_u32 mfh_fp8x4_encode(float v0, float v1, float v2, float v3)
+{
+    mfh_u32 w;
+    if constexpr (E5) {
+        w = (mfh_u32)__builtin_amdgcn_cvt_pk_bf8_f32(mfh_fp8_prep<true>(v0), mfh_fp8_prep<true>(v1), 0, false);
+        w = (mfh_u32)__builtin_amdgcn_cvt_pk_bf8_f32(mfh_fp8_prep<true>(v2), mfh_fp8_prep<true>(v3), (int)w, true);
+    } else {
+        w = (mfh_u32)__builtin_amdgcn_cvt_pk_fp8_f32(mfh_fp8_prep<false>(v0), mfh_fp8_prep<false>(v1), 0, false);
+        w = (mfh_u32)__builtin_amdgcn_cvt_pk_fp8_f32(mfh_fp8_prep<false>(v2), mfh_fp8_prep<false>(v3), (int)w, true);
+    }
+    return mfh_fp8_nan_fix<E5>(w);
+}
+
+// One value -> its code.
+template <bool E5>
+MFH_DEV mfh_u32 mfh_fp8_encode(float v)
+{
+    mfh_u32 w;
+    if constexpr (E5) w = (mfh_u32)__builtin_amdgcn_cvt_pk_bf8_f32(mfh_fp8_prep<true>(v), 0.0f, 0, false);
+    else w = (mfh_u32)__builtin_amdgcn_cvt_pk_fp8_f32(mfh_fp8_prep<false>(v), 0.0f, 0, false);
+    return mfh_fp8_nan_fix<E5>(w) & 0xffu;
+}
+
+MFH_DEV mfh_u32 mfh_e4m3_encode(float v) { return mfh_fp8_encode<false>(v); }
+MFH_DEV mfh_u32 mfh_e5m2_encode(float v) { return mfh_fp8_encode<true>(v); }
 
 // ---- BF16 -------------------------------------------------------------------
 

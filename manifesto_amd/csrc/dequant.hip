@@ -437,6 +437,41 @@ MFH_DEV mfh_u32 byte_reg(const mfh_u32* w, int k)
     else return encode_byte<ENC>(decode_reg<IN>(w, k));
 }
 
+// Output bytes 4j .. 4j + 3 of a register copy of P consecutive elements,
+// element 4j + k in byte k (bytes past P are zero codes).  FP8 codes leave
+// the hardware converter four at a time.
+template <int IN, int ENC, int P>
+MFH_DEV mfh_u32 word_reg(const mfh_u32* w, int j)
+{
+    if constexpr (ENC == kF8E4M3 || ENC == kF8E5M2) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = 4 * j + k < P ? decode_reg<IN>(w, 4 * j + k) : 0.0f;
+        return mfh_fp8x4_encode<ENC == kF8E5M2>(v[0], v[1], v[2], v[3]);
+    } else {
+        mfh_u32 word = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (4 * j + k < P) word |= byte_reg<IN, ENC>(w, 4 * j + k) << (8 * k);
+        return word;
+    }
+}
+
+// The output bytes of elements e0 .. e0 + 3, read from memory, element e0 + k in byte k.
+template <int IN, int ENC>
+MFH_DEV mfh_u32 word_at(const void* in, mfh_i64 e0)
+{
+    if constexpr (ENC == kF8E4M3 || ENC == kF8E5M2) {
+        return mfh_fp8x4_encode<ENC == kF8E5M2>(decode_any<IN>(in, e0), decode_any<IN>(in, e0 + 1),
+                                                decode_any<IN>(in, e0 + 2), decode_any<IN>(in, e0 + 3));
+    } else {
+        mfh_u32 word = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; k++) word |= byte_at<IN, ENC>(in, e0 + k) << (8 * k);
+        return word;
+    }
+}
+
 // FP8 and Int4 sources, and any source whose buffers are not aligned for
 // k_encode_byte_wave: item = 16 elements decoded one by one -> one 16-byte
 // store of codes when the output is 16-byte aligned, else the element loop.
@@ -450,12 +485,7 @@ __global__ __launch_bounds__(kBlock) void k_encode_byte(const void* __restrict__
     for (mfh_i64 v = (mfh_i64)blockIdx.x * kBlock + threadIdx.x; v < nitems; v += stride) {
         u32x4 o;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            mfh_u32 word = 0u;
-#pragma unroll
-            for (int k = 0; k < 4; k++) word |= byte_at<IN, ENC>(in, v * 16 + 4 * q + k) << (8 * k);
-            o[q] = word;
-        }
+        for (int q = 0; q < 4; q++) o[q] = word_at<IN, ENC>(in, v * 16 + 4 * q);
         store_nt(&dst[v], o);
     }
     for (mfh_i64 i = nitems * 16 + (mfh_i64)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
@@ -498,7 +528,7 @@ __global__ __launch_bounds__(BS) void k_encode_byte_wave(const void* __restrict_
             const mfh_u32 w[4] = {x[q][0], x[q][1], x[q][2], x[q][3]};
             mfh_u32 code[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int k = 0; k < P; k++) code[k >> 2] |= byte_reg<IN, ENC>(w, k) << ((k & 3) * 8);
+            for (int j = 0; j < (P + 3) / 4; j++) code[j] = word_reg<IN, ENC, P>(w, j);
             const mfh_i64 e0 = c * kChunk + (mfh_i64)(q * 64 + lane) * P;
             if constexpr (PAIR) {
                 if (q & 1) {
