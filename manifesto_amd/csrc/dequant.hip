@@ -661,6 +661,39 @@ MFH_DEV mfh_u32 nibble_at(const void* in, mfh_i64 i)
     return (mfh_u32)(v < -8 ? -8 : (v > 7 ? 7 : v)) & 0xfu;
 }
 
+// The same for element k of a register copy of consecutive elements.
+// Integer sources clamp the integer itself: every integer type converts to
+// f64 monotonically, so saturating and truncating its f64 value and then
+// clamping gives the same nibble, without the float round trip.
+template <int IN>
+MFH_DEV mfh_u32 nibble_reg(const mfh_u32* w, int k)
+{
+    constexpr int S = size_of<IN>();
+    int v;
+    if constexpr (IN == kInt8 || IN == kInt16) {
+        const int x = __builtin_amdgcn_sbfe((int)w[k * S / 4], (k * 8 * S) & 31, 8 * S);
+        v = x < -8 ? -8 : (x > 7 ? 7 : x);
+    } else if constexpr (IN == kUint8 || IN == kUint16) {
+        const mfh_u32 x = __builtin_amdgcn_ubfe(w[k * S / 4], (k * 8 * S) & 31, 8 * S);
+        v = x > 7u ? 7 : (int)x;
+    } else if constexpr (IN == kInt32) {
+        const int x = (int)w[k];
+        v = x < -8 ? -8 : (x > 7 ? 7 : x);
+    } else if constexpr (IN == kUint32) {
+        v = w[k] > 7u ? 7 : (int)w[k];
+    } else if constexpr (IN == kInt64) {
+        const long long x = (long long)((mfh_u64)w[2 * k] | ((mfh_u64)w[2 * k + 1] << 32));
+        v = x < -8 ? -8 : (x > 7 ? 7 : (int)x);
+    } else if constexpr (IN == kUint64) {
+        const mfh_u64 x = (mfh_u64)w[2 * k] | ((mfh_u64)w[2 * k + 1] << 32);
+        v = x > 7u ? 7 : (int)x;
+    } else {
+        const int x = (int)(signed char)byte_reg<IN, kInt8>(w, k);
+        v = x < -8 ? -8 : (x > 7 ? 7 : x);
+    }
+    return (mfh_u32)v & 0xfu;
+}
+
 // Item = 32 elements -> one 16-byte store of nibbles (16-byte aligned
 // output), then the byte loop for the rest.
 template <int IN>
@@ -714,10 +747,7 @@ __global__ __launch_bounds__(BS) void k_encode_int4_wave(const void* __restrict_
             const mfh_u32 w[4] = {x[q][0], x[q][1], x[q][2], x[q][3]};
             mfh_u32 code[2] = {0u, 0u};
 #pragma unroll
-            for (int k = 0; k < P; k++) {
-                const int v = (int)(signed char)byte_reg<IN, kInt8>(w, k);
-                code[k >> 3] |= ((mfh_u32)(v < -8 ? -8 : (v > 7 ? 7 : v)) & 0xfu) << (4 * (k & 7));
-            }
+            for (int k = 0; k < P; k++) code[k >> 3] |= nibble_reg<IN>(w, k) << (4 * (k & 7));
             mfh_u8* o = out + (c * kChunk + (mfh_i64)(q * 64 + lane) * P) / 2;
             if constexpr (P == 16) store_nt(reinterpret_cast<u32x2*>(o), u32x2{code[0], code[1]});
             else if constexpr (P == 8) store_nt(reinterpret_cast<mfh_u32*>(o), code[0]);

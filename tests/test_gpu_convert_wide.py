@@ -177,7 +177,8 @@ def test_int4_from_every_code(in_dt):
         a = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(NP_OF[in_dt])
         n = a.size
     else:
-        a = np.tile(np.arange(256, dtype=np.uint8), 3)
+        # 41 copies: two whole 4 KiB wave chunks of 8-bit codes and a tail
+        a = np.tile(np.arange(256, dtype=np.uint8), 41)
         n = a.size * (2 if in_dt == O.INT4 else 1)
     check(convert_i4(a, in_dt, n), O.bytes_to_i4(in_dt, a, n), f"{in_dt}->i4")
 
