@@ -32,6 +32,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -910,6 +911,161 @@ def load_traffic():
     return doc.get("kernels", doc).get("fp8_e4m3_to_bf16", {}).get("traffic_bytes_per_dispatch")
 
 
+# ---- summaries of rocprofv3 output (CPU only; the tables under profiles/) ----
+
+PROF_CONFIG = {"fused_swiglu": 3, "fused_gelu_chain": 4, "k_axpy_f32": 1, "k_dequant_fp8": 2, "k_dequant_int4": 5}
+PROF_WINDOWS_MS = [(0, 2), (2, 4), (4, 8), (8, 15), (15, 30), (30, 60), (60, 120)]
+
+
+def prof_name(name):
+    """'void mfh::(anonymous namespace)::k_axpy_f32<1, 64>(float*, ...)' -> 'k_axpy_f32<1, 64>'."""
+    n = name[5:] if name.startswith("void ") else name
+    n = n.replace("mfh::(anonymous namespace)::", "")
+    depth = 0
+    for i, ch in enumerate(n):
+        depth += (ch == "<") - (ch == ">")
+        if ch == "(" and depth == 0:
+            return n[:i]
+    return n
+
+
+def prof_config(name):
+    return next((cfg for fam, cfg in PROF_CONFIG.items() if name.startswith(fam)), None)
+
+
+def prof_rows(d, suffix):
+    """Rows of the first rocprofv3 CSV file under `d` whose name ends in `suffix`."""
+    import csv
+    csv.field_size_limit(1 << 30)
+    for dp, _, files in sorted(os.walk(d)):
+        for f in sorted(files):
+            if f.endswith(suffix):
+                with open(os.path.join(dp, f)) as fh:
+                    return list(csv.DictReader(fh))
+    sys.exit(f"bench.py: no *{suffix} under {d}")
+
+
+def prof_dispatches(d):
+    """Kernel name -> [(start ns, duration ns)] in start order, BASELINE kernels only."""
+    out = {}
+    for r in prof_rows(d, "kernel_trace.csv"):
+        n = prof_name(r["Kernel_Name"])
+        if prof_config(n) or n.startswith("fused_gelu_chain"):
+            start = int(r["Start_Timestamp"])
+            out.setdefault(n, []).append((start, int(r["End_Timestamp"]) - start))
+    for v in out.values():
+        v.sort()
+    return out
+
+
+def prof_windows(replay, settled):
+    """Mean duration in windows of time after the first dispatch of `replay`
+    relative to `settled`, and the slowest run of 20 consecutive dispatches."""
+    t0 = replay[0][0]
+    cells = []
+    for lo, hi in PROF_WINDOWS_MS:
+        w = [d for t, d in replay if lo * 1e6 <= t - t0 < hi * 1e6]
+        cells.append(f"{statistics.mean(w) / settled - 1:+.1%} ({len(w)})" if w else "-")
+    worst = max(statistics.mean(d for _, d in replay[i:i + 20]) for i in range(0, max(1, len(replay) - 20), 10))
+    return cells, f"{worst / settled - 1:+.1%}"
+
+
+def summarize_trace(d, bench_json, timed_k):
+    """--summarize-trace: the kernel table and the clock-transient table of a
+    `rocprofv3 --kernel-trace --stats` run of this bench (`bench_json` holds
+    the JSON line that run printed), or, without `bench_json`, the transient
+    table of a `--transient` run, whose kernels each start from an idle GPU."""
+    trace = prof_dispatches(d)
+    if bench_json:
+        with open(bench_json) as f:
+            configs = {c["config"]: c for c in json.loads(f.read().strip().splitlines()[-1])["configs"]}
+        stats = {prof_name(r["Name"]): r for r in prof_rows(d, "kernel_stats.csv")}
+        print("| kernel | calls | avg ns | min ns | max ns | timed avg ns | algorithmic bytes | GB/s at timed avg "
+              "| bench step ns | bench GB/s | cast GB/s |\n|---|---|---|---|---|---|---|---|---|---|---|")
+        order = sorted((n for n in trace if prof_config(n) in configs), key=lambda n: -float(stats[n]["AverageNs"]))
+        for n in order:
+            c, s = configs[prof_config(n)], stats[n]
+            timed = statistics.mean(x for _, x in trace[n][-timed_k:])
+            cast = c.get("cast_same_mix", {}).get("GB_s")
+            print(f"| `{n}` | {s['Calls']} | {float(s['AverageNs']):.0f} | {s['MinNs']} | {s['MaxNs']} | {timed:.0f} | "
+                  f"{c['bytes_per_step']} | {c['bytes_per_step'] / timed:.0f} | {c['ms_per_step'] * 1e6:.0f} | "
+                  f"{c['GB_s']:.0f} | {cast if cast is None else round(cast)} |")
+        print("\n| kernel | timed avg ns | " + " | ".join(f"{a}–{b} ms" for a, b in PROF_WINDOWS_MS) +
+              " | worst 20 |\n|" + "---|" * (len(PROF_WINDOWS_MS) + 3))
+        for n in order:
+            replay = trace[n][configs[prof_config(n)]["rotated_sets"]:]  # after the eager launch per set
+            settled = statistics.mean(x for _, x in trace[n][-timed_k:])
+            cells, worst = prof_windows(replay, settled)
+            print(f"| `{n}` | {settled:.0f} | " + " | ".join(cells) + f" | {worst} |")
+        return
+    # --transient: every kernel's run follows an idle second; its graph
+    # replays start after the longest gap among its first dispatches
+    print("| kernel | dispatches | settled ns | " + " | ".join(f"{a}–{b} ms" for a, b in PROF_WINDOWS_MS) +
+          " | worst 20 |\n|" + "---|" * (len(PROF_WINDOWS_MS) + 4))
+    runs = []
+    for n, ds in trace.items():
+        cur = [ds[0]]
+        for x in ds[1:]:
+            if x[0] - cur[-1][0] > 1e9:
+                runs.append((cur[0][0], n, cur))
+                cur = []
+            cur.append(x)
+        runs.append((cur[0][0], n, cur))
+    for _, n, run in sorted(runs):
+        if len(run) < 2 * timed_k:
+            continue
+        gaps = [(run[i + 1][0] - run[i][0], i + 1) for i in range(min(60, len(run) - 1))]
+        replay = run[max(gaps)[1]:]
+        settled = statistics.mean(x for _, x in replay[-timed_k:])
+        cells, worst = prof_windows(replay, settled)
+        print(f"| `{n}` | {len(run)} | {settled:.0f} | " + " | ".join(c.split(" ")[0] for c in cells) + f" | {worst} |")
+
+
+def summarize_pmc(fetch_dir, write_dir):
+    """--summarize-pmc: HBM bytes per dispatch of each BASELINE kernel from
+    two `rocprofv3 --pmc` runs of `bench.py --profile` (FETCH_SIZE, then
+    WRITE_SIZE), median over each kernel's dispatches, each counter scaled by
+    what it reads for the profile run's 64 MiB f32 copy.  Prints the JSON of
+    profiles/pmc_traffic.json."""
+    def medians(d, counter):
+        per = {}
+        for r in prof_rows(d, "counter_collection.csv"):
+            if r["Counter_Name"] != counter:
+                continue
+            k = prof_name(r["Kernel_Name"])
+            per.setdefault(k, {}).setdefault(r["Dispatch_Id"], 0.0)
+            per[k][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        return {k: statistics.median(v.values()) for k, v in per.items()}
+    fetch, write = medians(fetch_dir, "FETCH_SIZE"), medians(write_dir, "WRITE_SIZE")
+    cal = next(k for k in fetch if k.startswith("k_convert_vec<2, 2"))
+    copy_bytes = 64 << 20
+    rscale, wscale = copy_bytes / (fetch[cal] * 1024), copy_bytes / (write[cal] * 1024)
+    labels = {1: "axpy_f32", 2: "fp8_e4m3_to_bf16", 3: "swiglu_bf16", 4: "gelu_chain_f16", 5: "int4_to_bf16"}
+    alg = {cls.cfg: cls.bytes_per_step for cls in WORKLOADS}
+    kernels = {}
+    for k in sorted(fetch, key=lambda k: prof_config(k) or 0):
+        cfg = prof_config(k)
+        if not cfg or k not in write:
+            continue
+        r, w = fetch[k] * 1024 * rscale, write[k] * 1024 * wscale
+        kernels[labels[cfg]] = {"kernel": k, "FETCH_SIZE_KiB": fetch[k], "WRITE_SIZE_KiB": write[k],
+                                "hbm_read_bytes": round(r), "hbm_write_bytes": round(w),
+                                "traffic_bytes_per_dispatch": round(r + w), "algorithmic_bytes": alg[cfg],
+                                "traffic_over_algorithmic": round((r + w) / alg[cfg], 4)}
+    doc = {"_about": ("HBM bytes per dispatch from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (two separate "
+                      "runs of `python3 bench.py --profile 5`, median over the dispatches of each kernel), each "
+                      f"scaled by what the counter reads for a 64 MiB f32 copy ({cal}): reads x{rscale:.4f}, "
+                      f"writes x{wscale:.4f}. Summarised by `python3 bench.py --summarize-pmc FETCH_DIR WRITE_DIR`."),
+           "commands": [f"rocprofv3 --pmc {c} -f csv -d $GRAFT_REPO_ROOT/gpurun_out/prof/{d} -o run -- "
+                        "python3 $GRAFT_REPO_ROOT/bench.py --profile 5" for c, d in (("FETCH_SIZE", "fetch"),
+                                                                                     ("WRITE_SIZE", "write"))],
+           "calibration": {"kernel": cal + " (f32 copy)", "bytes_read": copy_bytes, "bytes_written": copy_bytes,
+                           "FETCH_SIZE_KiB": fetch[cal], "WRITE_SIZE_KiB": write[cal],
+                           "read_scale": rscale, "write_scale": wscale},
+           "kernels": kernels}
+    print(json.dumps(doc, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -933,7 +1089,19 @@ def main():
                     help="each kernel (and two variants of the gelu chain) from an idle GPU, for a kernel trace")
     ap.add_argument("--footprint", action="store_true",
                     help="each BASELINE kernel over 1 to 32 rotated sets (one JSON line each)")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="print the kernel and transient tables of a rocprofv3 --kernel-trace --stats output "
+                         "directory (no GPU needed)")
+    ap.add_argument("--bench-json", metavar="FILE", help="with --summarize-trace: the JSON line that run printed")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print pmc_traffic.json from two rocprofv3 --pmc runs of --profile (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace, args.bench_json, args.steps)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(every config shards into contiguous per-GPU ranges with no exchange step, so "
