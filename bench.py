@@ -1066,6 +1066,26 @@ def summarize_pmc(fetch_dir, write_dir):
     print(json.dumps(doc, indent=1))
 
 
+def summarize_valu(d):
+    """--summarize-valu: VALU instructions per element of each BASELINE
+    kernel from a `rocprofv3 --pmc SQ_INSTS_VALU SQ_WAVES ...` run of
+    `bench.py --profile`: SQ_INSTS_VALU counts wave-level instructions over
+    the device, so per element it is SQ_INSTS_VALU * 64 / elements (median
+    over each kernel's dispatches)."""
+    per = {}
+    for r in prof_rows(d, "counter_collection.csv"):
+        k = prof_name(r["Kernel_Name"])
+        if prof_config(k):
+            disp = per.setdefault(k, {}).setdefault(r["Counter_Name"], {})
+            disp[r["Dispatch_Id"]] = disp.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    elements = {cls.cfg: cls.n for cls in WORKLOADS}
+    print("| kernel | elements | SQ_INSTS_VALU | SQ_WAVES | VALU instructions / element |\n|---|---|---|---|---|")
+    for k in sorted(per, key=prof_config):
+        m = {c: statistics.median(v.values()) for c, v in per[k].items()}
+        n = elements[prof_config(k)]
+        print(f"| `{k}` | {n:,} | {m['SQ_INSTS_VALU']:.4g} | {m['SQ_WAVES']:,.0f} | {m['SQ_INSTS_VALU'] * 64 / n:.2f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1095,7 +1115,12 @@ def main():
     ap.add_argument("--bench-json", metavar="FILE", help="with --summarize-trace: the JSON line that run printed")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print pmc_traffic.json from two rocprofv3 --pmc runs of --profile (no GPU needed)")
+    ap.add_argument("--summarize-valu", metavar="DIR",
+                    help="print VALU instructions per element from a rocprofv3 --pmc run of --profile (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize_valu:
+        summarize_valu(args.summarize_valu)
+        return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace, args.bench_json, args.steps)
         return
