@@ -81,13 +81,54 @@ struct Parser {
         }
         return true;
     }
+    // One UTF-8 sequence at p as Go's utf8.DecodeRune reads it: a malformed
+    // or overlong sequence, a surrogate or a value past U+10FFFF is U+FFFD
+    // and takes one byte.
+    unsigned rune()
+    {
+        const unsigned char* u = reinterpret_cast<const unsigned char*>(p);
+        const size_t left = (size_t)(end - p);
+        const unsigned b0 = u[0];
+        auto cont = [&](size_t i, unsigned lo, unsigned hi) { return i < left && u[i] >= lo && u[i] <= hi; };
+        if (b0 < 0x80) {
+            p += 1;
+            return b0;
+        }
+        if (b0 >= 0xc2 && b0 <= 0xdf && cont(1, 0x80, 0xbf)) {
+            p += 2;
+            return ((b0 & 0x1f) << 6) | (u[1] & 0x3f);
+        }
+        if (b0 >= 0xe0 && b0 <= 0xef) {
+            const unsigned lo = b0 == 0xe0 ? 0xa0 : 0x80, hi = b0 == 0xed ? 0x9f : 0xbf;
+            if (cont(1, lo, hi) && cont(2, 0x80, 0xbf)) {
+                p += 3;
+                return ((b0 & 0x0f) << 12) | ((u[1] & 0x3f) << 6) | (u[2] & 0x3f);
+            }
+        }
+        if (b0 >= 0xf0 && b0 <= 0xf4) {
+            const unsigned lo = b0 == 0xf0 ? 0x90 : 0x80, hi = b0 == 0xf4 ? 0x8f : 0xbf;
+            if (cont(1, lo, hi) && cont(2, 0x80, 0xbf) && cont(3, 0x80, 0xbf)) {
+                p += 4;
+                return ((b0 & 0x07) << 18) | ((u[1] & 0x3f) << 12) | ((u[2] & 0x3f) << 6) | (u[3] & 0x3f);
+            }
+        }
+        p += 1;
+        return 0xfffd;
+    }
+    // A string as encoding/json unquotes it: invalid UTF-8 and unpaired
+    // surrogate escapes become U+FFFD rather than errors.
     bool string(std::string& out)
     {
         if (p >= end || *p != '"') return fail_at("expected a string");
         p++;
         while (p < end && *p != '"') {
-            unsigned char c = (unsigned char)*p++;
+            unsigned char c = (unsigned char)*p;
             if (c < 0x20) return fail_at("control character in a string");
+            if (c >= 0x80) {
+                utf8(out, rune());
+                continue;
+            }
+            p++;
             if (c != '\\') {
                 out += (char)c;
                 continue;
@@ -106,11 +147,24 @@ struct Parser {
             case 'u': {
                 unsigned cp;
                 if (!hex4(&cp)) return false;
-                if (cp >= 0xd800 && cp < 0xdc00 && end - p >= 6 && p[0] == '\\' && p[1] == 'u') {
-                    p += 2;
-                    unsigned lo;
-                    if (!hex4(&lo)) return false;
-                    cp = (lo >= 0xdc00 && lo < 0xe000) ? 0x10000 + ((cp - 0xd800) << 10) + (lo - 0xdc00) : 0xfffd;
+                if (cp >= 0xd800 && cp < 0xe000) {
+                    // a high surrogate and a low one escaped right after it
+                    // make one code point; any other surrogate is U+FFFD and
+                    // the escape after it is read on its own
+                    const char* save = p;
+                    unsigned lo = 0;
+                    if (cp < 0xdc00 && end - p >= 6 && p[0] == '\\' && p[1] == 'u') {
+                        p += 2;
+                        std::string err;
+                        std::swap(err, error);
+                        if (!hex4(&lo)) lo = 0;
+                        std::swap(err, error);
+                    }
+                    if (lo >= 0xdc00 && lo < 0xe000) cp = 0x10000 + ((cp - 0xd800) << 10) + (lo - 0xdc00);
+                    else {
+                        p = save;
+                        cp = 0xfffd;
+                    }
                 }
                 utf8(out, cp);
                 break;

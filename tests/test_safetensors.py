@@ -150,3 +150,68 @@ def test_scale_for_a_tensor_stored_as_written_is_refused(tmp_path):
     rc = S._L().mfh_safetensors_load(f._h, b"w", None, b"s", 0, ctypes.byref(h))
     assert rc == -1 and "stored as written" in M.last_error()
     assert not h.value
+
+
+def test_header_parser_survives_mutated_headers(tmp_path):
+    # Every mutation of a valid header (bytes flipped, dropped, duplicated or
+    # cut, the stated length off by a few bytes) either indexes or raises
+    # MFHError; none may crash the process or read past the header.
+    rng = np.random.default_rng(31)
+    base = json.dumps({"__metadata__": {"format": "pt"},  # the key's escapes: \u00e9 and a surrogate pair
+                       "w\u00e9\U0001f600": {"dtype": "F8_E4M3", "shape": [2, 3], "data_offsets": [0, 6]},
+                       "s": {"dtype": "F32", "shape": [], "data_offsets": [6, 10]},
+                       "n": {"dtype": "I4", "shape": [4], "data_offsets": [10, 12]}}).encode()
+    assert b"\\ud83d\\ude00" in base
+    data = bytes(range(12))
+    seen = {"ok": 0, "error": 0}
+    for trial in range(400):
+        raw = bytearray(base)
+        for _ in range(int(rng.integers(1, 4))):
+            kind = int(rng.integers(0, 4))
+            at = int(rng.integers(0, len(raw)))
+            if kind == 0:
+                raw[at] = int(rng.integers(0, 256))
+            elif kind == 1 and len(raw) > 1:
+                del raw[at]
+            elif kind == 2:
+                raw[at:at] = raw[at:at + int(rng.integers(1, 8))]
+            else:
+                raw = raw[:at]
+        length = len(raw) + int(rng.integers(-3, 4)) if trial % 5 == 0 else len(raw)
+        path = tmp_path / f"m{trial}.safetensors"
+        with open(path, "wb") as f:
+            f.write(struct.pack("<Q", max(0, length)))
+            f.write(bytes(raw))
+            f.write(data)
+        try:
+            f = SafeTensorsFile(str(path))
+            for name in f.index():
+                try:
+                    f.read(name)
+                except M.MFHError:
+                    pass
+            seen["ok"] += 1
+        except M.MFHError:
+            seen["error"] += 1
+    assert seen["ok"] > 0 and seen["error"] > 0, seen
+
+
+def test_names_unquoted_like_encoding_json(tmp_path):
+    # encoding/json replaces invalid UTF-8 bytes and unpaired surrogate
+    # escapes with U+FFFD instead of failing; a high surrogate followed by
+    # an escape that is not a low surrogate leaves that escape to be read on
+    # its own
+    raw = ('{"a\\ud83d\\ude00": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]},'
+           ' "b\\udc00x": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]},'
+           ' "c\\ud800\\u0041": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]},'
+           ' "d\\ud800": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]},').encode()
+    raw += b' "e\xff\xc0\x80\xed\xa0\x80z\xc3\xa9": {"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}'
+    path = tmp_path / "names.safetensors"
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(raw)))
+        f.write(raw)
+        f.write(b"\x07")
+    names = list(SafeTensorsFile(str(path)).index())
+    # \xff: one U+FFFD; \xc0\x80 (overlong): two; \xed\xa0\x80 (a surrogate
+    # in UTF-8): three, one per byte; then "z" and a valid e-acute
+    assert names == ["a\U0001f600", "b�x", "c�A", "d�", "e" + "�" * 6 + "zé"]
