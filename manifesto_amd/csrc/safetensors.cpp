@@ -176,14 +176,28 @@ struct Parser {
         p++;
         return true;
     }
+    // -?(0|[1-9][0-9]*)(\.[0-9]+)?([eE][+-]?[0-9]+)?, as JSON (and Go's
+    // scanner) has it
     bool number(Json& v)
     {
         const char* s = p;
+        auto digits = [&] {
+            const char* d = p;
+            while (p < end && *p >= '0' && *p <= '9') p++;
+            return p > d;
+        };
         if (p < end && *p == '-') p++;
-        if (p >= end || !std::isdigit((unsigned char)*p)) return fail_at("bad number");
-        while (p < end && (std::isdigit((unsigned char)*p) || *p == '.' || *p == 'e' || *p == 'E' || *p == '+' ||
-                           *p == '-'))
+        if (p < end && *p == '0') p++;
+        else if (!(p < end && *p >= '1' && *p <= '9') || !digits()) return fail_at("bad number");
+        if (p < end && *p == '.') {
             p++;
+            if (!digits()) return fail_at("bad number");
+        }
+        if (p < end && (*p == 'e' || *p == 'E')) {
+            p++;
+            if (p < end && (*p == '+' || *p == '-')) p++;
+            if (!digits()) return fail_at("bad number");
+        }
         v.kind = Json::kNumber;
         v.text.assign(s, p);
         return true;
@@ -374,41 +388,53 @@ int index_file(mfh_safetensors& f)
     if (ok && ps.p != ps.end) ok = ps.fail_at("trailing data after the header object");
     if (!ok) return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors index: %s", ps.error.c_str());
     if (root.kind != Json::kObject) return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors index: header is not an object");
+    // Each entry decodes as json.Unmarshal fills TensorMeta
+    // (weights/reader.go:13-17,64-68): null anywhere leaves the field as it
+    // was, unknown fields are ignored, data_offsets fills [2]int64 (missing
+    // elements zero, extra ones skipped), and a value of the wrong type is an
+    // error.
     for (auto& kv : root.members) {
         if (kv.first == "__metadata__") continue;
         const Json& meta = kv.second;
-        if (meta.kind != Json::kObject)
+        if (meta.kind != Json::kObject && meta.kind != Json::kNull)
             return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors tensor \"%s\": not an object", kv.first.c_str());
         Entry e;
         e.name = kv.first;
-        bool have_offsets = false;
         for (auto& field : meta.members) {
             const Json& v = field.second;
+            if (v.kind == Json::kNull) {
+                if (key_is(field.first, "shape")) e.shape.clear();  // a nil slice
+                continue;
+            }
             if (key_is(field.first, "dtype")) {
                 if (v.kind != Json::kString)
                     return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors tensor \"%s\": dtype is not a string", e.name.c_str());
                 e.dtype_name = v.text;
                 e.dtype = parse_dtype(v.text);
             } else if (key_is(field.first, "shape")) {
-                if (v.kind != Json::kArray && v.kind != Json::kNull)
+                if (v.kind != Json::kArray)
                     return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors tensor \"%s\": shape is not an array", e.name.c_str());
                 e.shape.clear();
                 for (const Json& d : v.items) {
-                    int64_t x;
-                    if (!to_int64(d, &x))
+                    int64_t x = 0;
+                    if (d.kind != Json::kNull && !to_int64(d, &x))
                         return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors tensor \"%s\": shape holds a non-integer",
                                     e.name.c_str());
                     e.shape.push_back(x);
                 }
             } else if (key_is(field.first, "data_offsets")) {
-                if (v.kind != Json::kArray || v.items.size() != 2 || !to_int64(v.items[0], &e.begin) ||
-                    !to_int64(v.items[1], &e.end))
-                    return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors tensor \"%s\": data_offsets is not [begin, end]",
+                int64_t* slot[2] = {&e.begin, &e.end};
+                if (v.kind != Json::kArray)
+                    return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors tensor \"%s\": data_offsets is not an array",
                                 e.name.c_str());
-                have_offsets = true;
+                for (size_t i = 0; i < 2; i++) {
+                    if (i >= v.items.size()) *slot[i] = 0;
+                    else if (v.items[i].kind != Json::kNull && !to_int64(v.items[i], slot[i]))
+                        return fail(MFH_ERR_INVALID_ARGUMENT,
+                                    "safetensors tensor \"%s\": data_offsets holds a non-integer", e.name.c_str());
+                }
             }
         }
-        (void)have_offsets;  // absent offsets decode as [0, 0], as in the reference
         auto it = f.by_name.find(e.name);
         if (it != f.by_name.end()) f.entries[it->second] = std::move(e);  // a repeated key keeps the last value
         else {

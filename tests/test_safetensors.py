@@ -93,14 +93,38 @@ def test_dtype_parse_aliases(tmp_path):
     ('[1, 2]', None, "header is not an object"),
     ('{"a": 1}', None, 'safetensors tensor "a"'),
     ('{"a": {"shape": [1.5], "dtype": "F32", "data_offsets": [0, 4]}}', None, "non-integer"),
-    ('{"a": {"dtype": "F32", "data_offsets": [0]}}', None, "data_offsets"),
+    ('{"a": {"dtype": "F32", "data_offsets": 4}}', None, "data_offsets is not an array"),
+    ('{"a": {"dtype": "F32", "data_offsets": [0, true]}}', None, "data_offsets holds a non-integer"),
+    ('{"a": {"dtype": 7}}', None, "dtype is not a string"),
     ('{}', 10 ** 6, "unexpected EOF"),
     ('{} trailing', None, "trailing data"),
+    # numbers as JSON's grammar (and Go's scanner) has them
+    ('{"a": {"shape": [01]}}', None, "safetensors index"),
+    ('{"a": {"shape": [1.]}}', None, "bad number"),
+    ('{"a": {"shape": [1e]}}', None, "bad number"),
+    ('{"a": {"shape": [-]}}', None, "bad number"),
+    ('{"__metadata__": {"k": 1-2}}', None, "safetensors index"),
 ])
 def test_index_errors(tmp_path, header, length, match):
     path = write_raw(tmp_path / "bad.safetensors", header, length=length)
     with pytest.raises(M.MFHError, match=match):
         SafeTensorsFile(path)
+
+
+def test_entries_decode_as_json_unmarshal_fills_tensor_meta(tmp_path):
+    # weights/reader.go:13-17,64-68: null leaves a field as it was (a nil
+    # shape), data_offsets fills [2]int64 with missing elements zero and
+    # extra ones skipped, unknown fields and a null entry decode to zeros
+    header = ('{"a": {"dtype": "F32", "data_offsets": [4]},'
+              ' "b": {"dtype": null, "shape": [null, 3], "data_offsets": [0, 4, "x", {}]},'
+              ' "c": null,'
+              ' "d": {"DType": "U8", "Shape": [2], "extra": [1, 2], "data_offsets": [null, 2]},'
+              ' "e": {"dtype": "U8", "dtype": null, "shape": [5], "shape": null, "data_offsets": [1, 3],'
+              ' "data_offsets": [2]}}')
+    index = SafeTensorsFile(write_raw(tmp_path / "m.safetensors", header, b"\0" * 8)).index()
+    got = {k: (v.dtype, v.shape, list(v.data_offsets)) for k, v in index.items()}
+    assert got == {"a": ("F32", [], [4, 0]), "b": ("", [0, 3], [0, 4]), "c": ("", [], [0, 0]),
+                   "d": ("U8", [2], [0, 2]), "e": ("U8", [], [2, 0])}
 
 
 def test_truncated_file_and_out_of_range_reads(tmp_path):
