@@ -387,7 +387,10 @@ int index_file(mfh_safetensors& f)
     ps.ws();
     if (ok && ps.p != ps.end) ok = ps.fail_at("trailing data after the header object");
     if (!ok) return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors index: %s", ps.error.c_str());
-    if (root.kind != Json::kObject) return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors index: header is not an object");
+    // a null header unmarshals into an empty map, anything else but an
+    // object is a type error
+    if (root.kind != Json::kObject && root.kind != Json::kNull)
+        return fail(MFH_ERR_INVALID_ARGUMENT, "safetensors index: header is not an object");
     // Each entry decodes as json.Unmarshal fills TensorMeta
     // (weights/reader.go:13-17,64-68): null anywhere leaves the field as it
     // was, unknown fields are ignored, data_offsets fills [2]int64 (missing

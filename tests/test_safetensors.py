@@ -121,6 +121,7 @@ def test_entries_decode_as_json_unmarshal_fills_tensor_meta(tmp_path):
               ' "d": {"DType": "U8", "Shape": [2], "extra": [1, 2], "data_offsets": [null, 2]},'
               ' "e": {"dtype": "U8", "dtype": null, "shape": [5], "shape": null, "data_offsets": [1, 3],'
               ' "data_offsets": [2]}}')
+    assert SafeTensorsFile(write_raw(tmp_path / "n.safetensors", " null ")).index() == {}
     index = SafeTensorsFile(write_raw(tmp_path / "m.safetensors", header, b"\0" * 8)).index()
     got = {k: (v.dtype, v.shape, list(v.data_offsets)) for k, v in index.items()}
     assert got == {"a": ("F32", [], [4, 0]), "b": ("", [0, 3], [0, 4]), "c": ("", [], [0, 0]),
