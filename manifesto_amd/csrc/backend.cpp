@@ -538,6 +538,7 @@ const char* mfh_tensor_location(const mfh_tensor* t) { return t ? "hip" : nullpt
 int32_t mfh_tensor_state(const mfh_tensor* t)
 {
     if (tensor_dead(t)) return MFH_STATE_CLOSED;
+    std::lock_guard<std::mutex> lock(t->backend->mu);  // other threads mark and clear the same storage
     Storage& st = *t->storage;
     if (st.pending && st.done) {
         const Device* dev;
