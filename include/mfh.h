@@ -86,7 +86,9 @@ int mfh_stream_sync(void* stream);
  * (1, 2 or 4).  `kernel` is "fp8", "int4", "axpy", "axpy16", "convert" or
  * "fused"; 0 keeps the current setting and -1 restores the default.  Defaults
  * are measured on MI355X and can also be set with MFH_BPC_<KERNEL> /
- * MFH_UNROLL_<KERNEL>.  For "fused" the items per thread apply to kernels
+ * MFH_UNROLL_<KERNEL>.  "convert" reports 0 items per thread by default:
+ * each cast picks its own (2 where the output is wider than the source, else
+ * 1; 4 runs as 2).  For "fused" the items per thread apply to kernels
  * compiled afterwards.  A deployment knob with no counterpart in the
  * reference; results do not depend on it. */
 int mfh_set_launch_config(const char* kernel, int32_t blocks_per_cu, int32_t items_per_thread);

@@ -204,7 +204,7 @@ LaunchCfg g_cfg[(int)Kern::kCount] = {
     {"int4", {kMaxBlocksPerCu}, {2}, {256}, kSizes64To256},
     {"axpy", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
     {"axpy16", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
-    {"convert", {kMaxBlocksPerCu}, {1}, {0}, kSizes64To256},
+    {"convert", {kMaxBlocksPerCu}, {0}, {0}, kSizes64To256},  // 0: per cast
     {"fused", {0}, {0}, {0}, kSizes64To1024},
 };
 

@@ -202,6 +202,12 @@ def test_launch_config_set_keep_and_restore():
         M.set_launch_config("fp8", 0, 3)
     with pytest.raises(M.MFHError):
         M.set_launch_config("nope", 1, 1)
+    # the casts pick their items per thread themselves unless one is set
+    assert M.get_launch_config("convert")[1] == 0
+    M.set_launch_config("convert", 0, 2)
+    assert M.get_launch_config("convert")[1] == 2
+    M.set_launch_config("convert", 0, -1)
+    assert M.get_launch_config("convert")[1] == 0
 
 
 def test_launch_threads_set_keep_restore_and_limits():
