@@ -87,7 +87,7 @@ int mfh_stream_sync(void* stream);
  * "fused"; 0 keeps the current setting and -1 restores the default.  Defaults
  * are measured on MI355X and can also be set with MFH_BPC_<KERNEL> /
  * MFH_UNROLL_<KERNEL>.  "convert" reports 0 items per thread by default:
- * each cast picks its own (2 where the output is wider than the source, else
+ * each cast picks its own (2 where the output is four times the source, else
  * 1; 4 runs as 2).  For "fused" the items per thread apply to kernels
  * compiled afterwards.  A deployment knob with no counterpart in the
  * reference; results do not depend on it. */

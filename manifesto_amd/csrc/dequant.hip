@@ -260,23 +260,39 @@ MFH_DEV float dec16(mfh_u32 h)
 // 16-bit storage -> any output, one 16-byte store per item: 8 elements for a
 // 16-bit output, 4 for f32.  (The cast that sits between a bf16/f16 tensor and
 // an f32 fusion in the reference.)
-template <int IN, int OUT, int BS>
+template <int IN, int OUT, int BS, int U>
 __global__ __launch_bounds__(BS) void k_convert16_vec(const void* __restrict__ in, void* __restrict__ out,
                                                           mfh_i64 nitems)
 {
-    const mfh_i64 stride = (mfh_i64)gridDim.x * BS;
+    const mfh_i64 chunk = (mfh_i64)BS * U;  // items of a workgroup, thread t holding t, t + BS, ...
     u32x4* dst = reinterpret_cast<u32x4*>(out);
-    for (mfh_i64 v = (mfh_i64)blockIdx.x * BS + threadIdx.x; v < nitems; v += stride) {
+    for (mfh_i64 base = (mfh_i64)blockIdx.x * chunk; base < nitems; base += (mfh_i64)gridDim.x * chunk) {
         if constexpr (OUT == kFloat32) {
-            u32x2 w = reinterpret_cast<const u32x2*>(in)[v];
-            store_nt(&dst[v], u32x4{mfh_bits(dec16<IN>(w[0] & 0xffffu)), mfh_bits(dec16<IN>(w[0] >> 16)),
-                                    mfh_bits(dec16<IN>(w[1] & 0xffffu)), mfh_bits(dec16<IN>(w[1] >> 16))});
-        } else {
-            u32x4 w = load_nt(reinterpret_cast<const u32x4*>(in) + v);
-            u32x4 o;
+            u32x2 w[U];
 #pragma unroll
-            for (int k = 0; k < 4; k++) o[k] = encode_pair<OUT>(dec16<IN>(w[k] & 0xffffu), dec16<IN>(w[k] >> 16));
-            store_nt(&dst[v], o);
+            for (int u = 0; u < U; u++)  // past-the-end items load the last one again
+                w[u] = reinterpret_cast<const u32x2*>(in)[min(base + u * BS + (mfh_i64)threadIdx.x, nitems - 1)];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const mfh_i64 v = base + u * BS + (mfh_i64)threadIdx.x;
+                if (v < nitems)
+                    store_nt(&dst[v], u32x4{mfh_bits(dec16<IN>(w[u][0] & 0xffffu)), mfh_bits(dec16<IN>(w[u][0] >> 16)),
+                                            mfh_bits(dec16<IN>(w[u][1] & 0xffffu)), mfh_bits(dec16<IN>(w[u][1] >> 16))});
+            }
+        } else {
+            u32x4 w[U];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                w[u] = load_nt(reinterpret_cast<const u32x4*>(in) + min(base + u * BS + (mfh_i64)threadIdx.x, nitems - 1));
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const mfh_i64 v = base + u * BS + (mfh_i64)threadIdx.x;
+                u32x4 o;
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    o[k] = encode_pair<OUT>(dec16<IN>(w[u][k] & 0xffffu), dec16<IN>(w[u][k] >> 16));
+                if (v < nitems) store_nt(&dst[v], o);
+            }
         }
     }
 }
@@ -1057,9 +1073,14 @@ struct ConvertLaunch {
         constexpr int per = OUT == kFloat32 ? 4 : 8;
         if ((in_dt == kBFloat16 || in_dt == kFloat16) && aligned(in, per * 2) && aligned16(out) && n % per == 0) {
             int64_t nitems = n / per;
-            unsigned grid = grid_for(nitems, dev, Kern::kConvert, 1, BS);
-            if (in_dt == kBFloat16) k_convert16_vec<kBFloat16, OUT, BS><<<grid, BS, 0, stream>>>(in, out, nitems);
-            else k_convert16_vec<kFloat16, OUT, BS><<<grid, BS, 0, stream>>>(in, out, nitems);
+            // one item per thread unless the launch config sets two: the
+            // widening to f32 ran 1% slower with two
+            const int u = items_per_thread(Kern::kConvert) >= 2 ? 2 : 1;
+            unsigned grid = grid_for(nitems, dev, Kern::kConvert, u, BS);
+            if (in_dt == kBFloat16 && u == 2) k_convert16_vec<kBFloat16, OUT, BS, 2><<<grid, BS, 0, stream>>>(in, out, nitems);
+            else if (in_dt == kBFloat16) k_convert16_vec<kBFloat16, OUT, BS, 1><<<grid, BS, 0, stream>>>(in, out, nitems);
+            else if (u == 2) k_convert16_vec<kFloat16, OUT, BS, 2><<<grid, BS, 0, stream>>>(in, out, nitems);
+            else k_convert16_vec<kFloat16, OUT, BS, 1><<<grid, BS, 0, stream>>>(in, out, nitems);
             return launch_status("k_convert16_vec");
         }
         if constexpr (OUT != kFloat32) {
@@ -1074,11 +1095,12 @@ struct ConvertLaunch {
         // are aligned for them, else the element loop (256 threads)
         const int src_size = dtype_size(in_dt);
         const bool vec = src_size > 0 && aligned(in, (unsigned)std::min(per * src_size, 16)) && aligned16(out);
-        // items per thread: two where the output is wider than the source
+        // items per thread: two where the output is four times the source
         // (int8 -> f32 +14%), one elsewhere (same-width copies lose 2-3%
-        // with two), unless the launch config sets them
+        // with two, 2x widening gains nothing), unless the launch config
+        // sets them
         const int set_u = items_per_thread(Kern::kConvert);
-        const int u = set_u > 0 ? (set_u >= 2 ? 2 : 1) : (size_of<OUT>() > src_size ? 2 : 1);
+        const int u = set_u > 0 ? (set_u >= 2 ? 2 : 1) : (size_of<OUT>() >= 4 * src_size ? 2 : 1);
         const unsigned grid = vec ? grid_for(std::max<int64_t>(n / per, 1), dev, Kern::kConvert, u, BS)
                                   : grid_for(n, dev, Kern::kConvert);
         switch (in_dt) {
