@@ -119,3 +119,28 @@ def test_int4_encode_round_trip_past_2_31(torch):
         want = torch.clamp(v[lo:hi], -8, 7)
         assert torch.equal(back[lo:hi], want), f"int4 round trip mismatch in [{lo}, {hi})"
     assert int(packed[-1]) >> 4 == 0
+
+
+@pytest.mark.parametrize("in_dt", [M.BFLOAT16, M.FLOAT64, M.INT8])
+def test_casts_to_f32_past_2_31(torch, in_dt):
+    # bf16 -> f32 (k_convert16_vec), f64 -> f32 (k_narrow_f64_vec) and
+    # int8 -> f32 (k_convert_vec, two items per thread) over an odd count past
+    # 2^31: each is exact or one IEEE rounding (f64 -> f32 of finite values is
+    # round-to-nearest-even, which torch's cast also does)
+    n = (1 << 31) + 5
+    log(f"cast {in_dt} -> f32, n = {n}")
+    g = torch.Generator(device="cuda").manual_seed(36 + in_dt)
+    if in_dt == M.INT8:
+        src = torch.randint(-128, 128, (n,), dtype=torch.int8, device="cuda", generator=g)
+    else:
+        tdt = torch.bfloat16 if in_dt == M.BFLOAT16 else torch.float64
+        src = torch.randn(n, dtype=torch.float32, device="cuda", generator=g).to(tdt)
+        if in_dt == M.FLOAT64:
+            src.mul_(1.0 + 2.0 ** -30)  # bits below f32 precision, so the narrowing rounds
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    M.convert(out.data_ptr(), M.FLOAT32, src.data_ptr(), in_dt, n, stream())
+    for lo, hi in chunks(n):
+        want = src[lo:hi].float()
+        assert torch.equal(out[lo:hi].view(torch.int32), want.view(torch.int32)), f"{in_dt} mismatch in [{lo}, {hi})"
+    del src, out
+    torch.cuda.empty_cache()
