@@ -542,14 +542,13 @@ __global__ __launch_bounds__(kBlock) void k_encode_byte(const void* __restrict__
 // of a wave reading 1 KiB contiguously: a wave takes chunks of 4 KiB of
 // source, lane l the 16-byte pieces l, l + 64, l + 128 and l + 192 of its
 // chunk, and writes the 16 / size output bytes of each piece next to its
-// neighbours' (16-, 4- or 2-byte stores, 8-byte ones for 2-byte sources).
-// With PAIR (2-byte sources, output 16-byte aligned) lane l takes the
-// adjacent pieces 2l, 2l + 1 (and 128 + 2l, 129 + 2l) so that their 16
-// bytes leave in one 16-byte store instead of two 8-byte ones: 2-4% faster.
-// One lane taking 16 consecutive elements instead (64 bytes of f32) spreads
-// each load instruction over 4 KiB: f32 -> e4m3 ran at 4.4 TB/s that way.
-// Elements past the last whole chunk run the element loop.
-template <int IN, int ENC, int BS, bool PAIR>
+// neighbours' (16-, 8-, 4- or 2-byte stores).  Lanes taking two adjacent
+// pieces each, so that 2-byte sources store 16 bytes at a time, split every
+// load instruction over 2 KiB: bf16 -> e4m3 ran 4% slower that way.  One lane
+// taking 16 consecutive elements (64 bytes of f32) spreads each load
+// instruction over 4 KiB: f32 -> e4m3 ran at 4.4 TB/s that way.  Elements
+// past the last whole chunk run the element loop.
+template <int IN, int ENC, int BS>
 __global__ __launch_bounds__(BS) void k_encode_byte_wave(const void* __restrict__ in, mfh_u8* __restrict__ out,
                                                              mfh_i64 n)
 {
@@ -557,18 +556,14 @@ __global__ __launch_bounds__(BS) void k_encode_byte_wave(const void* __restrict_
     constexpr int P = 16 / S;          // elements (and output bytes) per 16-byte piece
     constexpr int kPieces = 4;         // pieces per lane per chunk
     constexpr mfh_i64 kChunk = 64 * kPieces * P;  // elements per wave chunk
-    static_assert(!PAIR || P == 8, "pairs are for 2-byte sources");
     const int lane = (int)threadIdx.x & 63;
     const mfh_i64 waves = (mfh_i64)gridDim.x * (BS / 64);
     const mfh_i64 nchunks = n / kChunk;
     for (mfh_i64 c = (mfh_i64)blockIdx.x * (BS / 64) + (threadIdx.x >> 6); c < nchunks; c += waves) {
         u32x4 x[kPieces];
 #pragma unroll
-        for (int q = 0; q < kPieces; q++) {
-            const int piece = PAIR ? (q >> 1) * 128 + 2 * lane + (q & 1) : q * 64 + lane;
-            x[q] = load_nt(reinterpret_cast<const u32x4*>(in) + c * (64 * kPieces) + piece);
-        }
-        mfh_u32 prev[2] = {0u, 0u};
+        for (int q = 0; q < kPieces; q++)
+            x[q] = load_nt(reinterpret_cast<const u32x4*>(in) + c * (64 * kPieces) + q * 64 + lane);
 #pragma unroll
         for (int q = 0; q < kPieces; q++) {
             const mfh_u32 w[4] = {x[q][0], x[q][1], x[q][2], x[q][3]};
@@ -576,15 +571,7 @@ __global__ __launch_bounds__(BS) void k_encode_byte_wave(const void* __restrict_
 #pragma unroll
             for (int j = 0; j < (P + 3) / 4; j++) code[j] = word_reg<IN, ENC, P>(w, j);
             const mfh_i64 e0 = c * kChunk + (mfh_i64)(q * 64 + lane) * P;
-            if constexpr (PAIR) {
-                if (q & 1) {
-                    const mfh_i64 p0 = c * kChunk + (mfh_i64)((q >> 1) * 128 + 2 * lane) * P;
-                    store_nt(reinterpret_cast<u32x4*>(out + p0), u32x4{prev[0], prev[1], code[0], code[1]});
-                } else {
-                    prev[0] = code[0];
-                    prev[1] = code[1];
-                }
-            } else if constexpr (P == 16) store_nt(reinterpret_cast<u32x4*>(out + e0), u32x4{code[0], code[1], code[2], code[3]});
+            if constexpr (P == 16) store_nt(reinterpret_cast<u32x4*>(out + e0), u32x4{code[0], code[1], code[2], code[3]});
             else if constexpr (P == 8) store_nt(reinterpret_cast<u32x2*>(out + e0), u32x2{code[0], code[1]});
             else if constexpr (P == 4) store_nt(reinterpret_cast<mfh_u32*>(out + e0), code[0]);
             else store_nt(reinterpret_cast<mfh_u16*>(out + e0), (mfh_u16)code[0]);
@@ -608,43 +595,32 @@ int cast_threads(int in_dt, int out_size)
     return src > 0 && out_size >= 4 * src ? 256 : 64;
 }
 
-template <int ENC, int BS, bool PAIR>
+template <int ENC, int BS>
 int launch_encode_byte_wave(const Device* dev, mfh_u8* out, const void* in, int in_dt, int64_t n, int size,
                             hipStream_t stream)
 {
     const int64_t chunk_elems = 64 * 4 * (16 / size);
     const unsigned grid = grid_for(std::max<int64_t>(n / chunk_elems, 1) * 64, dev, Kern::kConvert, 1, BS);
-    if constexpr (PAIR) {
-        switch (in_dt) {
-        case kFloat16: k_encode_byte_wave<kFloat16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
-        case kBFloat16: k_encode_byte_wave<kBFloat16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
-        case kInt16: k_encode_byte_wave<kInt16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
-        case kUint16: k_encode_byte_wave<kUint16, ENC, BS, true><<<grid, BS, 0, stream>>>(in, out, n); break;
-        default: return fail(MFH_ERR_INVALID_ARGUMENT, "mfh_convert: paired encode of %s", dtype_name(in_dt));
-        }
-        return launch_status("k_encode_byte_wave");
-    } else {
-        switch (in_dt) {
+    switch (in_dt) {
 #define MFH_ENCODE_WAVE_CASE(DT) \
-    case DT: k_encode_byte_wave<DT, ENC, BS, false><<<grid, BS, 0, stream>>>(in, out, n); break;
-            MFH_ENCODE_WAVE_CASE(kFloat64)
-            MFH_ENCODE_WAVE_CASE(kFloat32)
-            MFH_ENCODE_WAVE_CASE(kFloat16)
-            MFH_ENCODE_WAVE_CASE(kBFloat16)
-            MFH_ENCODE_WAVE_CASE(kInt64)
-            MFH_ENCODE_WAVE_CASE(kInt32)
-            MFH_ENCODE_WAVE_CASE(kInt16)
-            MFH_ENCODE_WAVE_CASE(kInt8)
-            MFH_ENCODE_WAVE_CASE(kUint64)
-            MFH_ENCODE_WAVE_CASE(kUint32)
-            MFH_ENCODE_WAVE_CASE(kUint16)
-            MFH_ENCODE_WAVE_CASE(kUint8)
+    case DT: k_encode_byte_wave<DT, ENC, BS><<<grid, BS, 0, stream>>>(in, out, n); break;
+        MFH_ENCODE_WAVE_CASE(kFloat64)
+        MFH_ENCODE_WAVE_CASE(kFloat32)
+        MFH_ENCODE_WAVE_CASE(kFloat16)
+        MFH_ENCODE_WAVE_CASE(kBFloat16)
+        MFH_ENCODE_WAVE_CASE(kInt64)
+        MFH_ENCODE_WAVE_CASE(kInt32)
+        MFH_ENCODE_WAVE_CASE(kInt16)
+        MFH_ENCODE_WAVE_CASE(kInt8)
+        MFH_ENCODE_WAVE_CASE(kUint64)
+        MFH_ENCODE_WAVE_CASE(kUint32)
+        MFH_ENCODE_WAVE_CASE(kUint16)
+        MFH_ENCODE_WAVE_CASE(kUint8)
 #undef MFH_ENCODE_WAVE_CASE
-        default:
-            return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
-        }
-        return launch_status("k_encode_byte_wave");
+    default:
+        return fail(MFH_ERR_DTYPE_UNSUPPORTED, "mfh_convert: input dtype %s is not supported", dtype_name(in_dt));
     }
+    return launch_status("k_encode_byte_wave");
 }
 
 template <int ENC>
@@ -652,19 +628,12 @@ int launch_encode_byte(const Device* dev, mfh_u8* out, const void* in, int in_dt
 {
     // unpacked numeric sources: whole 4 KiB source chunks per wave when the
     // source is 16-byte aligned and the output aligned for the kernel's
-    // stores (2-byte sources: 16 bytes for paired pieces, else 8)
+    // stores (16 / size bytes)
     const int size = in_dt == kF8E4M3 || in_dt == kF8E5M2 || in_dt == kInt4 ? 0 : dtype_size(in_dt);
-    if (size > 0 && aligned16(in)) {
-        const uintptr_t at = reinterpret_cast<uintptr_t>(out);
-        if (size == 2 && (at & 15) == 0)
-            return with_block(cast_threads(in_dt, 1), [&](auto block) {
-                return launch_encode_byte_wave<ENC, decltype(block)::value, true>(dev, out, in, in_dt, n, size, stream);
-            });
-        if ((at & (uintptr_t)(16 / size - 1)) == 0)
-            return with_block(cast_threads(in_dt, 1), [&](auto block) {
-                return launch_encode_byte_wave<ENC, decltype(block)::value, false>(dev, out, in, in_dt, n, size, stream);
-            });
-    }
+    if (size > 0 && aligned16(in) && (reinterpret_cast<uintptr_t>(out) & (uintptr_t)(16 / size - 1)) == 0)
+        return with_block(cast_threads(in_dt, 1), [&](auto block) {
+            return launch_encode_byte_wave<ENC, decltype(block)::value>(dev, out, in, in_dt, n, size, stream);
+        });
     const int vec_ok = aligned16(out) && n >= 16;
     const int64_t items = vec_ok ? n / 16 : n;
     const unsigned grid = grid_for(items, dev, Kern::kConvert);
