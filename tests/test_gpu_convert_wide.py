@@ -97,9 +97,8 @@ def test_wide_sources_tails_misaligned(in_dt, out_dt, n, pad):
 @pytest.mark.parametrize("out_pad", [0, 1, 2, 8, 16])
 @pytest.mark.parametrize("in_dt", [O.FLOAT16, O.INT16])
 def test_int8_from_2byte_sources_every_output_alignment(in_dt, out_pad):
-    # 2-byte sources pair two pieces per lane into one 16-byte store when the
-    # output is 16-byte aligned, write 8-byte stores when it is 8-byte
-    # aligned, and run the 16-element items otherwise
+    # 2-byte sources write one 8-byte store per 16-byte source piece when the
+    # output is 8-byte aligned and run the 16-element items otherwise
     n = 3 * 4096 + 37
     a = np.random.default_rng(out_pad).integers(0, 1 << 16, n, dtype=np.uint32).astype(np.uint16).view(NP_OF[in_dt])
     got = convert(a, in_dt, O.INT8, n, pad_out=out_pad)
