@@ -1056,9 +1056,8 @@ def summarize_pmc(fetch_dir, write_dir):
                       "runs of `python3 bench.py --profile 5`, median over the dispatches of each kernel), each "
                       f"scaled by what the counter reads for a 64 MiB f32 copy ({cal}): reads x{rscale:.4f}, "
                       f"writes x{wscale:.4f}. Summarised by `python3 bench.py --summarize-pmc FETCH_DIR WRITE_DIR`."),
-           "commands": [f"rocprofv3 --pmc {c} -f csv -d $GRAFT_REPO_ROOT/gpurun_out/prof/{d} -o run -- "
-                        "python3 $GRAFT_REPO_ROOT/bench.py --profile 5" for c, d in (("FETCH_SIZE", "fetch"),
-                                                                                     ("WRITE_SIZE", "write"))],
+           "commands": [f"rocprofv3 --pmc {c} -f csv -d {d} -o run -- python3 bench.py --profile 5"
+                        for c, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir))],
            "calibration": {"kernel": cal + " (f32 copy)", "bytes_read": copy_bytes, "bytes_written": copy_bytes,
                            "FETCH_SIZE_KiB": fetch[cal], "WRITE_SIZE_KiB": write[cal],
                            "read_scale": rscale, "write_scale": wscale},
