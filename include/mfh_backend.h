@@ -136,8 +136,12 @@ int mfh_tensor_sync(mfh_tensor* tensor);
 int mfh_tensor_slice(const mfh_tensor* tensor, int64_t start, int64_t length, mfh_tensor** view);
 int mfh_tensor_reshape(const mfh_tensor* tensor, const int64_t* dims, int32_t rank, mfh_tensor** view);
 
-/* Tensor.Close: waits, then frees storage this tensor owns.  Idempotent.
- * mfh_tensor_release also frees the handle. */
+/* Tensor.Close: waits for the device to finish every queued use, then
+ * returns the storage this tensor owns to its backend.  The backend keeps up
+ * to 2 GiB of such blocks for later tensors of the same byte size (an
+ * upload then skips hipMalloc) and frees them when an allocation fails and
+ * at mfh_backend_close.  Idempotent.  mfh_tensor_release also frees the
+ * handle. */
 int mfh_tensor_close(mfh_tensor* tensor);
 int mfh_tensor_release(mfh_tensor* tensor);
 

@@ -14,6 +14,7 @@
 // so a stale tensor reports closed instead of touching freed memory.
 #include <algorithm>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <set>
@@ -51,8 +52,54 @@ struct BackendState {
     void* dstage[kRing] = {nullptr, nullptr};
     hipEvent_t slot_free[kRing] = {nullptr, nullptr};
     std::set<std::shared_ptr<Storage>> owned;
+    // Device blocks of closed tensors, kept for later tensors of the same
+    // byte size: a hipMalloc of a 117 MB tensor took about a tenth of its
+    // PCIe upload.  A block enters only after every queued use of it has
+    // finished (a close waits for that), so a new tensor gets idle memory.
+    // At most kCacheCap bytes are kept; hipMalloc failure and shutdown
+    // return them.
+    static constexpr size_t kCacheCap = size_t(2) << 30;
+    std::multimap<size_t, void*> cache;
+    size_t cached = 0;
 
     ~BackendState() { shut(); }
+
+    int alloc(size_t bytes, void** p)
+    {
+        auto it = cache.find(bytes);
+        if (it != cache.end()) {
+            *p = it->second;
+            cached -= bytes;
+            cache.erase(it);
+            return MFH_OK;
+        }
+        if (hipMalloc(p, bytes) == hipSuccess) return MFH_OK;
+        (void)hipGetLastError();
+        trim(0);
+        return check_hip(hipMalloc(p, bytes), "hipMalloc");
+    }
+
+    // `p` must be idle: no queued work may still touch it.
+    int release(void* p, size_t bytes)
+    {
+        if (bytes > kCacheCap) return check_hip(hipFree(p), "hipFree");
+        cache.emplace(bytes, p);
+        cached += bytes;
+        return trim(kCacheCap);
+    }
+
+    int trim(size_t cap)
+    {
+        int rc = MFH_OK;
+        while (cached > cap && !cache.empty()) {
+            auto it = cache.begin();  // smallest first: the big blocks are the expensive ones to remake
+            const int r = check_hip(hipFree(it->second), "hipFree");
+            if (rc == MFH_OK) rc = r;
+            cached -= it->first;
+            cache.erase(it);
+        }
+        return rc;
+    }
 
     // Frees everything; storage handles left in tensors see `freed`.
     int shut()
@@ -76,6 +123,7 @@ struct BackendState {
             s->pending = false;
         }
         owned.clear();
+        keep(trim(0) == MFH_OK ? hipSuccess : hipErrorUnknown, "hipFree(block cache)");
         for (int i = 0; i < kRing; i++) {
             if (pinned[i]) keep(hipHostFree(pinned[i]), "hipHostFree");
             if (dstage[i]) keep(hipFree(dstage[i]), "hipFree");
@@ -307,7 +355,7 @@ int upload_from(mfh_backend* b, const int64_t* shape, int32_t rank, const Plan& 
                     n_bytes, (long long)t->elements, dtype_string(plan.src), (long long)expected);
     auto st = std::make_shared<Storage>();
     st->bytes = (size_t)t->elements * dtype_size(plan.out);
-    if (st->bytes) MFH_TRY(check_hip(hipMalloc(&st->ptr, st->bytes), "hipMalloc"));
+    if (st->bytes) MFH_TRY(s.alloc(st->bytes, &st->ptr));
     int rc = stream_in(s, plan, source, n_bytes, t->elements, *st);
     if (rc == MFH_OK) rc = check_hip(hipEventCreateWithFlags(&st->done, hipEventDisableTiming), "hipEventCreate");
     if (rc == MFH_OK) rc = check_hip(hipEventRecord(st->done, s.stream), "hipEventRecord");
@@ -615,9 +663,13 @@ int mfh_tensor_close(mfh_tensor* t)
     if (st.done) (void)hipEventDestroy(st.done);
     st.done = nullptr;
     if (st.ptr) {
-        // work queued on the backend stream may still read it
-        if (t->backend->stream) (void)hipStreamSynchronize(t->backend->stream);
-        int frc = check_hip(hipFree(st.ptr), "hipFree");
+        // Work on any stream may still use the block, including the
+        // caller's own launches on its dispatch pointer: the device-wide
+        // wait that hipFree would make first makes it idle, and an idle block
+        // goes to the backend's cache.
+        int frc = check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        frc = frc == MFH_OK && rc == MFH_OK ? t->backend->release(st.ptr, st.bytes)
+                                            : check_hip(hipFree(st.ptr), "hipFree");
         if (rc == MFH_OK) rc = frc;
     }
     st.ptr = nullptr;
@@ -727,7 +779,7 @@ int mfh_backend_graph_call(mfh_backend* backend, mfh_graph* graph, const char* c
         t->storage->bytes = (size_t)n * dtype_size(dt);
         made.push_back(std::move(t));
         Storage& st = *made.back()->storage;
-        if (st.bytes && (rc = check_hip(hipMalloc(&st.ptr, st.bytes), "hipMalloc")) != MFH_OK) return undo(rc);
+        if (st.bytes && (rc = s.alloc(st.bytes, &st.ptr)) != MFH_OK) return undo(rc);
         outs[j] = mfh_value{output_keys[j], st.ptr, dt, {0}, n};
     }
     // Order after work still queued on the inputs (uploads, axpys, earlier

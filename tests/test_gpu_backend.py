@@ -216,6 +216,35 @@ def test_axpy_through_another_backend():
         a.release()
 
 
+def test_closed_blocks_are_reused_for_the_same_size():
+    # a closed tensor's block returns to its backend's cache and the next
+    # tensor of the same byte size gets it, with its own contents
+    b = Backend(0)
+    try:
+        rng = np.random.default_rng(41)
+        n = 3 * CHUNK // 4 + 5  # f32: several staging chunks
+        first = rng.normal(0, 1, n).astype(np.float32)
+        t = b.upload([n], O.FLOAT32, first)
+        p = t.dispatch_pointer()
+        t.release()
+        second = rng.normal(0, 1, n).astype(np.float32)
+        u = b.upload([n], O.FLOAT32, second)  # same bytes: the cached block
+        assert u.dispatch_pointer() == p
+        v = b.upload([n + 1], O.FLOAT32, np.ones(n + 1, np.float32))  # another size: a new block
+        assert v.dispatch_pointer() != p
+        assert b.download(u)[1] == second.tobytes()
+        # an FP8 upload stored as bf16 takes a block of its stored size
+        codes = rng.integers(0, 256, 2 * n, dtype=np.uint8)
+        u.release()
+        w = b.upload([2 * n], O.F8E4M3, codes)  # 2n bf16 = the f32 block's bytes
+        assert w.dispatch_pointer() == p
+        assert b.download(w)[1] == O.bytes_to_bf16(O.F8E4M3, codes).tobytes()
+        v.release()
+        w.release()
+    finally:
+        b.release()
+
+
 def test_backend_close_invalidates_tensors():
     b = Backend(0)
     t = b.upload([4], O.FLOAT32, np.ones(4, np.float32))
