@@ -1263,9 +1263,6 @@ int graph_call_noalloc(Graph& g, const mfh_value* inputs, int32_t n_inputs, cons
     return launch_all(g, P, topo, 1, stream, base, false);
 }
 
-// compiler.PlanGraph (compiler/plan.go:242-290): buildPlanningTopology
-// (:29-90), PlanWorkspace, attachGraphIOPorts (:179-228), ScheduleStreams.
-// The graph is taken in its own order (graph calls need it topological).
 // The dtype and element count a call with these inputs gives output `key`,
 // by prepare()'s rules, from the inputs' names, dtypes and counts alone.
 int output_shape(Graph& g, const mfh_value* inputs, int32_t n_inputs, const std::string& key, uint8_t* dtype,
@@ -1287,6 +1284,9 @@ int output_shape(Graph& g, const mfh_value* inputs, int32_t n_inputs, const std:
     return MFH_OK;
 }
 
+// compiler.PlanGraph (compiler/plan.go:242-290): buildPlanningTopology
+// (:29-90), PlanWorkspace, attachGraphIOPorts (:179-228), ScheduleStreams.
+// The graph is taken in its own order (graph calls need it topological).
 int plan_graph(Graph& g, const mfh_value* inputs, int32_t n_inputs, int64_t align, int32_t max_streams, Topology* t)
 {
     Prepared P;
