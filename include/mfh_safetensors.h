@@ -13,6 +13,8 @@
  * through the backend's pinned staging ring (pread into a pinned chunk while
  * the previous chunk's DMA and dequant run) without reading the whole file
  * into host memory; FP8 / Int4 tensors arrive dequantised.
+ * mfh_safetensors_load_async queues the same load and returns once the file
+ * has been read.
  */
 #ifndef MFH_SAFETENSORS_H
 #define MFH_SAFETENSORS_H
@@ -69,6 +71,17 @@ int mfh_safetensors_read(const mfh_safetensors* file, const char* name, void* ds
  * other dtypes fail with MFH_ERR_DTYPE_UNSUPPORTED. */
 int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_backend* backend,
                          const char* scale_name, int64_t group, mfh_tensor** tensor);
+
+/* The same load as Backend.UploadAsync (tensor/backend.go:37-40) would make
+ * it: returns once the file has been read and every chunk is queued, with
+ * the tensor MFH_STATE_PENDING until its last DMA and dequant have run
+ * (mfh_tensor_sync, mfh_backend_download and mfh_tensor_close wait for it).
+ * Loads queued back to back keep the staging ring running across tensor
+ * boundaries: the file read of one tensor's first chunk overlaps the DMA and
+ * dequant of the previous tensor's last chunk, which a synchronous load
+ * waits out. */
+int mfh_safetensors_load_async(const mfh_safetensors* file, const char* name, mfh_backend* backend,
+                               const char* scale_name, int64_t group, mfh_tensor** tensor);
 
 #ifdef __cplusplus
 }

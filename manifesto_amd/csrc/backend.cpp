@@ -51,6 +51,10 @@ struct BackendState {
     void* pinned[kRing] = {nullptr, nullptr};
     void* dstage[kRing] = {nullptr, nullptr};
     hipEvent_t slot_free[kRing] = {nullptr, nullptr};
+    // The slot the next chunk takes.  It carries over from one upload to the
+    // next, so the first chunk of an upload queued behind an asynchronous one
+    // fills the slot that upload's last chunk is not using.
+    int next_slot = 0;
     std::set<std::shared_ptr<Storage>> owned;
     // Device blocks of closed tensors, kept for later tensors of the same
     // byte size: a hipMalloc of a 117 MB tensor took about a tenth of its
@@ -251,8 +255,9 @@ int stream_in(BackendState& s, const Plan& p, Source& src, size_t n_src, int64_t
     }
     const int out_size = dtype_size(p.out);
     size_t done = 0;
-    for (int c = 0; done < n_src; c++) {
-        const int slot = c % kRing;
+    while (done < n_src) {
+        const int slot = s.next_slot;
+        s.next_slot = (slot + 1) % kRing;
         const size_t len = std::min(chunk, n_src - done);
         int64_t first = 0, count = 0;  // elements of this chunk
         if (p.src == kInt4) {

@@ -598,8 +598,12 @@ int mfh_safetensors_read(const mfh_safetensors* file, const char* name, void* ds
     return MFH_OK;
 }
 
-int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_backend* backend, const char* scale_name,
-                         int64_t group, mfh_tensor** tensor)
+}  // extern "C"
+
+namespace {
+
+int load(const mfh_safetensors* file, const char* name, mfh_backend* backend, const char* scale_name, int64_t group,
+         bool wait, mfh_tensor** tensor)
 {
     if (tensor) *tensor = nullptr;
     const Entry* e = find(file, name);
@@ -651,7 +655,23 @@ int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_back
         p.scale_dt = se->dtype;
         p.group = group;
     }
-    return upload_from(backend, e->shape.data(), (int32_t)e->shape.size(), p, src, len, true, tensor);
+    return upload_from(backend, e->shape.data(), (int32_t)e->shape.size(), p, src, len, wait, tensor);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mfh_safetensors_load(const mfh_safetensors* file, const char* name, mfh_backend* backend, const char* scale_name,
+                         int64_t group, mfh_tensor** tensor)
+{
+    return load(file, name, backend, scale_name, group, true, tensor);
+}
+
+int mfh_safetensors_load_async(const mfh_safetensors* file, const char* name, mfh_backend* backend,
+                               const char* scale_name, int64_t group, mfh_tensor** tensor)
+{
+    return load(file, name, backend, scale_name, group, false, tensor);
 }
 
 }  // extern "C"

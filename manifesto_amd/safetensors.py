@@ -36,6 +36,7 @@ def _L():
             "mfh_safetensors_find": (i32, [vp, cp]),
             "mfh_safetensors_read": (c.c_int, [vp, cp, vp, sz, c.POINTER(sz)]),
             "mfh_safetensors_load": (c.c_int, [vp, cp, vp, cp, i64, c.POINTER(vp)]),
+            "mfh_safetensors_load_async": (c.c_int, [vp, cp, vp, cp, i64, c.POINTER(vp)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -83,13 +84,20 @@ class SafeTensorsFile:
         check(L.mfh_safetensors_read(self._h, name.encode(), buf, n.value, ctypes.byref(n)))
         return buf.raw[:n.value]
 
-    def load(self, name: str, backend: Backend, scale: str | None = None, group: int = 0) -> Tensor:
-        """Streams one tensor onto `backend` (FP8 / I4 dequantised)."""
+    def _load(self, fn, name, backend, scale, group) -> Tensor:
         _backend_L()
         h = ctypes.c_void_p()
-        check(_L().mfh_safetensors_load(self._h, name.encode(), backend._h,
-                                        scale.encode() if scale else None, group, ctypes.byref(h)))
+        check(fn(self._h, name.encode(), backend._h, scale.encode() if scale else None, group, ctypes.byref(h)))
         return Tensor(backend, h)
+
+    def load(self, name: str, backend: Backend, scale: str | None = None, group: int = 0) -> Tensor:
+        """Streams one tensor onto `backend` (FP8 / I4 dequantised)."""
+        return self._load(_L().mfh_safetensors_load, name, backend, scale, group)
+
+    def load_async(self, name: str, backend: Backend, scale: str | None = None, group: int = 0) -> Tensor:
+        """The same load, returned once the file has been read; the tensor is
+        pending until its transfer and dequant have run (Tensor.sync)."""
+        return self._load(_L().mfh_safetensors_load_async, name, backend, scale, group)
 
     def close(self) -> None:
         if getattr(self, "_h", None):

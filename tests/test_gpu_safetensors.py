@@ -138,6 +138,50 @@ def test_load_many_grouped_int4_tensors(backend, tmp_path):
         t.release()
 
 
+def test_async_loads_back_to_back(backend, tmp_path):
+    # Loads queued one after another without a wait: the staging ring runs
+    # on across tensor boundaries (tensors of 1, 2 and 3 chunks, so the next
+    # load starts on either slot), a download and a synchronous load come in
+    # between, and every tensor matches the oracle and its synchronous load.
+    rng = np.random.default_rng(3)
+    codes = rng.integers(0, 256, 40 * (1 << 20) + 3, dtype=np.uint8)   # 3 chunks
+    f32 = rng.normal(0, 1, 5 * (1 << 20) + 7).astype(np.float32)        # 2 chunks
+    bf16 = O.f32_to_bf16(rng.normal(0, 1, 1001).astype(np.float32))     # 1 chunk
+    e5 = rng.integers(0, 256, 17 * (1 << 20), dtype=np.uint8)           # 2 chunks
+    rows, cols, group = 2048, 4096, 128
+    packed = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+    s16 = O.f32_to_f16(rng.uniform(0.005, 0.02, rows * cols // group).astype(np.float32))
+    scale = np.array([0.0125], np.float32)
+    f = SafeTensorsFile(write(tmp_path / "a.safetensors", {
+        "q": ("F8_E4M3", [codes.size], codes.tobytes()), "q_scale": ("F32", [], scale.tobytes()),
+        "f": ("F32", [f32.size], f32.tobytes()), "b": ("BF16", [1001], bf16.tobytes()),
+        "k": ("F8_E5M2", [e5.size], e5.tobytes()),
+        "w": ("I4", [rows, cols], packed.tobytes()), "w_scales": ("F16", [rows, cols // group], s16.tobytes())}))
+    want = {"q": O.dequant_fp8(codes, O.F8E4M3, 0.0125, O.BFLOAT16).tobytes(), "f": f32.tobytes(),
+            "b": bf16.tobytes(), "k": O.bytes_to_bf16(O.F8E5M2, e5).tobytes(),
+            "w": O.dequant_int4(packed, rows * cols, s16, O.FLOAT16, group, O.BFLOAT16).tobytes()}
+    scales = {"q": ("q_scale", 0), "w": ("w_scales", group)}
+    order = ["q", "b", "f", "w", "k", "q", "w", "b", "f"]
+    tensors = []
+    for i, name in enumerate(order):
+        sc, g = scales.get(name, (None, 0))
+        tensors.append((name, f.load_async(name, backend, scale=sc, group=g)))
+        if i == 4:
+            # a download and a synchronous load between queued loads
+            assert backend.download(tensors[1][1])[1] == want["b"]
+            t = f.load("f", backend)
+            assert backend.download(t)[1] == want["f"]
+            t.release()
+    for name, t in tensors:
+        assert t.state() in (0, 1)  # ready or pending
+    for name, t in tensors:
+        t.sync()
+        assert t.state() == 0
+        assert backend.download(t)[1] == want[name], name
+        t.release()
+    log("safetensors: async loads back to back match the oracle")
+
+
 @pytest.mark.parametrize("group, n", [(7, 40 * (1 << 20) + 5), (1, 14 * (1 << 20) + 1), (96, 33 * (1 << 20) + 2),
                                       (4096, 3 * (1 << 22) + 77)])
 def test_grouped_int4_across_staging_chunks(backend, tmp_path, group, n):
