@@ -650,8 +650,8 @@ def pcie_run(M, O):
     and config 5's Int4 tensor with its f16 group scales (dequantised on the
     device while the next chunk crosses PCIe), a 134 MB f32 upload and
     download, and the same FP8 / Int4 tensors loaded from a SafeTensors
-    file, one synchronous load after another and all four queued with
-    load_async before the first wait.  Source bytes per second: the first pass over four tensors on a
+    file, one synchronous upload or load after another and all four queued
+    (the queued uploads, load_async) before the first wait.  Source bytes per second: the first pass over four tensors on a
     fresh backend (every output allocated with hipMalloc) and the best of
     three more passes, whose outputs come from the blocks the previous
     pass's closed tensors left in the backend's cache."""
@@ -667,6 +667,13 @@ def pcie_run(M, O):
     codes = [rng.integers(0, 256, 4096 * 14336, dtype=np.uint8) for _ in range(4)]
     f32 = rng.standard_normal(1 << 25).astype(np.float32)
     int4_bytes = 4 * (packed[0].nbytes + s16[0].nbytes)
+
+    def queued(ts):
+        # every upload queued first, then each waited for: the clock stops
+        # once all four are resident
+        for t in ts:
+            t.sync()
+        return ts
 
     def rate(fn, nbytes, what):
         bb = Backend(0)  # an empty block cache
@@ -691,6 +698,12 @@ def pcie_run(M, O):
          4 * codes[0].nbytes, "upload_fp8 e4m3 -> bf16, 4 x [4096,14336] from host memory")
     rate(lambda bb: [bb.upload_int4([rows, cols], packed[k], s16[k], O.FLOAT16, group) for k in range(4)],
          int4_bytes, "upload_int4 + f16 scales -> bf16, 4 x [14336,4096] from host memory")
+    rate(lambda bb: queued([bb.upload_fp8([4096, 14336], O.F8E4M3, codes[k], 0.0125, queued=True)
+                            for k in range(4)]),
+         4 * codes[0].nbytes, "upload_fp8 e4m3 -> bf16, 4 x [4096,14336] from host memory, queued")
+    rate(lambda bb: queued([bb.upload_int4([rows, cols], packed[k], s16[k], O.FLOAT16, group, queued=True)
+                            for k in range(4)]),
+         int4_bytes, "upload_int4 + f16 scales -> bf16, 4 x [14336,4096] from host memory, queued")
     rate(lambda bb: [bb.upload([f32.size], O.FLOAT32, f32)], f32.nbytes, "upload f32, 134 MB")
     t = b.upload([f32.size], O.FLOAT32, f32)
     out = bytearray(f32.nbytes)
@@ -723,13 +736,6 @@ def pcie_run(M, O):
              "SafeTensors F8_E4M3 -> bf16, 4 tensors (page cache warm)")
         rate(lambda bb: [sf.load(f"w{k}", bb, scale=f"w{k}_s", group=group) for k in range(4)], int4_bytes,
              "SafeTensors I4 + F16 scales -> bf16, 4 tensors (page cache warm)")
-
-        def queued(ts):
-            # every load queued first, then each waited for: the clock stops
-            # once all four are resident
-            for t in ts:
-                t.sync()
-            return ts
         rate(lambda bb: queued([sf.load_async(f"q{k}", bb) for k in range(4)]), 4 * codes[0].nbytes,
              "SafeTensors F8_E4M3 -> bf16, 4 tensors queued with load_async (page cache warm)")
         rate(lambda bb: queued([sf.load_async(f"w{k}", bb, scale=f"w{k}_s", group=group) for k in range(4)]),

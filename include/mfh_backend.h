@@ -96,6 +96,19 @@ int mfh_backend_upload_int4(mfh_backend* backend, const int64_t* shape, int32_t 
                             size_t n_bytes, const void* group_scales, uint8_t scale_dtype, int64_t group,
                             uint8_t out_dtype, mfh_tensor** tensor);
 
+/* The same uploads with UploadAsync's return: once the source bytes (and the
+ * group scales) have been copied into the staging ring and every chunk is
+ * queued, so the host buffers may be reused; the tensor is
+ * MFH_STATE_PENDING until its last chunk has been dequantised.  Uploads
+ * queued back to back share one staging pipeline: the copy of a tensor's
+ * first chunk overlaps the DMA and dequant of the previous tensor's last. */
+int mfh_backend_upload_fp8_async(mfh_backend* backend, const int64_t* shape, int32_t rank, uint8_t fp8_dtype,
+                                 const void* codes, size_t n_bytes, float scale, uint8_t out_dtype,
+                                 mfh_tensor** tensor);
+int mfh_backend_upload_int4_async(mfh_backend* backend, const int64_t* shape, int32_t rank, const void* packed,
+                                  size_t n_bytes, const void* group_scales, uint8_t scale_dtype, int64_t group,
+                                  uint8_t out_dtype, mfh_tensor** tensor);
+
 /* Backend.Download (tensor/backend.go:59): waits for the tensor, copies its
  * storage to `dst` (capacity `dst_bytes`) and reports the storage dtype and
  * byte count.  Tensor.RawBytes goes through it. */

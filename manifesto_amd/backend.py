@@ -46,6 +46,8 @@ def _L():
             "mfh_backend_upload_sparse": (c.c_int, [vp]),
             "mfh_backend_upload_fp8": (c.c_int, [vp, shp, i32, u8, vp, sz, c.c_float, u8, c.POINTER(vp)]),
             "mfh_backend_upload_int4": (c.c_int, [vp, shp, i32, vp, sz, vp, u8, i64, u8, c.POINTER(vp)]),
+            "mfh_backend_upload_fp8_async": (c.c_int, [vp, shp, i32, u8, vp, sz, c.c_float, u8, c.POINTER(vp)]),
+            "mfh_backend_upload_int4_async": (c.c_int, [vp, shp, i32, vp, sz, vp, u8, i64, u8, c.POINTER(vp)]),
             "mfh_backend_download": (c.c_int, [vp, vp, c.POINTER(u8), vp, sz, c.POINTER(sz)]),
             "mfh_backend_close": (c.c_int, [vp]),
             "mfh_backend_release": (c.c_int, [vp]),
@@ -192,22 +194,26 @@ class Backend:
     def upload_sparse(self):
         check(_L().mfh_backend_upload_sparse(self._h))
 
-    def upload_fp8(self, dims, fp8_dtype: int, codes, scale: float, out_dtype: int = abi.BFLOAT16) -> Tensor:
+    def upload_fp8(self, dims, fp8_dtype: int, codes, scale: float, out_dtype: int = abi.BFLOAT16,
+                   queued: bool = False) -> Tensor:
+        """Scaled FP8 upload; `queued` returns once the codes are staged and
+        every chunk is queued (the tensor pending until it has run)."""
+        fn = _L().mfh_backend_upload_fp8_async if queued else _L().mfh_backend_upload_fp8
         arr, rank = _shape(dims)
         ptr, nbytes, keep = _buf(codes)
         h = ctypes.c_void_p()
-        check(_L().mfh_backend_upload_fp8(self._h, arr, rank, fp8_dtype, ptr, nbytes, scale, out_dtype,
-                                          ctypes.byref(h)))
+        check(fn(self._h, arr, rank, fp8_dtype, ptr, nbytes, scale, out_dtype, ctypes.byref(h)))
         return Tensor(self, h)
 
     def upload_int4(self, dims, packed, scales, scale_dtype: int, group: int,
-                    out_dtype: int = abi.BFLOAT16) -> Tensor:
+                    out_dtype: int = abi.BFLOAT16, queued: bool = False) -> Tensor:
+        """Int4 upload with per-group scales; `queued` as for upload_fp8."""
+        fn = _L().mfh_backend_upload_int4_async if queued else _L().mfh_backend_upload_int4
         arr, rank = _shape(dims)
         ptr, nbytes, keep = _buf(packed)
         sptr, _, skeep = _buf(scales)
         h = ctypes.c_void_p()
-        check(_L().mfh_backend_upload_int4(self._h, arr, rank, ptr, nbytes, sptr, scale_dtype, group, out_dtype,
-                                           ctypes.byref(h)))
+        check(fn(self._h, arr, rank, ptr, nbytes, sptr, scale_dtype, group, out_dtype, ctypes.byref(h)))
         return Tensor(self, h)
 
     def download(self, tensor: Tensor, out=None):

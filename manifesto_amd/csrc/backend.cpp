@@ -474,8 +474,12 @@ int mfh_backend_upload_sparse(mfh_backend* backend)
     return fail(MFH_ERR_LAYOUT_UNSUPPORTED, "tensor: layout not supported");
 }
 
-int mfh_backend_upload_fp8(mfh_backend* backend, const int64_t* shape, int32_t rank, uint8_t fp8_dtype,
-                           const void* codes, size_t n_bytes, float scale, uint8_t out_dtype, mfh_tensor** tensor)
+}  // extern "C"
+
+namespace {
+
+int upload_fp8(mfh_backend* backend, const int64_t* shape, int32_t rank, uint8_t fp8_dtype, const void* codes,
+               size_t n_bytes, float scale, uint8_t out_dtype, bool wait, mfh_tensor** tensor)
 {
     if (tensor) *tensor = nullptr;
     if (fp8_dtype != kF8E4M3 && fp8_dtype != kF8E5M2)
@@ -486,12 +490,12 @@ int mfh_backend_upload_fp8(mfh_backend* backend, const int64_t* shape, int32_t r
     p.src = fp8_dtype;
     p.out = out_dtype;
     p.scale = scale;
-    return upload(backend, shape, rank, p, codes, n_bytes, true, tensor);
+    return upload(backend, shape, rank, p, codes, n_bytes, wait, tensor);
 }
 
-int mfh_backend_upload_int4(mfh_backend* backend, const int64_t* shape, int32_t rank, const void* packed,
-                            size_t n_bytes, const void* group_scales, uint8_t scale_dtype, int64_t group,
-                            uint8_t out_dtype, mfh_tensor** tensor)
+int upload_int4(mfh_backend* backend, const int64_t* shape, int32_t rank, const void* packed, size_t n_bytes,
+                const void* group_scales, uint8_t scale_dtype, int64_t group, uint8_t out_dtype, bool wait,
+                mfh_tensor** tensor)
 {
     if (tensor) *tensor = nullptr;
     const Device* dev;
@@ -513,7 +517,40 @@ int mfh_backend_upload_int4(mfh_backend* backend, const int64_t* shape, int32_t 
     p.scales = &scales;
     p.scale_dt = scale_dtype;
     p.group = group;
-    return upload(backend, shape, rank, p, packed, n_bytes, true, tensor);
+    return upload(backend, shape, rank, p, packed, n_bytes, wait, tensor);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mfh_backend_upload_fp8(mfh_backend* backend, const int64_t* shape, int32_t rank, uint8_t fp8_dtype,
+                           const void* codes, size_t n_bytes, float scale, uint8_t out_dtype, mfh_tensor** tensor)
+{
+    return upload_fp8(backend, shape, rank, fp8_dtype, codes, n_bytes, scale, out_dtype, true, tensor);
+}
+
+int mfh_backend_upload_fp8_async(mfh_backend* backend, const int64_t* shape, int32_t rank, uint8_t fp8_dtype,
+                                 const void* codes, size_t n_bytes, float scale, uint8_t out_dtype,
+                                 mfh_tensor** tensor)
+{
+    return upload_fp8(backend, shape, rank, fp8_dtype, codes, n_bytes, scale, out_dtype, false, tensor);
+}
+
+int mfh_backend_upload_int4(mfh_backend* backend, const int64_t* shape, int32_t rank, const void* packed,
+                            size_t n_bytes, const void* group_scales, uint8_t scale_dtype, int64_t group,
+                            uint8_t out_dtype, mfh_tensor** tensor)
+{
+    return upload_int4(backend, shape, rank, packed, n_bytes, group_scales, scale_dtype, group, out_dtype, true,
+                       tensor);
+}
+
+int mfh_backend_upload_int4_async(mfh_backend* backend, const int64_t* shape, int32_t rank, const void* packed,
+                                  size_t n_bytes, const void* group_scales, uint8_t scale_dtype, int64_t group,
+                                  uint8_t out_dtype, mfh_tensor** tensor)
+{
+    return upload_int4(backend, shape, rank, packed, n_bytes, group_scales, scale_dtype, group, out_dtype, false,
+                       tensor);
 }
 
 int mfh_backend_download(mfh_backend* backend, const mfh_tensor* tensor, uint8_t* dtype, void* dst, size_t dst_bytes,

@@ -138,6 +138,42 @@ def test_async_upload_and_sync(backend):
     assert backend.download(t)[1] == data.tobytes()
 
 
+def test_queued_scaled_uploads_back_to_back(backend):
+    # Scaled FP8 and grouped Int4 uploads queued without a wait (tensors of
+    # 1 to 3 staging chunks, so each starts on either ring slot), their host
+    # buffers overwritten as soon as each call returns: every tensor matches
+    # the oracle.
+    rng = np.random.default_rng(11)
+    rows, cols, group = 1024, 8192, 128
+    cases = []
+    for k, n_codes in enumerate([2 * CHUNK + 77, CHUNK // 3, CHUNK + 5]):
+        codes = rng.integers(0, 256, n_codes, dtype=np.uint8)
+        cases.append(("fp8", codes.copy(), O.dequant_fp8(codes, O.F8E5M2 if k % 2 else O.F8E4M3, -0.75,
+                                                           O.BFLOAT16), k % 2))
+        packed = rng.integers(0, 256, rows * cols // 2 * (k + 1), dtype=np.uint8)
+        s16 = O.f32_to_f16(rng.uniform(0.005, 0.02, rows * cols * (k + 1) // group).astype(np.float32))
+        cases.append(("int4", (packed.copy(), s16.copy()),
+                      O.dequant_int4(packed, rows * cols * (k + 1), s16, O.FLOAT16, group, O.BFLOAT16), k))
+    tensors = []
+    for kind, src, want, k in cases:
+        if kind == "fp8":
+            t = backend.upload_fp8([src.size], O.F8E5M2 if k else O.F8E4M3, src, -0.75, O.BFLOAT16, queued=True)
+            src[:] = 0
+        else:
+            packed, s16 = src
+            t = backend.upload_int4([rows * (k + 1), cols], packed, s16, O.FLOAT16, group, O.BFLOAT16, queued=True)
+            packed[:] = 0
+            s16[:] = 0
+        assert t.state() in (STATE_PENDING, STATE_READY)
+        tensors.append((t, want))
+    for t, want in tensors:
+        t.sync()
+        assert t.state() == STATE_READY
+        np.testing.assert_array_equal(np.frombuffer(backend.download(t)[1], np.uint16), want)
+        t.release()
+    log("queued scaled uploads match the oracle")
+
+
 def test_views_and_lifecycle(backend):
     data = np.arange(24, dtype=np.float32)
     t = backend.upload([2, 3, 4], O.FLOAT32, data)
