@@ -231,6 +231,20 @@ int mfh_fusion_launch(const mfh_kernel* kernel, const void* const* inputs, int32
 
 int mfh_fusion_release(mfh_kernel* kernel);
 
+/* A directory where compiled kernels are kept between processes (no
+ * counterpart in the reference, whose CPU and Metal kernels need no compile
+ * step; for processes that would otherwise pay hiprtc's 0.3-2 s per distinct
+ * kernel at every start).  A compile first looks for a file written by an
+ * identical earlier compile (same hiprtc version, options and source text,
+ * checked byte for byte) and otherwise writes one.  NULL or "" turns it off.
+ * Default: the MFH_KERNEL_CACHE_DIR environment variable, else off.  The
+ * directory must exist and be trusted like any code the process loads. */
+int mfh_fusion_cache_dir(const char* dir);
+
+/* Kernels compiled by hiprtc and kernels read from the cache directory since
+ * the process started. */
+int mfh_fusion_cache_stats(int64_t* compiles, int64_t* disk_hits);
+
 #ifdef __cplusplus
 }
 #endif

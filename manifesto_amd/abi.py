@@ -91,6 +91,8 @@ def _declare(L):
         "mfh_fusion_num_inputs": (i32, [vp]),
         "mfh_fusion_launch": (c.c_int, [vp, c.POINTER(vp), i32, vp, i64, vp]),
         "mfh_fusion_release": (c.c_int, [vp]),
+        "mfh_fusion_cache_dir": (c.c_int, [c.c_char_p]),
+        "mfh_fusion_cache_stats": (c.c_int, [c.POINTER(i64), c.POINTER(i64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -178,6 +180,19 @@ def linspace(out: int, out_dtype: int, count: int, start: float, stop: float, en
 
 
 # ---- fused kernels -----------------------------------------------------------
+
+def fusion_cache_dir(path) -> None:
+    """Keeps compiled kernels in directory `path` between processes (None
+    turns it off)."""
+    check(lib().mfh_fusion_cache_dir(os.fsencode(path) if path else None))
+
+
+def fusion_cache_stats() -> tuple:
+    """(kernels compiled by hiprtc, kernels read from the cache directory)."""
+    compiles, hits = ctypes.c_int64(), ctypes.c_int64()
+    check(lib().mfh_fusion_cache_stats(ctypes.byref(compiles), ctypes.byref(hits)))
+    return compiles.value, hits.value
+
 
 class FusedKernel:
     """One compiled FusionAST (the HIP codegen target).

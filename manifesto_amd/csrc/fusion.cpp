@@ -16,10 +16,15 @@
 // every Add/Sub/Mul/Div rounds on its own as in Go, and cached by its text.
 #include <hip/hiprtc.h>
 
+#include <unistd.h>
+
 #include <atomic>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
+#include <string>
 #include <unordered_map>
 #include <vector>
 
@@ -193,6 +198,124 @@ std::unordered_map<std::string, std::shared_ptr<CodeObject>> g_cache;
 // handles (captured graph calls) know theirs may be gone.
 std::atomic<uint64_t> g_module_generation{0};
 
+const char* const kCompileOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                                       "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature",
+                                       "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-kernarg-preload-count=16"};
+
+// ---- compiled code kept on disk between processes ----------------------------
+//
+// One file per kernel, named by a hash of what produced it.  A file holds the
+// compiler identity (hiprtc version and options), the full kernel source and
+// the code object, followed by a checksum; it is used only when identity and
+// source match this compile exactly and the checksum holds, so a hash
+// collision, a stale or a truncated file costs a compile and nothing else.
+// Files are written under a temporary name and renamed into place, so
+// processes sharing the directory never read a partial file.  The directory
+// must be trusted like any code the process loads.
+
+std::mutex g_disk_mu;
+std::string g_disk_dir;
+bool g_disk_dir_set = false;
+std::atomic<int64_t> g_disk_hits{0}, g_compiles{0};
+
+constexpr char kDiskMagic[8] = {'M', 'F', 'H', 'K', 'O', 'D', 'E', '1'};
+constexpr uint64_t kDiskMaxBytes = uint64_t(256) << 20;
+
+uint64_t fnv1a(const void* data, size_t n, uint64_t h = 1469598103934665603ull)
+{
+    const unsigned char* p = static_cast<const unsigned char*>(data);
+    for (size_t i = 0; i < n; i++) h = (h ^ p[i]) * 1099511628211ull;
+    return h;
+}
+
+std::string disk_dir()
+{
+    std::lock_guard<std::mutex> lock(g_disk_mu);
+    if (!g_disk_dir_set) {
+        const char* env = std::getenv("MFH_KERNEL_CACHE_DIR");
+        g_disk_dir = env ? env : "";
+        g_disk_dir_set = true;
+    }
+    return g_disk_dir;
+}
+
+std::string compiler_identity()
+{
+    int major = 0, minor = 0;
+    (void)hiprtcVersion(&major, &minor);
+    std::string id = "hiprtc " + std::to_string(major) + "." + std::to_string(minor);
+    for (const char* o : kCompileOptions) id += std::string(" ") + o;
+    return id;
+}
+
+void put_blob(std::string& out, const void* p, uint64_t n)
+{
+    out.append(reinterpret_cast<const char*>(&n), sizeof n);
+    out.append(static_cast<const char*>(p), n);
+}
+
+std::string disk_path(const std::string& dir, const std::string& identity, const std::string& source)
+{
+    const uint64_t h = fnv1a(source.data(), source.size(), fnv1a(identity.data(), identity.size()));
+    char name[40];
+    std::snprintf(name, sizeof name, "/%016llx.hsaco", (unsigned long long)h);
+    return dir + name;
+}
+
+// The code object stored for (identity, source), if a whole, matching file holds one.
+bool disk_load(const std::string& path, const std::string& identity, const std::string& source, std::vector<char>* code)
+{
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    std::string data;
+    char buf[1 << 16];
+    size_t n;
+    while ((n = std::fread(buf, 1, sizeof buf, f)) > 0 && data.size() <= kDiskMaxBytes) data.append(buf, n);
+    std::fclose(f);
+    size_t at = 0;
+    auto take = [&](std::string* blob) {
+        uint64_t len;
+        if (data.size() - at < sizeof len) return false;
+        std::memcpy(&len, data.data() + at, sizeof len);
+        at += sizeof len;
+        if (len > data.size() - at) return false;
+        blob->assign(data.data() + at, len);
+        at += len;
+        return true;
+    };
+    if (data.size() < sizeof kDiskMagic + sizeof(uint64_t) || std::memcmp(data.data(), kDiskMagic, sizeof kDiskMagic))
+        return false;
+    const size_t body = data.size() - sizeof(uint64_t);
+    uint64_t sum;
+    std::memcpy(&sum, data.data() + body, sizeof sum);
+    if (sum != fnv1a(data.data(), body)) return false;
+    data.resize(body);
+    at = sizeof kDiskMagic;
+    std::string id, src, obj;
+    if (!take(&id) || !take(&src) || !take(&obj) || at != data.size()) return false;
+    if (id != identity || src != source || obj.empty()) return false;
+    code->assign(obj.begin(), obj.end());
+    return true;
+}
+
+// Best effort: a directory that cannot be written only costs later compiles.
+void disk_store(const std::string& path, const std::string& identity, const std::string& source,
+                const std::vector<char>& code)
+{
+    std::string data(kDiskMagic, sizeof kDiskMagic);
+    put_blob(data, identity.data(), identity.size());
+    put_blob(data, source.data(), source.size());
+    put_blob(data, code.data(), code.size());
+    const uint64_t sum = fnv1a(data.data(), data.size());
+    data.append(reinterpret_cast<const char*>(&sum), sizeof sum);
+    static std::atomic<uint64_t> serial{0};
+    const std::string tmp = path + ".tmp." + std::to_string((long long)getpid()) + "." + std::to_string(serial++);
+    FILE* f = std::fopen(tmp.c_str(), "wb");
+    if (!f) return;
+    const bool ok = std::fwrite(data.data(), 1, data.size(), f) == data.size();
+    if (std::fclose(f) != 0 || !ok || std::rename(tmp.c_str(), path.c_str()) != 0) std::remove(tmp.c_str());
+}
+
 int compile_source(const std::string& source, const std::string& kernel_name, std::shared_ptr<CodeObject>* out)
 {
     {
@@ -203,13 +326,25 @@ int compile_source(const std::string& source, const std::string& kernel_name, st
             return MFH_OK;
         }
     }
+    const std::string dir = disk_dir();
+    std::string identity, path;
+    if (!dir.empty()) {
+        identity = compiler_identity();
+        path = disk_path(dir, identity, source);
+        auto obj = std::make_shared<CodeObject>();
+        if (disk_load(path, identity, source, &obj->code)) {
+            obj->kernel_name = kernel_name;
+            g_disk_hits++;
+            std::lock_guard<std::mutex> lock(g_cache_mu);
+            *out = g_cache.emplace(source, obj).first->second;
+            return MFH_OK;
+        }
+    }
     hiprtcProgram prog;
     if (hiprtcCreateProgram(&prog, source.c_str(), (kernel_name + ".hip").c_str(), 0, nullptr, nullptr) != HIPRTC_SUCCESS)
         return fail(MFH_ERR_COMPILE, "codegen hip: hiprtcCreateProgram failed");
-    const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
-                          "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature",
-                          "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-kernarg-preload-count=16"};
-    hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
+    hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof kCompileOptions / sizeof kCompileOptions[0]),
+                                           kCompileOptions);
     if (rc != HIPRTC_SUCCESS) {
         size_t log_size = 0;
         hiprtcGetProgramLogSize(prog, &log_size);
@@ -225,6 +360,8 @@ int compile_source(const std::string& source, const std::string& kernel_name, st
     hiprtcGetCode(prog, obj->code.data());
     hiprtcDestroyProgram(&prog);
     obj->kernel_name = kernel_name;
+    g_compiles++;
+    if (!dir.empty()) disk_store(path, identity, source, obj->code);
     std::lock_guard<std::mutex> lock(g_cache_mu);
     auto it = g_cache.emplace(source, obj).first;
     *out = it->second;
@@ -526,6 +663,22 @@ int mfh_fusion_compile(const mfh_ast_node* nodes, int32_t n_nodes, const mfh_ope
                        uint8_t out_dtype, const char* output_port, uint32_t flags, mfh_kernel** kernel)
 {
     return emit_hip(nodes, n_nodes, inputs, n_inputs, out_dtype, output_port, flags, kernel);
+}
+
+int mfh_fusion_cache_dir(const char* dir)
+{
+    std::lock_guard<std::mutex> lock(g_disk_mu);
+    g_disk_dir = dir ? dir : "";
+    while (g_disk_dir.size() > 1 && g_disk_dir.back() == '/') g_disk_dir.pop_back();
+    g_disk_dir_set = true;
+    return MFH_OK;
+}
+
+int mfh_fusion_cache_stats(int64_t* compiles, int64_t* disk_hits)
+{
+    if (compiles) *compiles = g_compiles.load();
+    if (disk_hits) *disk_hits = g_disk_hits.load();
+    return MFH_OK;
 }
 
 const char* mfh_fusion_source(const mfh_kernel* kernel) { return kernel ? kernel->source.c_str() : nullptr; }
