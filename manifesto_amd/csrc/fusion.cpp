@@ -268,9 +268,9 @@ bool disk_load(const std::string& path, const std::string& identity, const std::
     FILE* f = std::fopen(path.c_str(), "rb");
     if (!f) return false;
     std::string data;
-    char buf[1 << 16];
+    std::vector<char> buf(1 << 16);
     size_t n;
-    while ((n = std::fread(buf, 1, sizeof buf, f)) > 0 && data.size() <= kDiskMaxBytes) data.append(buf, n);
+    while ((n = std::fread(buf.data(), 1, buf.size(), f)) > 0 && data.size() <= kDiskMaxBytes) data.append(buf.data(), n);
     std::fclose(f);
     size_t at = 0;
     auto take = [&](std::string* blob) {
