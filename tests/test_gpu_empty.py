@@ -94,5 +94,17 @@ def test_backend_empty_tensor_round_trip():
         dt, data = b.download(t)
         assert dt == M.FLOAT32 and bytes(data) == b""
         t.close()
+        # every upload form, synchronous and queued, with no elements
+        empty = np.zeros(0, np.uint8)
+        scales = np.zeros(0, np.float16)
+        made = [b.upload_async([0], M.BFLOAT16, b""),
+                b.upload_fp8([0, 7], M.F8E4M3, empty, 0.5),
+                b.upload_fp8([0], M.F8E5M2, empty, 0.5, M.FLOAT32, queued=True),
+                b.upload_int4([3, 0], empty, scales, M.FLOAT16, 128),
+                b.upload_int4([0], empty, scales, M.FLOAT16, 128, M.FLOAT16, queued=True)]
+        for t in made:
+            t.sync()
+            assert t.len() == 0 and bytes(b.download(t)[1]) == b""
+            t.release()
     finally:
         b.close()
