@@ -711,3 +711,149 @@ def test_bytes_to_i4_follows_bytes_to_i8():
                  dtype=np.float32)
     got = O.bytes_to_i8(O.INT4, O.bytes_to_i4(O.FLOAT32, f, f.size))[:f.size].tolist()
     assert got == [0, 0, 0, 0, 7, -8, 7, -8, 7, -8, 0, 7, -8, 3]
+
+
+# --------------------------------------------------------------------------
+# Build-defined extensions of the reference, pinned by the reference's own
+# semantics.  Broadcast: CPUKernel.Run requires every input to hold at least
+# `count` values (codegen/cpu.go:78-85), so a periodic or scalar operand must
+# give exactly what the same chain gives on its pre-expanded copy.  Int4 group
+# scale: decodeInt4ToFloat64 (dtype/convert/decoders.go:262-289) gives the
+# signed nibble, low nibble first, and the build multiplies it by the f32 value
+# of scale[i // group] once, then narrows like float32VectorBytes.
+# --------------------------------------------------------------------------
+
+CONFIG4_CHAIN = (O.N_ADD, (O.N_GELU, (O.N_MUL, (O.N_ADD, ("in", 0), ("in", 1)), ("in", 2))), ("in", 3))
+
+
+def _expanded(a, period, count):
+    """The reference's own operand: `count` values, element e = a[e % period]."""
+    return np.resize(np.asarray(a, dtype=np.float32), count)
+
+
+@pytest.mark.parametrize("count", [4096 * 3, 4096 * 3 + 17, 5])
+def test_periodic_operands_equal_their_pre_expanded_copies_config4(count):
+    rng = np.random.default_rng(count)
+    x = rng.standard_normal(count).astype(np.float32)
+    r = rng.standard_normal(count).astype(np.float32)
+    bias = rng.normal(0, 0.02, 4096).astype(np.float32)
+    s = np.array([1.1], np.float32)
+    nodes = O.flatten(CONFIG4_CHAIN)
+    got = O.run(nodes, [x, bias, s, r], count, periods=[0, 4096, 1, 0])
+    want = O.run(nodes, [x, _expanded(bias, 4096, count), np.full(count, s[0], np.float32), r], count)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def _random_chain(rng, n_inputs, depth):
+    if depth == 0 or rng.random() < 0.25:
+        return ("in", int(rng.integers(0, n_inputs)))
+    op = int(rng.choice([O.N_ADD, O.N_SUB, O.N_MUL, O.N_DIV, O.N_MAX, O.N_MIN, O.N_NEG, O.N_ABS,
+                         O.N_RELU, O.N_SILU, O.N_GELU, O.N_SIGMOID, O.N_TANH, O.N_LEAKY_RELU]))
+    if O.arity(op) == 2:
+        return (op, _random_chain(rng, n_inputs, depth - 1), _random_chain(rng, n_inputs, depth - 1))
+    return (op, _random_chain(rng, n_inputs, depth - 1))
+
+
+def test_periodic_operands_equal_their_pre_expanded_copies_random_chains():
+    rng = np.random.default_rng(2024)
+    count = 3 * 7 * 64 + 11
+    for trial in range(40):
+        n_in = int(rng.integers(1, 5))
+        nodes = O.flatten(_random_chain(rng, n_in, 4))
+        periods = [int(rng.choice([0, 1, 7, 64, 100, count])) for _ in range(n_in)]
+        arrays = [rng.normal(0, 2, p if p > 0 else count).astype(np.float32) for p in periods]
+        got = O.run(nodes, arrays, count, periods=periods)
+        want = O.run(nodes, [_expanded(a, p, count) if p > 0 else a for a, p in zip(arrays, periods)], count)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), (trial, periods)
+        assert np.array_equal(bits(got[~nan]), bits(want[~nan])), (trial, periods)
+
+
+# Scales that reach every branch of the product: exact products, zeros of
+# both signs, an f16 subnormal, the largest f16, Inf and NaN.
+_INT4_F16_SCALES = np.array([0x2148, 0x251F, 0x3C00, 0xB800, 0x0000, 0x8000, 0x0001, 0x03FF, 0x7BFF, 0x7C00,
+                             0xFC00, 0x7E00, 0x7D01], dtype=np.uint16)
+
+
+def _int4_closed(packed, n, scale_f32, group):
+    """(nib - 16 (nib >= 8)) * scale[i // group], low nibble first, in f32."""
+    nib = np.empty(2 * packed.size, dtype=np.int64)
+    nib[0::2], nib[1::2] = packed & 15, packed >> 4
+    q = (nib - 16 * (nib >= 8))[:n].astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (q * scale_f32[np.arange(n) // group]).astype(np.float32)
+
+
+@pytest.mark.parametrize("out_dtype", [O.FLOAT32, O.BFLOAT16, O.FLOAT16])
+@pytest.mark.parametrize("group, n", [(128, 128 * 26), (128, 128 * 26 - 37), (96, 96 * 26 + 5), (3, 3 * 26 + 1)])
+def test_dequant_int4_is_nibble_times_group_scale_then_narrowed(out_dtype, group, n):
+    # Every byte (so all 16 codes on both nibbles) under each special f16
+    # scale, one scale per group; a partial last group, odd counts (the last
+    # byte's high nibble unused) and groups that are not powers of two.
+    groups = -(-n // group)
+    scales = np.resize(_INT4_F16_SCALES, groups)
+    packed = np.resize(np.arange(256, dtype=np.uint8), (n + 1) // 2)
+    np.random.default_rng(group + n).shuffle(packed)
+    prod = _int4_closed(packed, n, scales.view(np.float16).astype(np.float32), group)
+    got = _as_bits(O.dequant_int4(packed, n, scales, O.FLOAT16, group, out_dtype))
+    nan = np.isnan(prod)
+    assert np.array_equal(got[~nan], _as_bits(_narrow(prod[~nan], out_dtype)))
+    # NaN products keep the x86 multiply's NaN: Inf * 0 is the default NaN
+    # 0xffc00000, a NaN scale propagates quieted with its payload
+    sf = scales.view(np.uint16).astype(np.uint32)[np.arange(n) // group]
+    s32 = scales.view(np.float16).astype(np.float32).view(np.uint32)[np.arange(n) // group]
+    want_nan = np.where((sf & 0x7FFF) > 0x7C00, s32 | 0x00400000, 0xFFC00000)
+    assert [int(b) for b in got[nan]] == [_nan_narrow(b, out_dtype) for b in want_nan[nan]]
+
+
+@pytest.mark.parametrize("scale_dtype", [O.FLOAT32, O.BFLOAT16])
+def test_dequant_int4_wide_scales(scale_dtype):
+    rng = np.random.default_rng(scale_dtype)
+    n, group = 128 * 40 + 3, 128
+    packed = rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
+    s32 = rng.uniform(-3, 3, -(-n // group)).astype(np.float32)
+    if scale_dtype == O.BFLOAT16:
+        scales = _narrow(s32, O.BFLOAT16)
+        s32 = (scales.astype(np.uint32) << 16).view(np.float32)
+    else:
+        scales = s32
+    want = _narrow(_int4_closed(packed, n, s32, group), O.BFLOAT16)
+    assert np.array_equal(O.dequant_int4(packed, n, scales, scale_dtype, group, O.BFLOAT16), want)
+
+
+def test_extension_checks_catch_planted_mistakes():
+    # Planted in restatements written here, never in the product: each one is
+    # told apart from the oracle by the checks above.
+    rng = np.random.default_rng(99)
+    count = 4096 * 2 + 9
+    x = rng.standard_normal(count).astype(np.float32)
+    r = rng.standard_normal(count).astype(np.float32)
+    bias = rng.normal(0, 0.02, 4096).astype(np.float32)
+    s = np.array([1.1], np.float32)
+    nodes = O.flatten(CONFIG4_CHAIN)
+    periodic = O.run(nodes, [x, bias, s, r], count, periods=[0, 4096, 1, 0])
+    # (1) broadcast by e // p (each bias value repeated) instead of e % p
+    wrong = np.repeat(bias, -(-count // 4096))[:count]
+    assert not np.array_equal(bits(O.run(nodes, [x, wrong, np.full(count, 1.1, np.float32), r], count)),
+                              bits(periodic))
+    # Int4: every byte, f16 scales that differ per group, group 128
+    n, group = 128 * 8 + 3, 128
+    packed = np.resize(np.arange(256, dtype=np.uint8), (n + 1) // 2)
+    scales = O.f32_to_f16(rng.uniform(0.005, 0.02, -(-n // group)).astype(np.float32))
+    sf = scales.view(np.float16).astype(np.float32)
+    got = O.dequant_int4(packed, n, scales, O.FLOAT16, group, O.BFLOAT16)
+    assert np.array_equal(got, _narrow(_int4_closed(packed, n, sf, group), O.BFLOAT16))
+    nib = np.empty(2 * packed.size, dtype=np.int64)
+    # (2) the group counted over bytes rather than elements
+    nib[0::2], nib[1::2] = packed & 15, packed >> 4
+    q = (nib - 16 * (nib >= 8))[:n].astype(np.float32)
+    by_bytes = (q * sf[(np.arange(n) // 2) // group]).astype(np.float32)
+    assert not np.array_equal(_narrow(by_bytes, O.BFLOAT16), got)
+    # (3) the high nibble first
+    nib[0::2], nib[1::2] = packed >> 4, packed & 15
+    q = (nib - 16 * (nib >= 8))[:n].astype(np.float32)
+    assert not np.array_equal(_narrow((q * sf[np.arange(n) // group]).astype(np.float32), O.BFLOAT16), got)
+    # (4) unsigned nibbles (no sign extension)
+    nib[0::2], nib[1::2] = packed & 15, packed >> 4
+    q = nib[:n].astype(np.float32)
+    assert not np.array_equal(_narrow((q * sf[np.arange(n) // group]).astype(np.float32), O.BFLOAT16), got)
