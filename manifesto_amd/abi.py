@@ -18,6 +18,7 @@ UINT64, UINT32, UINT16, UINT8 = 12, 13, 14, 15
 
 OPERAND_FULL, OPERAND_PERIODIC, OPERAND_SCALAR = 0, 1, 2
 FUSION_PRECISE = 1
+FUSION_SHORT_QUOTIENT = 2
 
 MFH_OK = 0
 

@@ -58,6 +58,9 @@
 #define mfh_sqrtf(x) std::sqrt((float)(x))
 #define MFH_KEEP(x) ((void)0)
 #define mfh_med3f(x, lo, hi) std::fmin(std::fmax((float)(x), (float)(lo)), (float)(hi))
+#define mfh_absf(x) std::fabs((float)(x))
+#define mfh_maxf(a, b) std::fmax((float)(a), (float)(b))
+#define mfh_minf(a, b) std::fmin((float)(a), (float)(b))
 #define mfh_is_nan_or_inf_class(v) (std::isnan(v) || std::isinf(v))
 inline unsigned mfh_fbits(float f) { unsigned u; __builtin_memcpy(&u, &f, 4); return u; }
 inline float mfh_fromfbits(unsigned u) { float f; __builtin_memcpy(&f, &u, 4); return f; }
@@ -90,6 +93,10 @@ extern "C" __device__ double __ocml_log_f64(double);
 // select (which serialises the unrolled elements).  Emits no instruction.
 #define MFH_KEEP(x) __asm__ volatile("" : "+v"(x))
 #define mfh_med3f(x, lo, hi) __builtin_amdgcn_fmed3f((x), (lo), (hi))
+// |x| is a source modifier on gfx950 (no instruction of its own).
+#define mfh_absf(x) __builtin_fabsf(x)
+#define mfh_maxf(a, b) __builtin_fmaxf((a), (b))
+#define mfh_minf(a, b) __builtin_fminf((a), (b))
 __device__ inline unsigned mfh_fbits(float f) { return __builtin_bit_cast(unsigned, f); }
 __device__ inline float mfh_fromfbits(unsigned u) { return __builtin_bit_cast(float, u); }
 __device__ inline int mfh_low_int(double d) { return (int)(unsigned)__builtin_bit_cast(unsigned long long, d); }
@@ -147,6 +154,22 @@ MFH_MATH float mfh_div_one_plus(float n, float e)
     return mfh_fmaf(res, r, q);
 }
 
+// n / (1 + e) for the exact 1 + e: d = fl(1 + e) and its rounding error
+// dl = min(1, e) - (d - max(1, e)) (Fast2Sum: both terms are positive and the
+// larger goes first) both enter the residual, so the quotient is corrected for
+// the reciprocal's error and for d's rounding.  Four VALU instructions more
+// than mfh_div_one_plus; chains that stream f32 use it (f32 results show the
+// rounding of d, 16-bit results hide it), and 1 + e may then be a rounding tie.
+MFH_MATH float mfh_div_one_plus_exact(float n, float e)
+{
+    const float d = 1.0f + e;
+    const float dl = mfh_minf(e, 1.0f) - (d - mfh_maxf(e, 1.0f));
+    const float r = mfh_rcpf(d);
+    const float q = n * r;
+    const float res = mfh_fmaf(-q, dl, mfh_fmaf(-q, d, n));
+    return mfh_fmaf(res, r, q);
+}
+
 MFH_MATH bool mfh_is_inf(float v) { return (mfh_fbits(v) & 0x7fffffffu) == 0x7f800000u; }
 MFH_MATH bool mfh_is_nan(float v) { return (mfh_fbits(v) & 0x7fffffffu) > 0x7f800000u; }
 
@@ -154,23 +177,24 @@ MFH_MATH bool mfh_is_nan(float v) { return (mfh_fbits(v) & 0x7fffffffu) > 0x7f80
 MFH_MATH float mfh_sigmoid_ref(float v) { return (float)(1.0 / (1.0 + mfh_exp_f64(-(double)v))); }
 MFH_MATH float mfh_silu_ref(float v) { return (float)((double)v / (1.0 + mfh_exp_f64(-(double)v))); }
 
-// gelu in the reference's f64 form 0.5 v (1 + tanh(inner)).  For
-// inner <= -0.625 tanh is formed as -(1 - 2 / (e^(2|inner|) + 1)), the form in
-// which Go's math.Tanh (and glibc's) evaluates it there, because in that range
-// 1 + tanh cancels and its result carries the f64 quantum of exactly that
-// expression.  Elsewhere any faithful f64 tanh gives the same f32 result.
+// gelu in the reference's f64 form 0.5 v (1 + tanh(inner)), with
+// s = e^(-2 inner) and y = 2 / (s + 1).  For inner <= -0.625 tanh is
+// -(1 - y), the form in which Go's math.Tanh (and glibc's) evaluates it there
+// (s = e^(2|inner|)), and 1 + tanh is formed as 1 - (1 - y) with the same f64
+// roundings, because in that range 1 + tanh cancels and its result carries
+// the f64 quantum of exactly that expression.  Above it 1 + tanh(inner) = y
+// exactly, and y is faithful (one f64 exp, one division), so the f32 result is
+// that of any faithful f64 tanh but for f64 rounding ties.  One exp and one
+// division serve both ranges: a third of the instructions of an f64 tanh,
+// whose double-word steps the fast forms' flagged elements would otherwise
+// pay for.
 MFH_MATH float mfh_gelu_ref(float v)
 {
-    double d = (double)v;
-    double inner = MFH_SQRT_2_OVER_PI_D * (d + MFH_GELU_A_D * d * d * d);
-    double th;
-    if (inner > -0.625) {
-        th = mfh_tanh_f64(inner);
-    } else {
-        double s = mfh_exp_f64(-2.0 * inner);
-        th = -(1.0 - 2.0 / (s + 1.0));
-    }
-    return (float)(0.5 * d * (1.0 + th));
+    const double d = (double)v;
+    const double inner = MFH_SQRT_2_OVER_PI_D * (d + MFH_GELU_A_D * d * d * d);
+    const double y = 2.0 / (mfh_exp_f64(-2.0 * inner) + 1.0);
+    const double one_plus_th = inner > -0.625 ? y : 1.0 - (1.0 - y);
+    return (float)(0.5 * d * one_plus_th);
 }
 
 // Each fast activation comes in two parts: mfh_<name>_fast(v, rare) is
@@ -221,6 +245,16 @@ MFH_MATH float mfh_silu_fast(float v, bool& rare)
     return mfh_div_one_plus(v, mfh_exp_neg(m));
 }
 
+// The same with the exact 1 + e^-v (mfh_div_one_plus_exact), for chains that
+// stream f32: within 2 f32 ulps and bit-identical to the reference for more
+// inputs, at four more VALU instructions per element.
+MFH_MATH float mfh_silu_fast_x(float v, bool& rare)
+{
+    const float m = mfh_med3f(v, -16.5f, 87.0f);
+    rare |= m != v;
+    return mfh_div_one_plus_exact(v, mfh_exp_neg(m));
+}
+
 // Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
 // t = -2 inner log2(e) = d w, w = KA + KB d^2, formed and reduced in f64 (the
 // cubic needs more than f32's 24 bits where E is large) and 2^f, |f| <= 1/2,
@@ -236,31 +270,52 @@ MFH_MATH float mfh_silu_fast(float v, bool& rare)
 // reference's tanh is exactly 1 there.
 #define MFH_GELU_KA (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_LOG2E_D)
 #define MFH_GELU_KB (-2.0 * MFH_SQRT_2_OVER_PI_D * MFH_GELU_A_D * MFH_LOG2E_D)
-MFH_MATH float mfh_gelu_fast(float v, bool& rare)
+MFH_MATH float mfh_gelu_e(float c)
 {
-    const float c = mfh_med3f(v, -4.9f, 1024.0f);
-    rare |= c != v;
     const double d = (double)c;
     const double w = mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA);
     const double tk = mfh_fma(w, d, MFH_ROUND_INT_D);
     const double kd = tk - MFH_ROUND_INT_D;
     const float p = mfh_exp2f_hw((float)mfh_fma(w, d, -kd));
-    return mfh_div_one_plus(v, mfh_ldexpf(p, mfh_low_int(tk)));
+    return mfh_ldexpf(p, mfh_low_int(tk));
 }
 
-#define MFH_FAST_OR_REF(name)                                           \
-    MFH_RARE float mfh_##name##_rare(float v) { return mfh_##name##_ref(v); } \
-    MFH_MATH float mfh_##name(float v)                                   \
+MFH_MATH float mfh_gelu_fast(float v, bool& rare)
+{
+    const float c = mfh_med3f(v, -4.9f, 1024.0f);
+    rare |= c != v;
+    return mfh_div_one_plus(v, mfh_gelu_e(c));
+}
+
+// With the exact 1 + E, for chains that stream f32 (as mfh_silu_fast_x).
+MFH_MATH float mfh_gelu_fast_x(float v, bool& rare)
+{
+    const float c = mfh_med3f(v, -4.9f, 1024.0f);
+    rare |= c != v;
+    return mfh_div_one_plus_exact(v, mfh_gelu_e(c));
+}
+
+// mfh_<name>_rare: the reference form as a real call (MFH_RARE), which the
+// generated kernels use to recompute flagged elements.  mfh_<name>(v): the
+// fast form, or the reference form where the fast one sets its flag (the
+// host accuracy sweep measures these).
+#define MFH_FAST_OR_REF(name, fast, ref)                                \
+    MFH_MATH float name(float v)                                        \
     {                                                                   \
         bool rare = false;                                              \
-        float s = mfh_##name##_fast(v, rare);                           \
+        float s = fast(v, rare);                                        \
         MFH_KEEP(s);                                                    \
-        if (rare) s = mfh_##name##_rare(v);                             \
+        if (rare) s = ref(v);                                           \
         return s;                                                       \
     }
-MFH_FAST_OR_REF(sigmoid)
-MFH_FAST_OR_REF(silu)
-MFH_FAST_OR_REF(gelu)
+MFH_RARE float mfh_sigmoid_rare(float v) { return mfh_sigmoid_ref(v); }
+MFH_RARE float mfh_silu_rare(float v) { return mfh_silu_ref(v); }
+MFH_RARE float mfh_gelu_rare(float v) { return mfh_gelu_ref(v); }
+MFH_FAST_OR_REF(mfh_sigmoid, mfh_sigmoid_fast, mfh_sigmoid_rare)
+MFH_FAST_OR_REF(mfh_silu, mfh_silu_fast, mfh_silu_rare)
+MFH_FAST_OR_REF(mfh_silu_x, mfh_silu_fast_x, mfh_silu_rare)
+MFH_FAST_OR_REF(mfh_gelu, mfh_gelu_fast, mfh_gelu_rare)
+MFH_FAST_OR_REF(mfh_gelu_x, mfh_gelu_fast_x, mfh_gelu_rare)
 #undef MFH_FAST_OR_REF
 
 MFH_MATH float mfh_exp_ref(float v) { return (float)mfh_exp_f64((double)v); }

@@ -19,6 +19,7 @@
 #include <unistd.h>
 
 #include <atomic>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -80,23 +81,118 @@ int link(const std::vector<mfh_ast_node>& nodes, int idx, std::vector<int>& c0, 
     return next;
 }
 
+// How an Emitter evaluates Sigmoid, Silu and Gelu.
+enum class Form {
+    kFast,      // branch-free fast forms; each ORs the element's flag `qe`
+    kFallback,  // the reference forms as real calls (recomputing flagged elements)
+    kPrecise,   // the reference forms inline (MFH_FUSION_PRECISE)
+};
+
+bool is_fast_activation(int type) { return type == kNodeSigmoid || type == kNodeSilu || type == kNodeGelu; }
+
+bool is_transcendental(int type)
+{
+    return type == kNodeExp || type == kNodeLog || type == kNodeTanh || is_fast_activation(type);
+}
+
+// Cancellation guards.  A fast activation's value a' is within 2 f32 ulps of
+// the reference's a, i.e. |a' - a| <= 2^-22 |a|, and every op between it and
+// the output is IEEE-exact in both evaluations except for that difference.
+// An Add/Sub s = a + b whose result is much smaller than a turns it into an
+// error of up to 2^-22 |a| / |s| relative to s, which for a 16-bit output can
+// exceed one storage ulp (config 4: gelu + residual cancelling to an f16
+// denormal).  The generated code flags the element when |s| F < |a| and
+// recomputes flagged elements with the reference forms.  With e the operand's
+// error in f32 ulps (2 for the activation, one more for each Mul, Div, Sqrt or
+// LeakyReLU between it and the Add/Sub) and m the output's mantissa bits
+// (10 for f16, 7 for bf16), F = 0.7 2^(22-m) / e: unflagged, the difference
+// is at most e 2^-23 F |s| = 0.7 2^(-1-m) |s|, under 0.7 of the storage ulp
+// of s (which exceeds 2^(-1-m) |s|), plus one f32 rounding of s; the two
+// rounded results are then at most one storage ulp apart.  f16 denormal
+// results are covered by the same test (unflagged, |a| < F 2^-14 and the
+// difference is under 2^-25).  The guarantee is made where the activation
+// reaches the output through exactly one Add/Sub and no other transcendental
+// node (the BASELINE chains); other paths keep the node-envelope contract.
+// f32 outputs carry every f32 ulp of the node, so they take no guard.
+struct Guard {
+    int factor = 0;  // flag when |s| factor < M; 0 = no guard
+    bool lhs = false, rhs = false;  // which operands carry an activation's error (M = the max of those)
+};
+
+std::vector<Guard> plan_guards(const std::vector<mfh_ast_node>& nodes, const std::vector<int>& c0,
+                               const std::vector<int>& c1, uint8_t out_dtype, bool precise)
+{
+    const int n = (int)nodes.size();
+    std::vector<Guard> guards(n);
+    const int mantissa = out_dtype == kFloat16 ? 10 : out_dtype == kBFloat16 ? 7 : 0;
+    if (precise || mantissa == 0) return guards;
+    std::vector<int> parent(n, -1);
+    for (int i = 0; i < n; i++) {
+        if (c0[i] >= 0) parent[c0[i]] = i;
+        if (c1[i] >= 0) parent[c1[i]] = i;
+    }
+    // Per Add/Sub: the error of each operand in f32 ulps (0: none), or off
+    // when an activation below it reaches the output by another Add/Sub or
+    // through another transcendental node.
+    std::vector<int> ulps_lhs(n, 0), ulps_rhs(n, 0);
+    std::vector<bool> off(n, false);
+    for (int a = 0; a < n; a++) {
+        if (!is_fast_activation(nodes[a].type)) continue;
+        int rounding = 0, add = -1, adds = 0;
+        bool lhs = false, other = false;
+        for (int from = a, p = parent[a]; p >= 0; from = p, p = parent[p]) {
+            const int t = nodes[p].type;
+            if (t == kNodeAdd || t == kNodeSub) {
+                if (adds++ == 0) {
+                    add = p;
+                    lhs = from == c0[p];
+                }
+            } else if (t == kNodeMul || t == kNodeDiv || t == kNodeSqrt || t == kNodeLeakyReLU) {
+                if (adds == 0) rounding++;
+            } else if (is_transcendental(t)) {
+                other = true;
+            }
+        }
+        if (add < 0) continue;
+        if (adds > 1 || other) {
+            off[add] = true;
+            continue;
+        }
+        // relative errors add through Mul/Div: a sum over the side's
+        // activations bounds the side's error
+        (lhs ? ulps_lhs[add] : ulps_rhs[add]) += 2 + rounding;
+    }
+    for (int i = 0; i < n; i++) {
+        if (off[i] || (ulps_lhs[i] == 0 && ulps_rhs[i] == 0)) continue;
+        const int factor = (int)(0.7 * std::ldexp(1.0, 22 - mantissa) / (ulps_lhs[i] + ulps_rhs[i]));
+        if (factor < 2) continue;
+        guards[i].factor = factor;
+        guards[i].lhs = ulps_lhs[i] > 0;
+        guards[i].rhs = ulps_rhs[i] > 0;
+    }
+    return guards;
+}
+
 struct Emitter {
     const std::vector<mfh_ast_node>& nodes;
     const std::vector<int>& c0;
     const std::vector<int>& c1;
-    bool precise;
-    std::string body;
-    int tmp = 0;
+    Form form;
+    // Silu and Gelu with the exact 1 + E in their quotient (mfh_*_fast_x):
+    // chains that stream f32.
+    bool exact_tail = false;
+    const std::vector<Guard>* guards = nullptr;  // kFast only
+    std::string prefix = "t";
     // Vector loop only: inputs held as packed f16 words w<k>[u][j >> 1]
     // (empty in the element loop).
     std::vector<bool> packed16 = {};
-    // Vector loop only: Sigmoid, Silu and Gelu call their branch-free fast
-    // forms, which OR each element's rare-range flag into the item's bool
-    // `q`; `deferred` is set once such a call has been emitted.
-    bool defer_rare = false;
-    bool deferred = false;
+    std::string body = "";
+    int tmp = 0;
+    // Set once the element's flag `qe` has been written: a fast activation or
+    // a guard was emitted.
+    bool flagged = false;
 
-    std::string fresh() { return "t" + std::to_string(tmp++); }
+    std::string fresh() { return prefix + std::to_string(tmp++); }
 
     std::string let(const std::string& expr)
     {
@@ -108,10 +204,24 @@ struct Emitter {
     std::string activation(const char* name, const std::string& a)
     {
         const std::string fn = std::string("mfh_") + name;
-        if (precise) return let(fn + "_ref(" + a + ")");
-        if (!defer_rare) return let(fn + "(" + a + ")");
-        deferred = true;
-        return let(fn + "_fast(" + a + ", q)");
+        if (form == Form::kPrecise) return let(fn + "_ref(" + a + ")");
+        if (form == Form::kFallback) return let(fn + "_rare(" + a + ")");
+        flagged = true;
+        const bool x = exact_tail && std::string(name) != "sigmoid";  // sigmoid's quotient is f64
+        return let(fn + (x ? "_fast_x(" : "_fast(") + a + ", qe)");
+    }
+
+    // s = a + b (or a - b): the cancellation guard of node idx, if planned.
+    std::string guarded(int idx, const std::string& s, const std::string& a, const std::string& b)
+    {
+        if (form != Form::kFast || !guards || (*guards)[idx].factor == 0) return s;
+        const Guard& g = (*guards)[idx];
+        std::string m = g.lhs && g.rhs ? "mfh_maxf(mfh_absf(" + a + "), mfh_absf(" + b + "))"
+                        : g.lhs        ? "mfh_absf(" + a + ")"
+                                       : "mfh_absf(" + b + ")";
+        body += "        qe |= !(mfh_absf(" + s + ") * " + std::to_string(g.factor) + ".0f >= " + m + ");\n";
+        flagged = true;
+        return s;
     }
 
     // Returns the name holding node idx's value for the current element.
@@ -133,15 +243,22 @@ struct Emitter {
             };
             std::string wa = word(c0[idx]), wb = word(c1[idx]);
             if (!wa.empty() && !wb.empty()) return let("mfh_add_hh(" + wa + ", j & 1, " + wb + ", j & 1)");
-            if (!wb.empty()) return let("mfh_add_fh(" + emit(c0[idx]) + ", " + wb + ", j & 1)");
-            if (!wa.empty()) return let("mfh_add_fh(" + emit(c1[idx]) + ", " + wa + ", j & 1)");
+            // a leaf carries no activation error: the guard's operand is the other side
+            if (!wb.empty()) {
+                std::string a = emit(c0[idx]);
+                return guarded(idx, let("mfh_add_fh(" + a + ", " + wb + ", j & 1)"), a, a);
+            }
+            if (!wa.empty()) {
+                std::string b = emit(c1[idx]);
+                return guarded(idx, let("mfh_add_fh(" + b + ", " + wa + ", j & 1)"), b, b);
+            }
         }
         std::string a = emit(c0[idx]);
         if (node_arity(n.type) == 2) {
             std::string b = emit(c1[idx]);
             switch (n.type) {
-            case kNodeAdd: return let(a + " + " + b);
-            case kNodeSub: return let(a + " - " + b);
+            case kNodeAdd: return guarded(idx, let(a + " + " + b), a, b);
+            case kNodeSub: return guarded(idx, let(a + " - " + b), a, b);
             case kNodeMul: return let(a + " * " + b);
             case kNodeDiv: return let(a + " / " + b);
             case kNodeMax: return let("(" + a + " > " + b + ") ? " + a + " : " + b);
@@ -488,18 +605,27 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     const bool stream_loads = read_bytes >= (out_dtype == kFloat32 ? 4 : 2);
 
     // Element loop: every operand decoded to f32.  Vector loop: f16 operands
-    // stay packed words so that adds can take them directly.
-    Emitter em{list, c0, c1, precise, "", 0};
-    std::string result = em.emit(0);
+    // stay packed words so that adds can take them directly.  Without
+    // MFH_FUSION_PRECISE each element runs the fast forms and the planned
+    // cancellation guards, which set its flag `qe`; flagged elements are then
+    // recomputed with the reference forms (real calls), so the item's main
+    // body has no branch.  Chains that stream f32 take Silu and Gelu with the
+    // exact 1 + E (their results show every f32 ulp; four VALU instructions
+    // more per element, where a 16-bit chain's bytes would not cover them).
+    const Form main_form = precise ? Form::kPrecise : Form::kFast;
+    const bool exact_tail = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
+    const std::vector<Guard> guards = plan_guards(list, c0, c1, out_dtype, precise);
     std::vector<bool> packed16(n_inputs, false);
     for (int k = 0; k < n_inputs; k++)
         packed16[k] = inputs[k].mode != MFH_OPERAND_SCALAR && inputs[k].dtype == kFloat16;
-    Emitter emv{list, c0, c1, precise, "", 0, packed16, true};
-    std::string vresult = emv.emit(0);
-    // With fast activations, elements in a rare range are recomputed after
-    // the item's main body by the same expression with the per-element forms.
-    Emitter emr{list, c0, c1, precise, "", 0, packed16};
-    const std::string rresult = emv.deferred ? emr.emit(0) : "";
+    Emitter em{list, c0, c1, main_form, exact_tail, &guards};
+    const std::string result = em.emit(0);
+    Emitter emf{list, c0, c1, Form::kFallback, exact_tail, nullptr, "f"};
+    const std::string fresult = em.flagged ? emf.emit(0) : "";
+    Emitter emv{list, c0, c1, main_form, exact_tail, &guards, "t", packed16};
+    const std::string vresult = emv.emit(0);
+    Emitter emvf{list, c0, c1, Form::kFallback, exact_tail, nullptr, "f", packed16};
+    const std::string vfresult = emv.flagged ? emvf.emit(0) : "";
 
     std::string identifier = output_port && *output_port ? output_port : "anon";
     std::string kernel_name = "fused_" + sanitize(output_port ? output_port : "");
@@ -554,16 +680,22 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
         operands += "        const float x" + ks + " = " + value + ";\n";
     }
     src += "            float r[" + V + "];\n";
-    if (emv.deferred) src += "            bool q = false;\n";
+    if (emv.flagged) src += "            bool qv[" + V + "];\n";
     src += "#pragma unroll\n            for (int j = 0; j < " + V + "; j++) {\n";
-    src += operands + emv.body;
-    src += "                r[j] = " + vresult + ";\n            }\n";
-    if (emv.deferred) {
-        // an item with an element in a rare range: every element again with
-        // the per-element forms (the same value for the others)
-        src += "            if (q) {\n#pragma unroll\n                for (int j = 0; j < " + V + "; j++) {\n";
-        src += operands + emr.body;
-        src += "                    r[j] = " + rresult + ";\n                }\n            }\n";
+    src += operands;
+    if (emv.flagged) src += "        bool qe = false;\n";
+    src += emv.body;
+    src += "                r[j] = " + vresult + ";\n";
+    if (emv.flagged) src += "                qv[j] = qe;\n";
+    src += "            }\n";
+    if (emv.flagged) {
+        // the item's flagged elements again, with the reference forms
+        src += "            bool qany = false;\n#pragma unroll\n            for (int j = 0; j < " + V +
+               "; j++) qany |= qv[j];\n";
+        src += "            if (qany) {\n#pragma unroll\n                for (int j = 0; j < " + V +
+               "; j++) {\n                    if (!qv[j]) continue;\n";
+        src += operands + emvf.body;
+        src += "                    r[j] = " + vfresult + ";\n                }\n            }\n";
     }
     src += "            mfh_st" + V + "_" + osfx + "(pout, it * " + V + ", r);\n        }\n    }\n";
     // scalar tail (and the whole range when the vector path is off)
@@ -576,8 +708,11 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
             src += "        const float x" + ks + " = mfh_ld1_" + io_suffix(inputs[k].dtype) + "(p" + ks + ", " +
                    operand_index(inputs[k], "i") + ");\n";
     }
+    if (em.flagged) src += "        bool qe = false;\n";
     src += em.body;
-    src += std::string("        mfh_st1_") + osfx + "(pout, i, " + result + ");\n    }\n}\n";
+    src += "        float res = " + result + ";\n";
+    if (em.flagged) src += "        if (qe) {\n" + emf.body + "        res = " + fresult + ";\n        }\n";
+    src += std::string("        mfh_st1_") + osfx + "(pout, i, res);\n    }\n}\n";
 
     auto kernel = std::make_unique<mfh_kernel>();
     kernel->identifier = identifier;

@@ -59,10 +59,12 @@ def test_emit_hip_swiglu_source_shape():
     assert "streamed loads" in src
     assert "mfh_st8_bf16(pout, it * 8, r)" in src
     assert src.count("for (mfh_i64 i = nvec * 8 + tid; i < n; i += stride)") == 1
-    # the vector loop runs the branch-free fast form with a per-item rare flag
-    # and recomputes flagged items with the per-element form; the scalar tail
-    # uses the per-element form directly
-    assert "mfh_silu_fast(x0, q)" in src and "if (q) {" in src and src.count("mfh_silu(x0)") == 2
+    # every element runs the branch-free fast form, which sets the element's
+    # flag; flagged elements (vector loop and scalar tail) are recomputed with
+    # the reference form as a real call.  No Add/Sub follows the activation:
+    # no cancellation guard.
+    assert src.count("mfh_silu_fast(x0, qe)") == 2 and "if (qany) {" in src and "if (qe) {" in src
+    assert src.count("mfh_silu_rare(x0)") == 2 and "qe |=" not in src
     assert "8 elements per item, 1 item(s) per thread" in src  # f32-only math: one item per thread
 
 
@@ -80,14 +82,74 @@ def test_emit_hip_broadcast_operands():
     assert "mfh_add_fh(t2, w3[u][j >> 1], j & 1)" in src
     assert "const float x1 = mfh_ld1_f16(p1, (i % 4096LL));" in src  # element loop decodes
     assert "const float s2 = mfh_ld1_f32(p2, 0);" in src
-    assert "mfh_gelu_fast(t1, q)" in src and "mfh_gelu(t1)" in src
+    assert "mfh_gelu_fast(t1, qe)" in src and "mfh_gelu_rare(f1)" in src
+    # gelu + residual can cancel: f16 output, so the guard's factor is 0.7 * 2^12 / 2
+    assert src.count("qe |= !(mfh_absf(t3) * 1433.0f >= mfh_absf(t2));") == 2
     # one item per thread; only a Sigmoid (mostly f64 work) takes two by default
     assert "8 elements per item, 1 item(s) per thread" in src
     sig = M.FusedKernel(flatten((N_SIGMOID, ("in", 0))), [(M.FLOAT16, M.OPERAND_FULL, 0)], M.FLOAT16, "sig")
     assert "8 elements per item, 2 item(s) per thread" in sig.source
     precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)
     assert "mfh_gelu_ref(" in precise.source and "_fast(" not in precise.source.split("EmitHIP")[1]
-    assert "if (q)" not in precise.source and "1 item(s) per thread" in precise.source
+    assert "qe" not in precise.source and "1 item(s) per thread" in precise.source
+
+
+def guard_lines(src):
+    return [l.strip() for l in src.splitlines() if l.strip().startswith("qe |=")]
+
+
+@pytest.mark.parametrize("out_dt, threshold", [(M.FLOAT16, 1433), (M.BFLOAT16, 11468), (M.FLOAT32, None)])
+def test_cancellation_guard_threshold_follows_the_output(out_dt, threshold):
+    # Sub(Gelu(x), y): the activation's 2-ulp error, amplified by the
+    # cancellation, must stay below 0.7 of a storage ulp: factor
+    # 0.7 * 2^(22 - mantissa bits) / 2, i.e. 1433 for f16 and 11468 for bf16;
+    # f32 outputs keep the node-envelope contract and take no guard.
+    nodes = flatten((N_SUB, (N_GELU, ("in", 0)), ("in", 1)))
+    k = M.FusedKernel(nodes, [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, out_dt, "g")
+    lines = guard_lines(k.source)
+    if threshold is None:
+        assert lines == []
+    else:
+        assert lines == [f"qe |= !(mfh_absf(t1) * {threshold}.0f >= mfh_absf(t0));"] * 2
+
+
+def test_cancellation_guard_counts_the_error_on_its_operands():
+    bf = [(M.BFLOAT16, M.OPERAND_FULL, 0)]
+    # one rounding op between the activation and the add: 3 ulps
+    k = M.FusedKernel(flatten((N_ADD, (N_MUL, (N_SILU, ("in", 0)), ("in", 1)), ("in", 2))), bf * 3, M.FLOAT16, "m")
+    assert guard_lines(k.source)[0] == "qe |= !(mfh_absf(t2) * 955.0f >= mfh_absf(t1));"
+    # activations on both operands: compared with the larger, 2 + 2 ulps
+    k = M.FusedKernel(flatten((N_SUB, (N_SILU, ("in", 0)), (N_GELU, ("in", 1)))), bf * 2, M.FLOAT16, "b")
+    assert guard_lines(k.source)[0] == "qe |= !(mfh_absf(t2) * 716.0f >= mfh_maxf(mfh_absf(t0), mfh_absf(t1)));"
+    # a second add on the path, or a transcendental above: no guarantee, no guard
+    k = M.FusedKernel(flatten((N_ADD, (N_ADD, (N_GELU, ("in", 0)), ("in", 1)), ("in", 2))), bf * 3, M.FLOAT16, "a2")
+    assert guard_lines(k.source) == []
+    k = M.FusedKernel(flatten((N_EXP, (N_ADD, (N_GELU, ("in", 0)), ("in", 1)))), bf * 2, M.FLOAT16, "e")
+    assert guard_lines(k.source) == []
+    # no activation, no guard; precise forms, no guard
+    k = M.FusedKernel(flatten((N_ADD, (N_RELU, ("in", 0)), ("in", 1))), bf * 2, M.FLOAT16, "r")
+    assert guard_lines(k.source) == [] and "qe" not in k.source
+    k = M.FusedKernel(flatten((N_ADD, (N_GELU, ("in", 0)), ("in", 1))), bf * 2, M.FLOAT16, "p",
+                      flags=M.FUSION_PRECISE)
+    assert guard_lines(k.source) == []
+
+
+def test_chains_that_stream_f32_carry_one_plus_e_exactly():
+    silu = flatten((N_MUL, (N_SILU, ("in", 0)), ("in", 1)))
+    gelu = flatten((N_GELU, ("in", 0)))
+    bf, f32 = (M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_FULL, 0)
+    assert "mfh_silu_fast(x0, qe)" in M.FusedKernel(silu, [bf, bf], M.BFLOAT16, "s16").source
+    assert "mfh_silu_fast_x(x0, qe)" in M.FusedKernel(silu, [bf, bf], M.FLOAT32, "s32").source
+    assert "mfh_silu_fast_x(x0, qe)" in M.FusedKernel(silu, [f32, bf], M.BFLOAT16, "s32i").source
+    # a scalar f32 operand does not make the chain stream f32
+    assert "mfh_silu_fast(x0, qe)" in M.FusedKernel(silu, [bf, (M.FLOAT32, M.OPERAND_SCALAR, 0)],
+                                                    M.BFLOAT16, "ss").source
+    assert "mfh_gelu_fast_x(x0, qe)" in M.FusedKernel(gelu, [f32], M.FLOAT32, "g32").source
+    short = M.FusedKernel(gelu, [f32], M.FLOAT32, "g32s", flags=M.FUSION_SHORT_QUOTIENT)
+    assert "mfh_gelu_fast(x0, qe)" in short.source
+    # sigmoid's quotient is f64 either way
+    sig = M.FusedKernel(flatten((N_SIGMOID, ("in", 0))), [f32], M.FLOAT32, "sg")
+    assert "mfh_sigmoid_fast(x0, qe)" in sig.source
 
 
 def test_emit_hip_item_width_follows_the_widest_operand():

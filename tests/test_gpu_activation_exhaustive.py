@@ -1,9 +1,12 @@
 """Every f32 input through the device's fast Sigmoid, Silu and Gelu nodes.
 
 The fast forms run on the GPU over all 2^32 f32 bit patterns (in chunks)
-beside the MFH_FUSION_PRECISE forms, which restate the reference's f64
-formulas (codegen/cpu.go:186-200) and round once, so they are within one f32
-ulp of the oracle (they differ only where an f64 result sits at an f32
+beside the MFH_FUSION_PRECISE forms.  An f32 chain carries 1 + E exactly in
+Silu's and Gelu's quotient; the form 16-bit chains use (the rounding of
+1 + E left in) runs here through MFH_FUSION_SHORT_QUOTIENT, so both are
+measured over every f32 input.  The precise forms, which restate the
+reference's f64 formulas (codegen/cpu.go:186-200) and round once, are within
+one f32 ulp of the oracle (they differ only where an f64 result sits at an f32
 rounding tie that two f64 libraries round differently).  NaN positions must
 match.  Every input where the fast form is `tol` or more ulps from the
 precise form is then checked against the CPU oracle itself, which it must be
@@ -36,21 +39,25 @@ def ulp_key(bits):
     return torch.where(b < 0, -(b & 0x7FFFFFFF), b)
 
 
-@pytest.mark.parametrize("node", sorted(TOL))
-def test_fast_activation_every_f32_input(node):
+CASES = [(O.N_SIGMOID, 0), (O.N_SILU, 0), (O.N_SILU, M.FUSION_SHORT_QUOTIENT), (O.N_GELU, 0),
+         (O.N_GELU, M.FUSION_SHORT_QUOTIENT)]
+
+
+@pytest.mark.parametrize("node, flags", CASES)
+def test_fast_activation_every_f32_input(node, flags):
     import torch
     M.init(0)
     tol = TOL[node]
     nodes = O.flatten((node, ("in", 0)))
     ops = [(M.FLOAT32, M.OPERAND_FULL, 0)]
-    fast_k = M.FusedKernel(nodes, ops, M.FLOAT32, f"exh_fast_{node}")
+    fast_k = M.FusedKernel(nodes, ops, M.FLOAT32, f"exh_fast_{node}", flags)
     precise_k = M.FusedKernel(nodes, ops, M.FLOAT32, f"exh_precise_{node}", M.FUSION_PRECISE)
     fast = torch.empty(CHUNK, dtype=torch.int32, device="cuda")
     precise = torch.empty(CHUNK, dtype=torch.int32, device="cuda")
     hist = torch.zeros(tol + 3, dtype=torch.int64, device="cuda")
     candidates = []
     for c in range((1 << 32) // CHUNK):
-        log(f"node {node}: bit patterns [{c * CHUNK:#x}, {(c + 1) * CHUNK:#x})")
+        log(f"node {node} flags {flags}: bit patterns [{c * CHUNK:#x}, {(c + 1) * CHUNK:#x})")
         x = (torch.arange(c * CHUNK, (c + 1) * CHUNK, dtype=torch.int64, device="cuda") - (1 << 31)).to(torch.int32)
         fast_k.launch([x.data_ptr()], fast.data_ptr(), CHUNK, stream())
         precise_k.launch([x.data_ptr()], precise.data_ptr(), CHUNK, stream())
@@ -65,7 +72,7 @@ def test_fast_activation_every_f32_input(node):
         if idx.numel():
             candidates.append(torch.stack([x[idx], fast[idx]], 1).cpu().numpy())
     h = hist.tolist()
-    log(f"node {node}: ulps from the precise form {h} (last bin: {tol + 2} or more)")
+    log(f"node {node} flags {flags}: ulps from the precise form {h} (last bin: {tol + 2} or more)")
     assert sum(h) == 1 << 32
     assert h[0] / (1 << 32) > 0.95, f"node {node}: only {h[0] / (1 << 32):.4f} identical to the precise form"
     if not candidates:
@@ -73,7 +80,31 @@ def test_fast_activation_every_f32_input(node):
     a = np.concatenate(candidates)
     want = O.eval_unary(node, a[:, 0].view(np.float32)).view(np.int32)
     dd = np.abs(ulp_key(a[:, 1]) - ulp_key(want))
-    log(f"node {node}: {a.shape[0]} inputs {tol}+ ulps from the precise form, at most {int(dd.max())} from the oracle")
+    log(f"node {node} flags {flags}: {a.shape[0]} inputs {tol}+ ulps from the precise form, at most {int(dd.max())} from the oracle")
     i = int(np.argmax(dd))
     assert dd.max() <= tol, (f"node {node}: {int(dd.max())} ulp from the oracle at x bits {a[i, 0] & 0xFFFFFFFF:#x}: "
                              f"got {a[i, 1] & 0xFFFFFFFF:#x} want {want[i] & 0xFFFFFFFF:#x}")
+
+
+@pytest.mark.parametrize("node", [O.N_SIGMOID, O.N_SILU, O.N_GELU, O.N_EXP, O.N_LOG, O.N_TANH])
+def test_precise_forms_against_the_oracle(node):
+    # The MFH_FUSION_PRECISE forms (and the flagged elements of the fast
+    # kernels, which run the same functions) against the CPU oracle itself on
+    # every 251st f32 bit pattern: within 1 f32 ulp, identical almost always.
+    import torch
+    from gpu_util import oracle_run_parallel
+    M.init(0)
+    nodes = O.flatten((node, ("in", 0)))
+    k = M.FusedKernel(nodes, [(M.FLOAT32, M.OPERAND_FULL, 0)], M.FLOAT32, f"precise_{node}", M.FUSION_PRECISE)
+    x = (torch.arange(0, 1 << 32, 251, dtype=torch.int64, device="cuda") - (1 << 31)).to(torch.int32)
+    out = torch.empty_like(x)
+    k.launch([x.data_ptr()], out.data_ptr(), x.numel(), stream())
+    got = out.cpu().numpy()
+    xs = x.cpu().numpy().view(np.float32)
+    log(f"node {node}: {xs.size} inputs through the oracle")
+    want = oracle_run_parallel(nodes, [xs], xs.size, align=1).view(np.int32)
+    nan_g, nan_w = (got & 0x7FFFFFFF) > 0x7F800000, (want & 0x7FFFFFFF) > 0x7F800000
+    assert np.array_equal(nan_g, nan_w), f"node {node}: NaN positions differ"
+    d = np.abs(ulp_key(got[~nan_w]) - ulp_key(want[~nan_w]))
+    log(f"node {node}: precise form vs oracle: max {int(d.max())} ulp, {float(np.mean(d == 0)):.7f} identical")
+    assert d.max() <= 1 and np.mean(d == 0) > 0.9999, f"node {node}: max {int(d.max())} ulp"

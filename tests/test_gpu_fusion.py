@@ -193,11 +193,13 @@ def test_storage_dtypes_tails_misaligned(in_dt, out_dt, count, pad):
     silu = O.eval_unary(O.N_SILU, gf)
     tail = lambda s: O.encode((s * uf).astype(np.float32) + np.float32(-0.5), out_dt)  # noqa: E731
     # f32 outputs show every silu ulp (cancellation near -0.5 amplifies it),
-    # 16-bit outputs hide most of them.  The fast Silu leaves the rounding of
-    # 1 + e^-v in its quotient (within its 2-ulp budget), which for inputs of
-    # this size keeps about 82% of the f32 results bit-identical (a fraction
-    # that says nothing for a handful of elements).
-    exact_floor = (0.75 if out_dt == O.FLOAT32 else 0.99) if count >= 1000 else 0.0
+    # 16-bit outputs hide most of them.  Chains that stream f32 carry 1 + e^-v
+    # exactly in the quotient; the floors hold with margin for these seeds
+    # (the 3-element case: at least one of three).
+    if out_dt == O.FLOAT32 or in_dt == O.FLOAT32:
+        exact_floor = 0.9 if count >= 1000 else 0.3
+    else:
+        exact_floor = 0.99 if count >= 1000 else 0.3
     check_envelope(got, silu, tail, out_dt, 2, f"{in_dt}->{out_dt} n={count} pad={pad}", min_exact=exact_floor)
     want = O.encode(O.run(nodes, [gf, uf], count), out_dt)
     assert np.array_equal(want.view(np.uint8), tail(silu).view(np.uint8))  # the tail restates the chain
@@ -238,9 +240,9 @@ def test_swiglu_config3_full_size(flags):
 def test_gelu_chain_config4_full_size(flags):
     # gelu_tanh((x + bias) * s) + residual, f16 [4, 4096, 4096],
     # bias [4096] ~ N(0, 0.02) broadcast along rows, s = fl32(1.1) scalar -> f16.
-    # Fast Gelu: every result inside the 2-ulp gelu-node envelope; where the
-    # residual add cancels, that envelope is wider than 1 f16 ulp, so the
-    # count and the worst case of those results are reported.
+    # Fast Gelu: every result inside the 2-ulp gelu-node envelope, and at
+    # most 1 f16 ulp from the oracle: where the residual add cancels the
+    # kernel's guard recomputes the element with the reference gelu.
     # MFH_FUSION_PRECISE: at most 1 f16 ulp from the oracle everywhere.
     n = 4 * 4096 * 4096
     rng = np.random.default_rng(0x5EED + 4)
@@ -270,8 +272,38 @@ def test_gelu_chain_config4_full_size(flags):
                   f"gelu node {g[i]!r}, got {got[i]:#06x} want {want[i]:#06x}")
     log(f"gelu chain config 4 (flags {flags}): bit-identical fraction {exact:.6f}, max f16 ulp {int(d.max())}, "
         f"results more than 1 f16 ulp off: {over.size} of {n}{detail}")
-    if flags:
-        assert d.max() <= 1, f"precise gelu chain: {int(d.max())} f16 ulps"
+    assert d.max() <= 1, f"gelu chain (flags {flags}): {int(d.max())} f16 ulps{detail}"
+
+
+@pytest.mark.parametrize("act", [O.N_GELU, O.N_SILU])
+@pytest.mark.parametrize("out_dt", [O.FLOAT16, O.BFLOAT16])
+@pytest.mark.parametrize("op", [O.N_ADD, O.N_SUB])
+@pytest.mark.parametrize("count, pad", [(8 * 8192, 0), (8 * 8192 + 5, 1)])
+def test_cancellation_after_a_fast_activation_within_one_storage_ulp(act, out_dt, op, count, pad):
+    # act(v) + r (or - r) where r is the activation's value rounded to the
+    # storage dtype, give or take two storage ulps, on three elements in four:
+    # the sum is the activation's own rounding error, so a 2-ulp f32 node
+    # error would be many storage ulps of it (an f16 denormal, typically).
+    # The cancellation guard sends those elements to the reference form, and
+    # every result stays within one storage ulp of the oracle.  pad > 0 loses
+    # the 16-byte alignment, so the element loop's guard runs instead.
+    rng = np.random.default_rng(7000 + 97 * act + 13 * out_dt + op + count + pad)
+    v = O.encode(rng.normal(0, 2, count).astype(np.float32), out_dt)
+    vf = O.decode(v, out_dt)
+    near = O.encode(O.eval_unary(act, vf), out_dt).astype(np.int32)
+    key = np.where(near & 0x8000, 0x8000 - near, near) + rng.integers(-2, 3, count)  # monotone line
+    near = np.where(key < 0, 0x8000 - key, key).astype(np.uint16)
+    r = near ^ np.uint16(0x8000) if op == O.N_ADD else near
+    free = rng.random(count) < 0.25
+    r[free] = O.encode(rng.normal(0, 2, int(free.sum())).astype(np.float32), out_dt)
+    nodes = O.flatten((op, (act, ("in", 0)), ("in", 1)))
+    got = run_fused(nodes, [(out_dt, M.OPERAND_FULL, 0)] * 2, [v, r], out_dt, count, pads=[pad, pad],
+                    name="cancel")
+    want = O.encode(O.run(nodes, [vf, O.decode(r, out_dt)], count), out_dt)
+    worst = compare_storage(got, want, out_dt, 1, f"cancellation act {act} op {op} out {out_dt} n {count}")
+    exact = float(np.mean(got.view(np.uint16) == want.view(np.uint16)))
+    log(f"cancellation act {act} op {op} out {out_dt} n {count} pad {pad}: max {worst} storage ulp, "
+        f"{exact:.6f} bit-identical")
 
 
 def test_periodic_operand_not_multiple_of_8():
