@@ -13,6 +13,7 @@
 // state outlive a released backend handle until the last tensor handle goes,
 // so a stale tensor reports closed instead of touching freed memory.
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -41,6 +42,9 @@ struct Storage {
     bool pending = false;
     hipEvent_t done = nullptr;       // recorded after the last queued work that touches it
     hipStream_t writer = nullptr;    // stream of the last resident axpy that wrote it
+    // Set once mfh_tensor_dispatch_pointer has handed the device address out:
+    // the caller's own launches on it are not ordered through `done`.
+    std::atomic<bool> exposed{false};
 };
 
 struct BackendState {
@@ -179,6 +183,14 @@ int tensor_ok(const mfh_tensor* t)
     if (!t) return fail(MFH_ERR_INVALID_ARGUMENT, "tensor is NULL");
     if (tensor_dead(t)) return fail(MFH_ERR_TENSOR_CLOSED, "tensor: closed");
     return MFH_OK;
+}
+
+// The device address of a live tensor, for this library's own launches,
+// which order themselves through the storage's `done` event.
+void* device_address(const mfh_tensor* t)
+{
+    if (tensor_dead(t) || !t->storage->ptr) return nullptr;
+    return static_cast<uint8_t*>(t->storage->ptr) + t->offset;
 }
 
 }  // namespace
@@ -640,8 +652,9 @@ int32_t mfh_tensor_state(const mfh_tensor* t)
 
 void* mfh_tensor_dispatch_pointer(const mfh_tensor* t)
 {
-    if (tensor_dead(t) || !t->storage->ptr) return nullptr;
-    return static_cast<uint8_t*>(t->storage->ptr) + t->offset;
+    void* p = device_address(t);
+    if (p) t->storage->exposed.store(true, std::memory_order_relaxed);
+    return p;
 }
 
 int mfh_tensor_sync(mfh_tensor* t)
@@ -701,15 +714,20 @@ int mfh_tensor_close(mfh_tensor* t)
     MFH_TRY(bind_device(&dev));
     std::lock_guard<std::mutex> lock(t->backend->mu);
     Storage& st = *t->storage;
+    // Close blocks until the tensor's own queued work is done (tensor.Tensor
+    // Close drains in-flight async ops): uploads, resident axpys and graph
+    // calls on any backend's stream, the last of which `done` follows.  Other
+    // work on the device is not waited for.
     int rc = wait_storage(st);
     if (st.done) (void)hipEventDestroy(st.done);
     st.done = nullptr;
     if (st.ptr) {
-        // Work on any stream may still use the block, including the
-        // caller's own launches on its dispatch pointer: the device-wide
-        // wait that hipFree would make first makes it idle, and an idle block
+        // A block whose address was handed out may still be in use by the
+        // caller's own launches, on any stream: only a device-wide wait (the
+        // one hipFree would make) orders after those.  The idle block then
         // goes to the backend's cache.
-        int frc = check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        int frc = st.exposed.load(std::memory_order_relaxed) ? check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize")
+                                                             : MFH_OK;
         frc = frc == MFH_OK && rc == MFH_OK ? t->backend->release(st.ptr, st.bytes)
                                             : check_hip(hipFree(st.ptr), "hipFree");
         if (rc == MFH_OK) rc = frc;
@@ -757,7 +775,7 @@ int mfh_axpy_onto_resident(mfh_backend* backend, mfh_tensor* y, const mfh_tensor
     for (Storage* st : {&ys, &xs})
         if (st->pending && st->done)
             MFH_TRY(check_hip(hipStreamWaitEvent(s.stream, st->done, 0), "hipStreamWaitEvent"));
-    mfh_axpy(mfh_tensor_dispatch_pointer(y), mfh_tensor_dispatch_pointer(x), y->elements, alpha, y->dtype, s.stream);
+    mfh_axpy(device_address(y), device_address(x), y->elements, alpha, y->dtype, s.stream);
     // Later readers of y, and closes of either tensor through its own
     // backend, wait for this launch.
     MFH_TRY(mark_pending(ys, s.stream));
@@ -791,7 +809,7 @@ int mfh_backend_graph_call(mfh_backend* backend, mfh_graph* graph, const char* c
     for (int32_t k = 0; k < n_inputs; k++) {
         MFH_TRY(tensor_ok(inputs[k]));
         const mfh_tensor& t = *inputs[k];
-        ins[k] = mfh_value{input_names[k], mfh_tensor_dispatch_pointer(&t), t.dtype, {0}, t.elements};
+        ins[k] = mfh_value{input_names[k], device_address(&t), t.dtype, {0}, t.elements};
     }
     // One flat tensor per output key, of the dtype and length the call gives it.
     std::vector<std::unique_ptr<mfh_tensor>> made;

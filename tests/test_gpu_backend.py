@@ -370,3 +370,47 @@ def test_graph_call_over_resident_tensors():
     finally:
         b.release()
         a.release()
+
+
+def test_close_waits_for_its_own_work_not_the_device():
+    # tensor.Tensor.Close drains the tensor's own in-flight work
+    # (tensor/tensor.go:66-70) and nothing else: with a long run of resident
+    # axpys queued on backend B, closing an idle tensor of backend A returns
+    # while they still run; closing a tensor that they read waits for its last
+    # use; a tensor whose device address was handed out (the caller may have
+    # launched on it anywhere) waits for the whole device.
+    import torch
+    a, b = Backend(0), Backend(0)
+    try:
+        n = 1 << 26  # 256 MiB of f32: one axpy streams 768 MiB, about 0.13 ms
+        ones = np.ones(n, np.float32)
+        y = b.upload([n], O.FLOAT32, np.zeros(n, np.float32))
+        xb = b.upload([n], O.FLOAT32, ones)
+        xa = a.upload([n], O.FLOAT32, ones)
+        idle = a.upload([1024], O.FLOAT32, np.arange(1024, dtype=np.float32))
+        log("close: queueing 400 axpys on backend B")
+        for _ in range(400):  # about 50 ms of device work
+            b.axpy_onto_resident(y, xb, 1.0)
+        for _ in range(8):  # the last reads of xa
+            b.axpy_onto_resident(y, xa, 1.0)
+        assert y.state() == STATE_PENDING
+        idle.close()
+        assert y.state() == STATE_PENDING, "closing an unrelated tensor waited for another backend's work"
+        xa.close()
+        assert y.state() == STATE_READY, "closing a tensor returned before the work that reads it"
+        # a handed-out address: the caller's own launch on another stream
+        xe = a.upload([n], O.FLOAT32, ones)
+        s = torch.cuda.current_stream()
+        for _ in range(100):
+            M.axpy(y.dispatch_pointer(), xe.dispatch_pointer(), n, 1.0, M.FLOAT32, s.cuda_stream)
+        done = torch.cuda.Event()
+        done.record(s)
+        xe.close()
+        assert done.query(), "closing a tensor with a handed-out address returned before the device was idle"
+        got = np.frombuffer(b.download(y)[1], np.float32)
+        assert np.all(got == 508.0)
+        xb.close()
+        y.close()
+    finally:
+        b.release()
+        a.release()
