@@ -203,13 +203,13 @@ typedef struct {
  * without it Sigmoid/Silu/Gelu use f32 algorithms within 2 ulp. */
 #define MFH_FUSION_PRECISE 1u
 
-/* Silu and Gelu keep the rounding of 1 + E in their quotient in every chain
- * (the form chains of 16-bit operands always use; within the same 2-ulp node
- * budget).  Without it a chain that streams f32 (an f32 output or a full or
- * periodic f32 operand) carries 1 + E exactly, four VALU instructions more
- * per element, since its results show every f32 ulp of the node.  For
- * measuring the 16-bit chains' form over f32 results; no counterpart in the
- * reference. */
+/* Silu and Gelu in their f32 fast forms in every chain (the forms chains of
+ * 16-bit operands always use: the rounding of 1 + E left in the quotient,
+ * within the 2-ulp node budget).  Without it a chain that streams f32 (an f32
+ * output or a full or periodic f32 operand) evaluates them in f64, about
+ * twice the instructions, since its results show every f32 ulp of the node.
+ * For measuring the 16-bit chains' forms over f32 results; no counterpart in
+ * the reference. */
 #define MFH_FUSION_SHORT_QUOTIENT 2u
 
 typedef struct mfh_kernel mfh_kernel;

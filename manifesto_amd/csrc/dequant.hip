@@ -59,6 +59,20 @@ MFH_DEV void store_one(void* out, mfh_i64 i, mfh_u32 enc)
 // 0.8% that way and stay plain).
 // Measured at [4096, 14336] on MI355X with the codes coming from HBM:
 // 6.1-6.2 TB/s, within 3% of a bf16 -> f32 cast moving the same bytes.
+// One table entry's decode by gfx950's converter (v_cvt_f32_fp8 /
+// v_cvt_f32_bf8), which decodes every finite and infinite OCP E4M3 / E5M2
+// code exactly and writes one canonical NaN for every NaN code; NaN codes
+// take the reference's bits instead, which keep the sign and, for E5M2, the
+// two mantissa bits (dtype/fp8.go:43-45,155-161).  Branch-free, a few VALU
+// instructions per entry where the integer decode (mfh_e4m3_bits /
+// mfh_e5m2_bits) normalises subnormals in divergent branches.
+MFH_DEV mfh_u32 fp8_bits_hw(mfh_u32 code, bool e5m2)
+{
+    const float f = e5m2 ? __builtin_amdgcn_cvt_f32_bf8((int)code, 0) : __builtin_amdgcn_cvt_f32_fp8((int)code, 0);
+    const mfh_u32 nan = ((code & 0x80u) << 24) | 0x7fc00000u | (e5m2 ? (code & 3u) << 21 : 0u);
+    return f != f ? nan : mfh_bits(f);
+}
+
 template <int OUT, int U, int BS>
 __global__ __launch_bounds__(BS) void k_dequant_fp8(const mfh_u8* __restrict__ in,
                                                         void* __restrict__ out, mfh_i64 n,
@@ -83,10 +97,8 @@ __global__ __launch_bounds__(BS) void k_dequant_fp8(const mfh_u8* __restrict__ i
     };
     mfh_i64 c = blockIdx.x;
     if (c < nchunks) load(c);
-    for (mfh_u32 e = t; e < 256; e += BS) {
-        mfh_u32 bits = fmt == kF8E4M3 ? mfh_e4m3_bits(e) : mfh_e5m2_bits(e);
-        lut[e] = encode_one<OUT>(mfh_scale_mul(mfh_f32(bits), scale));
-    }
+    for (mfh_u32 e = t; e < 256; e += BS)
+        lut[e] = encode_one<OUT>(mfh_scale_mul(mfh_f32(fp8_bits_hw(e, fmt == kF8E5M2)), scale));
     __syncthreads();
     for (; c < nchunks; c += gridDim.x) {
         if (c != (mfh_i64)blockIdx.x) load(c);
@@ -166,17 +178,37 @@ __global__ __launch_bounds__(BS) void k_dequant_int4(const mfh_u8* __restrict__ 
     const int t = (int)threadIdx.x;
     for (mfh_i64 c = blockIdx.x; c < nchunks; c += gridDim.x) {
         const mfh_i64 first = c * kChunk;
+        // Lane addresses are 32-bit offsets from uniform bases: the chunk's
+        // first packed item and its first item's group scale (element e0,
+        // group g0, e0 = g0 * group + r).  Items past the end load the last
+        // item instead of branching: a guarded load made the compiler wait
+        // for each scale inside its branch, one round trip per item, before
+        // issuing the next item's loads (5.3 against 6.2 TB/s).
+        const int last = (int)min<mfh_i64>(kChunk, nitems - first) - 1;
+        const mfh_i64 e0 = first * kElems;
+        const mfh_i64 g0 = e0 >> group_shift;
+        const mfh_u64 r = (mfh_u64)(e0 - (g0 << group_shift));
+        constexpr mfh_u32 kItemBytes = kElems / 2, kScaleBytes = SDT == kFloat32 ? 4 : 2;
+        const char* items = reinterpret_cast<const char*>(packed) + first * kItemBytes;
+        const char* group0 = static_cast<const char*>(scales) + g0 * kScaleBytes;
+        // The item's group relative to g0 is (r + j kElems) >> group_shift.
+        // A chunk spans fewer than 2^20 elements, so for larger groups the
+        // same formula with shift 20 and r' = 2^20 - (elements from e0 to
+        // the next group boundary), or 0 when that boundary lies past the
+        // chunk, gives the same 0 or 1: every item runs one 32-bit add and
+        // shift.
+        static_assert(kChunk * kElems < (1 << 20), "a chunk spans fewer than 2^20 elements");
+        const bool small_group = group_shift <= 20;
+        const mfh_u64 to_next = (1ull << min(group_shift, 62)) - r;
+        const mfh_u32 gr = small_group ? (mfh_u32)r : to_next >= (1u << 20) ? 0u : (1u << 20) - (mfh_u32)to_next;
+        const int gs = small_group ? group_shift : 20;
         mfh_u32 w[U], sb[U];
-        // Items past the end load the last item instead of branching: a
-        // guarded load made the compiler wait for each scale inside its
-        // branch, one round trip per item, before issuing the next item's
-        // loads (5.3 against 6.2 TB/s).
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const mfh_i64 i = min(first + u * BS + t, nitems - 1);
-            if constexpr (kElems == 8) w[u] = reinterpret_cast<const mfh_u32*>(packed)[i];
-            else w[u] = reinterpret_cast<const mfh_u16*>(packed)[i];
-            sb[u] = scale_bits<SDT>(scales, (i * kElems) >> group_shift);
+            const mfh_u32 j = (mfh_u32)min(u * BS + t, last);
+            if constexpr (kElems == 8) w[u] = *reinterpret_cast<const mfh_u32*>(items + j * kItemBytes);
+            else w[u] = *reinterpret_cast<const mfh_u16*>(items + j * kItemBytes);
+            sb[u] = scale_bits<SDT>(group0 + ((gr + j * kElems) >> gs) * kScaleBytes, 0);
         }
         __builtin_amdgcn_sched_barrier(0);  // every load of the chunk ahead of the first wait
         float s[U];

@@ -154,22 +154,6 @@ MFH_MATH float mfh_div_one_plus(float n, float e)
     return mfh_fmaf(res, r, q);
 }
 
-// n / (1 + e) for the exact 1 + e: d = fl(1 + e) and its rounding error
-// dl = min(1, e) - (d - max(1, e)) (Fast2Sum: both terms are positive and the
-// larger goes first) both enter the residual, so the quotient is corrected for
-// the reciprocal's error and for d's rounding.  Four VALU instructions more
-// than mfh_div_one_plus; chains that stream f32 use it (f32 results show the
-// rounding of d, 16-bit results hide it), and 1 + e may then be a rounding tie.
-MFH_MATH float mfh_div_one_plus_exact(float n, float e)
-{
-    const float d = 1.0f + e;
-    const float dl = mfh_minf(e, 1.0f) - (d - mfh_maxf(e, 1.0f));
-    const float r = mfh_rcpf(d);
-    const float q = n * r;
-    const float res = mfh_fmaf(-q, dl, mfh_fmaf(-q, d, n));
-    return mfh_fmaf(res, r, q);
-}
-
 MFH_MATH bool mfh_is_inf(float v) { return (mfh_fbits(v) & 0x7fffffffu) == 0x7f800000u; }
 MFH_MATH bool mfh_is_nan(float v) { return (mfh_fbits(v) & 0x7fffffffu) > 0x7f800000u; }
 
@@ -245,14 +229,29 @@ MFH_MATH float mfh_silu_fast(float v, bool& rare)
     return mfh_div_one_plus(v, mfh_exp_neg(m));
 }
 
-// The same with the exact 1 + e^-v (mfh_div_one_plus_exact), for chains that
-// stream f32: within 2 f32 ulps and bit-identical to the reference for more
-// inputs, at four more VALU instructions per element.
+// silu for chains that stream f32 (their results show every f32 ulp of the
+// node): the whole computation in f64, as the fast sigmoid makes it, e^-v =
+// 2^t by the round-to-integer reduction and the degree-8 polynomial
+// (2^-39.9), the reciprocal of 1 + e^-v plus one Newton step, times v, one
+// rounding.  The f32 result is the reference's except where the exact value
+// lies within about 2^-39 of an f32 rounding boundary.  Below -708 (and
+// -Inf, NaN) the reference's form; +Inf gives +Inf by itself.  About twice
+// the instructions of mfh_silu_fast, which the 4-byte elements of such a
+// chain leave room for.
+MFH_MATH double mfh_recip_one_plus_2exp(double t)
+{
+    const double tk = t + MFH_ROUND_INT_D;
+    const double kd = tk - MFH_ROUND_INT_D;
+    const double den = 1.0 + mfh_ldexp(mfh_exp2_poly_d(t - kd), mfh_low_int(tk));
+    const double r = mfh_rcp(den);
+    return mfh_fma(r, mfh_fma(-den, r, 1.0), r);
+}
+
 MFH_MATH float mfh_silu_fast_x(float v, bool& rare)
 {
-    const float m = mfh_med3f(v, -16.5f, 87.0f);
-    rare |= m != v;
-    return mfh_div_one_plus_exact(v, mfh_exp_neg(m));
+    const double x = (double)mfh_med3f(v, -708.0f, 800.0f);
+    rare |= !(v >= -708.0f);
+    return (float)((double)v * mfh_recip_one_plus_2exp(x * -MFH_LOG2E_D));
 }
 
 // Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
@@ -287,12 +286,15 @@ MFH_MATH float mfh_gelu_fast(float v, bool& rare)
     return mfh_div_one_plus(v, mfh_gelu_e(c));
 }
 
-// With the exact 1 + E, for chains that stream f32 (as mfh_silu_fast_x).
+// gelu for chains that stream f32: the same argument t = d w in f64, then
+// 2^t, the quotient and the product with v in f64 as mfh_silu_fast_x makes
+// them, one rounding.
 MFH_MATH float mfh_gelu_fast_x(float v, bool& rare)
 {
     const float c = mfh_med3f(v, -4.9f, 1024.0f);
     rare |= c != v;
-    return mfh_div_one_plus_exact(v, mfh_gelu_e(c));
+    const double d = (double)c;
+    return (float)((double)v * mfh_recip_one_plus_2exp(mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA) * d));
 }
 
 // mfh_<name>_rare: the reference form as a real call (MFH_RARE), which the

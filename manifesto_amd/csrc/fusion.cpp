@@ -178,8 +178,7 @@ struct Emitter {
     const std::vector<int>& c0;
     const std::vector<int>& c1;
     Form form;
-    // Silu and Gelu with the exact 1 + E in their quotient (mfh_*_fast_x):
-    // chains that stream f32.
+    // Silu and Gelu in their f64 forms (mfh_*_fast_x): chains that stream f32.
     bool exact_tail = false;
     const std::vector<Guard>* guards = nullptr;  // kFast only
     std::string prefix = "t";
@@ -207,7 +206,7 @@ struct Emitter {
         if (form == Form::kPrecise) return let(fn + "_ref(" + a + ")");
         if (form == Form::kFallback) return let(fn + "_rare(" + a + ")");
         flagged = true;
-        const bool x = exact_tail && std::string(name) != "sigmoid";  // sigmoid's quotient is f64
+        const bool x = exact_tail && std::string(name) != "sigmoid";  // sigmoid's fast form is f64 already
         return let(fn + (x ? "_fast_x(" : "_fast(") + a + ", qe)");
     }
 
@@ -591,9 +590,15 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // and the precise (f64 library) forms gain nothing.  Workgroups of one
     // wave (kFusedThreads).  mfh_set_launch_config("fused", ...) and
     // mfh_set_launch_threads("fused", ...) override these.
+    // Chains that stream f32 take Silu and Gelu in f64 forms: their results
+    // show every f32 ulp of the node, and their 4-byte elements leave room
+    // for about twice the instructions (MFH_FUSION_SHORT_QUOTIENT keeps the
+    // 16-bit chains' forms).
+    const bool exact_tail = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
     bool f64_fast = false;
     for (const mfh_ast_node& node : list)
-        if (!precise && node.type == kNodeSigmoid) f64_fast = true;
+        if (!precise && (node.type == kNodeSigmoid || (exact_tail && (node.type == kNodeSilu || node.type == kNodeGelu))))
+            f64_fast = true;
     const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : f64_fast ? 2 : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
     const int block = threads_per_block(Kern::kFused) > 0 ? threads_per_block(Kern::kFused) : kFusedThreads;
@@ -609,11 +614,8 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // MFH_FUSION_PRECISE each element runs the fast forms and the planned
     // cancellation guards, which set its flag `qe`; flagged elements are then
     // recomputed with the reference forms (real calls), so the item's main
-    // body has no branch.  Chains that stream f32 take Silu and Gelu with the
-    // exact 1 + E (their results show every f32 ulp; four VALU instructions
-    // more per element, where a 16-bit chain's bytes would not cover them).
+    // body has no branch.
     const Form main_form = precise ? Form::kPrecise : Form::kFast;
-    const bool exact_tail = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
     const std::vector<Guard> guards = plan_guards(list, c0, c1, out_dtype, precise);
     std::vector<bool> packed16(n_inputs, false);
     for (int k = 0; k < n_inputs; k++)

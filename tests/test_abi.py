@@ -134,7 +134,7 @@ def test_cancellation_guard_counts_the_error_on_its_operands():
     assert guard_lines(k.source) == []
 
 
-def test_chains_that_stream_f32_carry_one_plus_e_exactly():
+def test_chains_that_stream_f32_take_the_f64_forms():
     silu = flatten((N_MUL, (N_SILU, ("in", 0)), ("in", 1)))
     gelu = flatten((N_GELU, ("in", 0)))
     bf, f32 = (M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_FULL, 0)
@@ -147,9 +147,11 @@ def test_chains_that_stream_f32_carry_one_plus_e_exactly():
     assert "mfh_gelu_fast_x(x0, qe)" in M.FusedKernel(gelu, [f32], M.FLOAT32, "g32").source
     short = M.FusedKernel(gelu, [f32], M.FLOAT32, "g32s", flags=M.FUSION_SHORT_QUOTIENT)
     assert "mfh_gelu_fast(x0, qe)" in short.source
-    # sigmoid's quotient is f64 either way
+    # sigmoid's fast form is f64 either way; f64 forms take two items per thread
     sig = M.FusedKernel(flatten((N_SIGMOID, ("in", 0))), [f32], M.FLOAT32, "sg")
-    assert "mfh_sigmoid_fast(x0, qe)" in sig.source
+    assert "mfh_sigmoid_fast(x0, qe)" in sig.source and "2 item(s) per thread" in sig.source
+    assert "2 item(s) per thread" in M.FusedKernel(gelu, [f32], M.FLOAT32, "g32u").source
+    assert "1 item(s) per thread" in short.source
 
 
 def test_emit_hip_item_width_follows_the_widest_operand():

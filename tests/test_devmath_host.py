@@ -7,8 +7,8 @@ which the residual step that follows it makes immaterial, and gelu's
 v_exp_f32 by libm's exp2f, which is more accurate (the device gelu is
 checked over every f32 input by test_gpu_activation_exhaustive.py).  A strided sweep over all 2^32 f32 bit patterns
 is checked against the oracle's restatement of codegen/cpu.go:186-200:
-Sigmoid, Exp, Log, Tanh within 1 f32 ulp, Silu and Gelu within 2 (with and
-without the exact 1 + E of f32 chains), the
+Sigmoid, Exp, Log, Tanh within 1 f32 ulp, Silu and Gelu within 2 (within 1
+in the f64 forms that chains streaming f32 use), the
 MFH_FUSION_PRECISE forms within 1, NaN exactly where the reference's is.
 """
 import os
@@ -35,7 +35,7 @@ def report(tmp_path_factory):
     return rows
 
 
-TOL = {"sigmoid": 1, "silu": 2, "gelu": 2, "silu_x": 2, "gelu_x": 2, "exp_ref": 1, "log_ref": 1, "tanh_ref": 1,
+TOL = {"sigmoid": 1, "silu": 2, "gelu": 2, "silu_x": 1, "gelu_x": 1, "exp_ref": 1, "log_ref": 1, "tanh_ref": 1,
        "sigmoid_ref": 1, "silu_ref": 1, "gelu_ref": 1}
 
 

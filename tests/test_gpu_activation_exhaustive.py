@@ -1,10 +1,10 @@
 """Every f32 input through the device's fast Sigmoid, Silu and Gelu nodes.
 
 The fast forms run on the GPU over all 2^32 f32 bit patterns (in chunks)
-beside the MFH_FUSION_PRECISE forms.  An f32 chain carries 1 + E exactly in
-Silu's and Gelu's quotient; the form 16-bit chains use (the rounding of
-1 + E left in) runs here through MFH_FUSION_SHORT_QUOTIENT, so both are
-measured over every f32 input.  The precise forms, which restate the
+beside the MFH_FUSION_PRECISE forms.  An f32 chain evaluates Silu and Gelu
+in f64; the f32 forms 16-bit chains use (the rounding of 1 + E left in the
+quotient) run here through MFH_FUSION_SHORT_QUOTIENT, so both are measured
+over every f32 input.  The precise forms, which restate the
 reference's f64 formulas (codegen/cpu.go:186-200) and round once, are within
 one f32 ulp of the oracle (they differ only where an f64 result sits at an f32
 rounding tie that two f64 libraries round differently).  NaN positions must

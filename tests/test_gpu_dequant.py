@@ -102,6 +102,19 @@ def test_int4_groups_and_dtypes(group, scale_dt, out_dt):
     int4_case(n, group, scale_dt, out_dt, scales, rng)
 
 
+@pytest.mark.parametrize("group, n", [(8192, 5 * 8192 + 4099), (1 << 21, 3 * (1 << 21) + 4099),
+                                      (1 << 22, (1 << 23) + 8), (1 << 23, (1 << 23) - 24)])
+def test_int4_groups_larger_than_a_chunk(group, n):
+    # A workgroup's chunk spans 4096 elements (bf16 out), so these groups
+    # start mid-chunk (8192) or take the large-group form of the scale index
+    # (past 2^20 elements), with partial last groups.
+    rng = np.random.default_rng(group + n)
+    scales = rng.uniform(-0.05, 0.05, size=n // group + 2).astype(np.float32)
+    log(f"int4 group={group} n={n}")
+    for out_dt in (O.BFLOAT16, O.FLOAT32):
+        int4_case(n, group, O.FLOAT16, out_dt, scales, rng)
+
+
 def test_int4_every_nibble_and_special_scales():
     rng = np.random.default_rng(11)
     specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 6e-8, 65504.0, -1.5, 1e-45, 3e38],
