@@ -10,11 +10,13 @@ inputs (four times the 256 MB Infinity Cache) and the footprint is at least
 twice that cache: the kernels' non-temporal stores do not displace cached
 inputs, so a rotation whose inputs alone fit in the cache (four FP8 sets hold
 235 MB of codes) measures cache reads, not HBM (FP8 then reads 7.07 against
-6.2 TB/s, Int4 6.8 against 5.1).  The timed steps are replayed from a
-captured HIP graph so the clock sees kernel time, not Python launch overhead;
-the W warm-up steps replay the same graph first, and a bounded GPU spin queued
-ahead of the start event keeps the host's graph launch latency out of the
-timed region.  After timing, a sample of the timed outputs is checked against
+6.2 TB/s, Int4 6.8 against 5.1).  The K timed launches are queued behind a
+bounded GPU spin, so the start event fires with all of them queued and the
+timed region holds exactly K back-to-back kernels, not Python launch
+overhead: up to 64 steps as eager launches behind a spin sized to the host's
+measured enqueue time (the host checks that the spin had not ended when its
+last launch was queued), more as one replay of a captured HIP graph
+(`--graph` always replays); the warm-up steps run first.  After timing, a sample of the timed outputs is checked against
 the oracle ("sample_check").  The other BASELINE configs (axpy, SwiGLU, the
 f16 gelu chain, Int4) are measured the same way and listed under "configs";
 the two chains also give their MFH_FUSION_PRECISE kernel's rate ("precise":
@@ -202,7 +204,8 @@ class SwiGLU(Workload):
     def compile(self, flags=0):
         """The chain's kernel: fast transcendentals, or with
         MFH_FUSION_PRECISE the reference's f64 forms."""
-        self.k = self.M.FusedKernel(self.nodes, [(self.M.BFLOAT16, 0, 0)] * 2, self.M.BFLOAT16, "swiglu", flags)
+        self.k = self.M.FusedKernel(self.nodes, [(self.M.BFLOAT16, 0, 0)] * 2, self.M.BFLOAT16,
+                                    "swiglu_precise" if flags else "swiglu", flags)
 
     def make_set(self):
         t = self.torch
@@ -258,7 +261,7 @@ class GeluChain(Workload):
         M = self.M
         ops = [(M.FLOAT16, M.OPERAND_FULL, 0), (M.FLOAT16, M.OPERAND_PERIODIC, 4096),
                (M.FLOAT32, M.OPERAND_SCALAR, 0), (M.FLOAT16, M.OPERAND_FULL, 0)]
-        self.k = M.FusedKernel(self.nodes, ops, M.FLOAT16, "gelu_chain", flags)
+        self.k = M.FusedKernel(self.nodes, ops, M.FLOAT16, "gelu_chain_precise" if flags else "gelu_chain", flags)
 
     def make_set(self):
         t = self.torch
@@ -449,7 +452,7 @@ class CastMix(Workload):
 def time_same_mix(kind, base, torch, M, O, args):
     w = kind(base, torch, M, O)
     w.setup()
-    ms, _, _ = time_gpu(w, args.steps, args.warmup, use_graph=not args.no_graph)
+    ms, _, _ = time_gpu(w, args.steps, args.warmup, use_graph=True if args.graph else None)
     gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
     op = w.op
     del w
@@ -459,42 +462,71 @@ def time_same_mix(kind, base, torch, M, O, args):
 
 def warm_steps(w, args):
     """Untimed launches time_gpu makes before the timed region."""
-    if args.no_graph:
-        return max(args.warmup, len(w.sets))
     return len(w.sets) + max(1, -(-args.warmup // args.steps)) * args.steps
 
 
-# Clock cycles of the bounded spin (torch.cuda._sleep) queued ahead of each
-# timed region: about half a millisecond, which the host needs far less than
-# to enqueue the start event, the K timed launches and the end event.
-GATE_CYCLES = 1_000_000
+# The bounded spin (torch.cuda._sleep) queued ahead of each timed region.
+GATE_BASE_US = 500  # graph replays
+GATE_EAGER_BASE_US = 200  # eager launches, plus 3 times the host's enqueue time for each
+# Up to this many timed steps are launched eagerly behind a spin sized to the
+# host's enqueueing; more are one replay of a captured HIP graph.
+EAGER_MAX_STEPS = 64
+_gate_cycles_per_us = None
 
 
-def time_gpu(w, steps, warmup, use_graph=True):
-    """Runs `warmup` untimed steps, then times exactly `steps` steps (each one
-    launch over the next rotated buffer set) between two events on the
-    launch stream.  With use_graph the `steps` launches are captured into one
-    HIP graph, the warm-up runs as ceil(warmup / steps) untimed replays of it
-    (at least one) and one more replay is timed, so the timed region holds
-    back-to-back kernels with no host launch gaps and follows the same load.
-    Under sustained load the board sits at its power cap and the clock
-    settles over the first tens of milliseconds; a warm-up of a few replays
-    times the settled state.
+def gate_cycles(torch, us):
+    """Spin cycles for about `us` microseconds: torch.cuda._sleep counts the
+    shader clock, calibrated once with two events around a fixed spin."""
+    global _gate_cycles_per_us
+    if _gate_cycles_per_us is None:
+        s = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(s)
+        torch.cuda._sleep(2_000_000)
+        b.record(s)
+        b.synchronize()
+        _gate_cycles_per_us = 2_000_000 / (a.elapsed_time(b) * 1e3)
+    return int(us * _gate_cycles_per_us)
 
-    After the warm-up the host synchronises, queues a bounded spin kernel
-    (GATE_CYCLES), then the start event, the timed launches and the end event,
-    and synchronises on the end event.  The spin keeps the GPU from reaching
-    the start event before the timed launches are queued: from an idle GPU the
-    start event would otherwise fire at once and the timed region would hold
-    the host's graph launch latency (20-35 us per replay, measured against
-    the kernels' own durations under rocprofv3), which at K = 20 is 4-7% of
-    a step.  The spin itself ends before the start event fires."""
+
+def time_gpu(w, steps, warmup, use_graph=None):
+    """Runs the untimed warm-up, then times exactly `steps` steps (each one
+    launch over the next rotated buffer set) between two events on the launch
+    stream, which a synchronize precedes and the end event's wait follows.
+    The warm-up is one launch per rotated set and then ceil(warmup / steps) *
+    steps more (at least `steps`), so the timed region follows the same load
+    whatever W is.  Under sustained load the board sits at its power cap and
+    the clock settles over the first tens of milliseconds.
+
+    In both forms a bounded spin kernel is queued ahead of the start event,
+    so the GPU reaches the start event only once every timed launch is
+    queued: the timed region holds exactly `steps` back-to-back kernels and
+    neither the host's launch overhead nor its latency.
+    - Up to EAGER_MAX_STEPS steps (use_graph None or False): eager launches
+      behind a spin of 0.2 ms plus three times the host's enqueue time per
+      launch (measured over the warm-up launches) for each timed launch.  The
+      host checks that the start event had not yet fired when its last
+      launch was queued; if it had, the region could hold host gaps and the
+      measurement is taken again behind a spin four times longer (at most
+      three times).
+    - More steps (or use_graph True): the launches are captured into one HIP
+      graph; the warm-up replays it and one replay is timed behind a 0.5 ms
+      spin.  The replay adds its own entry and exit, about 12 us per replay
+      by rocprofv3 against the kernels' own durations: under 0.1 us per step
+      at K = 200 but 1-3% of a step at K = 20, which is why small K launches
+      eagerly (whose spin would in turn grow long at large K).  At K = 20 the
+      eager form measured FP8 28.06 against 28.42 us, Int4 24.27 against
+      24.62 and axpy 31.12 against 31.43 (same process, alternating)."""
     torch = w.torch
-    for i in range(len(w.sets) if use_graph else max(warmup, len(w.sets))):
-        w.step(i)
-    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if use_graph is None:
+        use_graph = steps > EAGER_MAX_STEPS
     if use_graph:
+        for i in range(len(w.sets)):
+            w.step(i)
+        torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         cap = torch.cuda.Stream()
         with torch.cuda.stream(cap):
@@ -505,28 +537,38 @@ def time_gpu(w, steps, warmup, use_graph=True):
         for _ in range(max(1, -(-warmup // steps))):
             graph.replay()
         torch.cuda.synchronize()
-        s = torch.cuda.current_stream()
         t0 = time.perf_counter()
-        torch.cuda._sleep(GATE_CYCLES)
+        torch.cuda._sleep(gate_cycles(torch, GATE_BASE_US))
         start.record(s)
         graph.replay()
         end.record(s)
         end.synchronize()
         wall = time.perf_counter() - t0
-    else:
-        s = torch.cuda.current_stream()
+        return start.elapsed_time(end) / steps, steps, wall
+    warm = len(w.sets) + max(1, -(-warmup // steps)) * steps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warm):
+        w.step(i)
+    host_us = (time.perf_counter() - t0) * 1e6 / warm
+    gate_us = GATE_EAGER_BASE_US + 3 * host_us * steps
+    for _ in range(3):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        torch.cuda._sleep(GATE_CYCLES)
+        torch.cuda._sleep(gate_cycles(torch, gate_us))
         start.record(s)
         for i in range(steps):
             w.step(i)
         end.record(s)
+        queued_ahead = not start.query()
         end.synchronize()
         wall = time.perf_counter() - t0
-    n = steps
-    ms = start.elapsed_time(end) / n
-    return ms, n, wall
+        if queued_ahead:
+            break
+        log(f"time_gpu: the timed launches were not all queued within a {gate_us:.0f} us spin; again behind a "
+            "longer one")
+        gate_us *= 4
+    return start.elapsed_time(end) / steps, steps, wall
 
 
 def cpu_threads():
@@ -628,9 +670,9 @@ def fit_fixed_cost(points):
 def sweep_run(torch, M, O, steps, warmup):
     """--sweep: every BASELINE kernel at launch sizes from 1/64 to 4x its
     config's (the same workload, element count scaled and rounded to whole
-    4096-element rows), timed exactly as the bench times a step (a graph of
-    `steps` launches over rotated buffer sets, after the warm-up replays),
-    beside the library's cast that moves the same bytes in the same
+    4096-element rows), timed exactly as the bench times a step (`steps`
+    launches over rotated buffer sets queued behind the gate, after the
+    warm-up), beside the library's cast that moves the same bytes in the same
     read:write mix (CastMix).  One JSON line per kernel and size, then one per
     kernel with a fit of step time = fixed + bytes / rate over the 1/4, 1 and
     4x points for both: a kernel whose fixed cost matches the cast's pays
@@ -1074,12 +1116,15 @@ def summarize_trace(d, bench_json, timed_k):
             c, s = configs[prof_config(n)], stats[n]
             timed = statistics.mean(x for _, x in trace[n][-timed_k:])
             cast = c.get("cast_same_mix", {}).get("GB_s")
+            step = c.get("precise", {}) if n.endswith("_precise") else c  # the chain's MFH_FUSION_PRECISE kernel
+            if n.endswith("_precise"):
+                cast = None
             print(f"| `{n}` | {s['Calls']} | {float(s['AverageNs']):.0f} | {s['MinNs']} | {s['MaxNs']} | {timed:.0f} | "
-                  f"{c['bytes_per_step']} | {c['bytes_per_step'] / timed:.0f} | {c['ms_per_step'] * 1e6:.0f} | "
-                  f"{c['GB_s']:.0f} | {cast if cast is None else round(cast)} |")
+                  f"{c['bytes_per_step']} | {c['bytes_per_step'] / timed:.0f} | {step['ms_per_step'] * 1e6:.0f} | "
+                  f"{step['GB_s']:.0f} | {'-' if cast is None else round(cast)} |")
         print("\n| kernel | timed avg ns | " + " | ".join(f"{a}–{b} ms" for a, b in PROF_WINDOWS_MS) +
               " | worst 20 |\n|" + "---|" * (len(PROF_WINDOWS_MS) + 3))
-        for n in order:
+        for n in (n for n in order if not n.endswith("_precise")):
             replay = trace[n][configs[prof_config(n)]["rotated_sets"]:]  # after the eager launch per set
             settled = statistics.mean(x for _, x in trace[n][-timed_k:])
             cells, worst = prof_windows(replay, settled)
@@ -1178,7 +1223,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="time one replay of a captured HIP graph of the K launches at every K")
     ap.add_argument("--no-torch", action="store_true",
                     help="skip the same-mix streams (library cast, torch) of each config")
     ap.add_argument("--only", type=int, default=0, help="measure only this BASELINE config")
@@ -1259,7 +1305,7 @@ def main():
             continue
         w = cls(torch, M, O)
         w.setup()
-        ms, n, wall = time_gpu(w, args.steps, args.warmup, use_graph=not args.no_graph)
+        ms, n, wall = time_gpu(w, args.steps, args.warmup, use_graph=True if args.graph else None)
         gbs = w.bytes_per_step / (ms * 1e-3) / 1e9
         r = {"config": cls.cfg, "workload": w.name, "kernel": w.kernel, "ms_per_step": round(ms, 5),
              "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
@@ -1271,7 +1317,7 @@ def main():
             # the same chain with MFH_FUSION_PRECISE (the reference's f64
             # transcendentals, bit-identical to it) on the same sets
             w.compile(M.FUSION_PRECISE)
-            pms, _, _ = time_gpu(w, args.steps, args.warmup, use_graph=not args.no_graph)
+            pms, _, _ = time_gpu(w, args.steps, args.warmup, use_graph=True if args.graph else None)
             pgbs = w.bytes_per_step / (pms * 1e-3) / 1e9
             r["precise"] = {"ms_per_step": round(pms, 5), "GB_s": round(pgbs, 1),
                             "frac_of_peak": round(pgbs / PEAK_GBS, 4), "sample_check": w.check()}
@@ -1308,11 +1354,11 @@ def main():
         "config": {"workload": "BASELINE config 2: fp8_e4m3 -> bf16 dequant [4096,14336], scale 0.0125",
                    "elements": Fp8.n, "algorithmic_bytes_per_step": Fp8.bytes_per_step,
                    "rotated_sets": head["rotated_sets"],
-                   "timing": ("HIP events on the launch stream around one replay of a graph of K launches over "
-                              "rotated buffer sets (>= 1 GiB of distinct inputs per rotation), after ceil(W/K) "
-                              "untimed replays of the same graph and a synchronize; a bounded GPU spin queued "
-                              "ahead of the start event keeps the host's graph launch latency out of the "
-                              "timed region")},
+                   "timing": ("HIP events on the launch stream around K back-to-back launches over rotated "
+                              "buffer sets (>= 1 GiB of distinct inputs per rotation), all queued behind a bounded "
+                              "GPU spin before the start event fires: eager launches for K <= 64 (checked by the "
+                              "host), one HIP graph replay above; after one launch per set, ceil(W/K)*K untimed "
+                              "warm-up launches and a synchronize")},
         "roofline": {"bound": "hbm", "achieved": head["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": load_traffic(), "kernel": head["kernel"]},
         "torch_same_mix": head.get("torch_same_mix"),
