@@ -179,7 +179,7 @@ struct Emitter {
     const std::vector<int>& c1;
     Form form;
     // Silu and Gelu in their f64 forms (mfh_*_fast_x): chains that stream f32.
-    bool exact_tail = false;
+    bool f64_forms = false;
     const std::vector<Guard>* guards = nullptr;  // kFast only
     std::string prefix = "t";
     // Vector loop only: inputs held as packed f16 words w<k>[u][j >> 1]
@@ -206,7 +206,7 @@ struct Emitter {
         if (form == Form::kPrecise) return let(fn + "_ref(" + a + ")");
         if (form == Form::kFallback) return let(fn + "_rare(" + a + ")");
         flagged = true;
-        const bool x = exact_tail && std::string(name) != "sigmoid";  // sigmoid's fast form is f64 already
+        const bool x = f64_forms && std::string(name) != "sigmoid";  // sigmoid's fast form is f64 already
         return let(fn + (x ? "_fast_x(" : "_fast(") + a + ", qe)");
     }
 
@@ -594,10 +594,10 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // show every f32 ulp of the node, and their 4-byte elements leave room
     // for about twice the instructions (MFH_FUSION_SHORT_QUOTIENT keeps the
     // 16-bit chains' forms).
-    const bool exact_tail = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
+    const bool f64_forms = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
     bool f64_fast = false;
     for (const mfh_ast_node& node : list)
-        if (!precise && (node.type == kNodeSigmoid || (exact_tail && (node.type == kNodeSilu || node.type == kNodeGelu))))
+        if (!precise && (node.type == kNodeSigmoid || (f64_forms && (node.type == kNodeSilu || node.type == kNodeGelu))))
             f64_fast = true;
     const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : f64_fast ? 2 : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
@@ -620,13 +620,13 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     std::vector<bool> packed16(n_inputs, false);
     for (int k = 0; k < n_inputs; k++)
         packed16[k] = inputs[k].mode != MFH_OPERAND_SCALAR && inputs[k].dtype == kFloat16;
-    Emitter em{list, c0, c1, main_form, exact_tail, &guards};
+    Emitter em{list, c0, c1, main_form, f64_forms, &guards};
     const std::string result = em.emit(0);
-    Emitter emf{list, c0, c1, Form::kFallback, exact_tail, nullptr, "f"};
+    Emitter emf{list, c0, c1, Form::kFallback, f64_forms, nullptr, "f"};
     const std::string fresult = em.flagged ? emf.emit(0) : "";
-    Emitter emv{list, c0, c1, main_form, exact_tail, &guards, "t", packed16};
+    Emitter emv{list, c0, c1, main_form, f64_forms, &guards, "t", packed16};
     const std::string vresult = emv.emit(0);
-    Emitter emvf{list, c0, c1, Form::kFallback, exact_tail, nullptr, "f", packed16};
+    Emitter emvf{list, c0, c1, Form::kFallback, f64_forms, nullptr, "f", packed16};
     const std::string vfresult = emv.flagged ? emvf.emit(0) : "";
 
     std::string identifier = output_port && *output_port ? output_port : "anon";
