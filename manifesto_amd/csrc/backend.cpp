@@ -726,11 +726,12 @@ int mfh_tensor_close(mfh_tensor* t)
         // caller's own launches, on any stream: only a device-wide wait (the
         // one hipFree would make) orders after those.  The idle block then
         // goes to the backend's cache.
-        int frc = st.exposed.load(std::memory_order_relaxed) ? check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize")
-                                                             : MFH_OK;
-        frc = frc == MFH_OK && rc == MFH_OK ? t->backend->release(st.ptr, st.bytes)
-                                            : check_hip(hipFree(st.ptr), "hipFree");
-        if (rc == MFH_OK) rc = frc;
+        const int wrc = st.exposed.load(std::memory_order_relaxed)
+                            ? check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize")
+                            : MFH_OK;
+        const int frc = wrc == MFH_OK && rc == MFH_OK ? t->backend->release(st.ptr, st.bytes)
+                                                      : check_hip(hipFree(st.ptr), "hipFree");
+        if (rc == MFH_OK) rc = wrc != MFH_OK ? wrc : frc;
     }
     st.ptr = nullptr;
     st.freed = true;
