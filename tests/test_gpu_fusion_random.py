@@ -1,0 +1,183 @@
+"""GPU parity of generated fused kernels on random chains, against the CPU
+evaluator (CPUKernel.Run, codegen/cpu.go:59-214).
+
+Each seed draws a random FusionAST over every node type, 1-3 inputs in
+f32/bf16/f16 storage as full, periodic (a repeating row) or scalar operands,
+an element count that exercises the vector loop, its scalar tail or the
+element loop alone, and buffers that may be misaligned by one element.  Two
+classes of chain, each with a property that holds for every element:
+
+1. Default flags (the fast Sigmoid/Silu/Gelu forms and the cancellation
+   guard), 16-bit outputs, chains in which every Sigmoid/Silu/Gelu reaches
+   the output through at most one Add/Sub and no transcendental node, and
+   has none below it.  There a fast node is within 2 f32 ulps of the
+   reference's and every other operation is exact in both evaluations, and
+   where the one Add/Sub cancels the guard recomputes the element with the
+   reference forms.  So every result is within one storage ulp of the
+   reference's, NaN where the reference's is NaN.
+2. MFH_FUSION_PRECISE (the reference's f64 forms, rounded once), any chain,
+   any output dtype: bit-identical to the reference, NaN where it is NaN.
+   The device's f64 exp/log/tanh and the oracle's libm may round the last
+   f64 bit differently; that changes the f32 result in about 2^-29 of
+   evaluations, so up to 1e-4 of a chain's elements may differ.
+
+Exp/Log/Tanh run the reference's f64 form in every mode.  Gelu's input goes
+through Max(., -4.5): below -4.9 the reference's 1 + tanh(inner) cancels in
+f64 and its result is a multiple of 2^-53 |v|/2, which two correct f64
+evaluations may place one multiple apart (the single-node tests cover that
+region).  NaN and |v| > 1024 still reach the fast form's rare path there.
+"""
+import numpy as np
+import pytest
+
+import manifesto_amd as M
+import oracle as O
+
+from gpu_util import compare_storage, empty_dev, log, nan_mask, stream, to_dev, to_host
+
+SIZE = {O.FLOAT32: 4, O.BFLOAT16: 2, O.FLOAT16: 2}
+NP = {O.FLOAT32: np.float32, O.BFLOAT16: np.uint16, O.FLOAT16: np.uint16}
+DTYPES = [O.FLOAT32, O.BFLOAT16, O.FLOAT16]
+ACTIVATIONS = [O.N_SIGMOID, O.N_SILU, O.N_GELU]
+TRANSCENDENTAL = [O.N_EXP, O.N_LOG, O.N_TANH]
+EXACT_UNARY = [O.N_NEG, O.N_ABS, O.N_SQRT, O.N_RELU, O.N_LEAKY_RELU]
+BINARY = [O.N_ADD, O.N_SUB, O.N_MUL, O.N_DIV, O.N_MAX, O.N_MIN]
+NAMES = {v: k[2:].lower() for k, v in vars(O).items() if k.startswith("N_") and isinstance(v, int)}
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    M.init(0)
+
+
+def random_tree(rng, depth, n_in, adds, above, act_adds):
+    """A random subtree.  `adds`: Add/Sub nodes between here and the root;
+    `above`: a transcendental node lies between here and the root; an
+    activation may be placed only where adds <= act_adds and not above
+    (act_adds < 0: anywhere)."""
+    if depth == 0 or rng.random() < 0.2:
+        if rng.random() < 0.15:
+            return ("const", float(np.float32(rng.normal(0, 2))))
+        return ("in", int(rng.integers(n_in)))
+    r = rng.random()
+    free = act_adds < 0
+    if r < 0.3 and (free or (not above and adds <= act_adds)):
+        act = ACTIVATIONS[int(rng.integers(3))]
+        child = random_tree(rng, depth - 1, n_in, adds, True, act_adds)
+        if act == O.N_GELU:
+            child = (O.N_MAX, child, ("const", -4.5))
+        return (act, child)
+    if r < 0.42:
+        return (TRANSCENDENTAL[int(rng.integers(3))], random_tree(rng, depth - 1, n_in, adds, True, act_adds))
+    if r < 0.6:
+        return (EXACT_UNARY[int(rng.integers(len(EXACT_UNARY)))],
+                random_tree(rng, depth - 1, n_in, adds, above, act_adds))
+    op = BINARY[int(rng.integers(len(BINARY)))]
+    a = adds + (op in (O.N_ADD, O.N_SUB))
+    return (op, random_tree(rng, depth - 1, n_in, a, above, act_adds),
+            random_tree(rng, depth - 1, n_in, a, above, act_adds))
+
+
+def describe(t):
+    if t[0] == "in":
+        return f"x{t[1]}"
+    if t[0] == "const":
+        return repr(t[1])
+    return f"{NAMES[t[0]]}(" + ", ".join(describe(c) for c in t[1:]) + ")"
+
+
+def random_values(rng, n):
+    """Mostly N(0, 2); some large, tiny and special values."""
+    v = rng.normal(0, 2, n).astype(np.float32)
+    pick = rng.random(n)
+    v = np.where(pick < 0.04, rng.uniform(-3000, 3000, n).astype(np.float32), v)
+    v = np.where((pick >= 0.04) & (pick < 0.06), (rng.normal(0, 1, n) * 1e-6).astype(np.float32), v)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, -1.0], dtype=np.float32)
+    v = np.where((pick >= 0.06) & (pick < 0.07), special[rng.integers(len(special), size=n)], v)
+    return v.astype(np.float32)
+
+
+def random_case(seed, act_adds, out_dtypes):
+    rng = np.random.default_rng(seed)
+    n_in = int(rng.integers(1, 4))
+    tree = random_tree(rng, int(rng.integers(2, 6)), n_in, 0, False, act_adds)
+    shape = int(rng.integers(3))
+    count = [8 * int(rng.integers(1000, 6000)), 8 * int(rng.integers(1000, 6000)) + int(rng.integers(1, 8)),
+             int(rng.integers(1, 40))][shape]
+    pad = int(rng.integers(2)) if rng.random() < 0.3 else 0
+    operands, arrays, values, periods = [], [], [], []
+    for k in range(n_in):
+        dt = DTYPES[int(rng.integers(3))]
+        mode = int(rng.choice(3, p=[0.6, 0.25, 0.15])) if k else 0  # input 0 full: it sets the output's offset
+        length = count if mode == M.OPERAND_FULL else 1 if mode == M.OPERAND_SCALAR else \
+            [8, 24, 4096, 12, 7][int(rng.integers(5))]
+        stored = O.encode(random_values(rng, length), dt)
+        operands.append((dt, mode, length if mode == M.OPERAND_PERIODIC else 0))
+        arrays.append(stored)
+        values.append(O.decode(stored, dt))
+        periods.append(0 if mode == M.OPERAND_FULL else length)
+    out_dt = out_dtypes[int(rng.integers(len(out_dtypes)))]
+    return tree, operands, arrays, values, periods, count, pad, out_dt
+
+
+def run_case(tree, operands, arrays, values, periods, count, pad, out_dt, flags, seed):
+    nodes = O.flatten(tree)
+    log(f"seed {seed} flags {flags}: {describe(tree)} over {[(o[0], o[1], o[2]) for o in operands]}, "
+        f"count {count} pad {pad} -> {out_dt}")
+    k = M.FusedKernel(nodes, operands, out_dt, f"r{seed}", flags)
+    try:
+        # only full operands take the padding: periodic and scalar ones are read by index
+        devs = [to_dev(a, pad=(pad if o[1] == M.OPERAND_FULL else 0) * a.itemsize) for a, o in zip(arrays, operands)]
+        out_pad = pad * SIZE[out_dt]
+        out, op = empty_dev(count * SIZE[out_dt], pad=out_pad)
+        k.launch([p for _, p in devs], op, count, stream())
+        got = to_host(out, NP[out_dt], pad=out_pad)
+    finally:
+        k.close()
+    want = O.encode(O.run(nodes, values, count, periods), out_dt)
+    return got, want
+
+
+def test_the_generator_keeps_class_one_chains_in_their_class():
+    # Every activation of a class-1 chain has at most one Add/Sub and no
+    # transcendental node on its way to the root, and none below it.
+    def walk(t, adds, above):
+        if t[0] in ("in", "const"):
+            return
+        if t[0] in ACTIVATIONS:
+            assert adds <= 1 and not above, t
+        below = above or t[0] in ACTIVATIONS or t[0] in TRANSCENDENTAL
+        for c in t[1:]:
+            walk(c, adds + (t[0] in (O.N_ADD, O.N_SUB)), below)
+
+    seen = 0
+    for seed in range(2000):
+        tree = random_case(seed, 1, [O.FLOAT16])[0]
+        walk(tree, 0, False)
+        seen += describe(tree).count("gelu") + describe(tree).count("silu") + describe(tree).count("sigmoid")
+    assert seen > 500
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(100, 132))
+def test_fast_forms_within_one_storage_ulp(gpu, seed):
+    case = random_case(seed, 1, [O.FLOAT16, O.BFLOAT16])
+    got, want = run_case(*case, 0, seed)
+    worst = compare_storage(got, want, case[-1], 1, f"seed {seed}")
+    log(f"seed {seed}: max {worst} storage ulp, {np.mean(got.view(np.uint16) == want.view(np.uint16)):.5f} "
+        f"bit-identical")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(200, 232))
+def test_precise_forms_match_the_reference(gpu, seed):
+    case = random_case(seed, -1, DTYPES)
+    out_dt = case[-1]
+    got, want = run_case(*case, M.FUSION_PRECISE, seed)
+    bits = np.uint32 if out_dt == O.FLOAT32 else np.uint16
+    gb, wb = got.view(bits), want.view(bits)
+    gn, wn = nan_mask(gb, out_dt), nan_mask(wb, out_dt)
+    differ = np.flatnonzero((gb != wb) & ~(gn & wn))
+    log(f"seed {seed}: {differ.size} of {gb.size} differ")
+    assert differ.size <= max(2, gb.size // 10000), \
+        f"seed {seed}: {differ.size} differ, first at {differ[:3]}: got {gb[differ[:3]]} want {wb[differ[:3]]}"
