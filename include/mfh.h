@@ -95,8 +95,8 @@ int mfh_set_launch_config(const char* kernel, int32_t blocks_per_cu, int32_t ite
 int mfh_get_launch_config(const char* kernel, int32_t* blocks_per_cu, int32_t* items_per_thread);
 
 /* Threads per workgroup of a kernel family, the third part of its launch
- * shape.  "fp8", "int4", "axpy", "axpy16" and "convert" run 64, 128 or 256
- * (defaults 128, 256, 64 and 64; "convert" picks per cast: 64 unless the
+ * shape.  "fp8", "axpy", "axpy16" and "convert" run 64, 128 or 256, "int4"
+ * also 512 (defaults 128, 64, 64 and 512; "convert" picks per cast: 64 unless the
  * output is four times the source, then 256; its element-by-element
  * fallbacks for misaligned buffers keep 256); "fused" takes any
  * power of two from 64 to 1024 and applies it to kernels compiled afterwards

@@ -1068,7 +1068,7 @@ struct Int4Launch {
         int64_t items = vec_ok ? std::max<int64_t>(n / elems, 1) : n;
         const int u = items_per_thread(Kern::kInt4);
         const mfh_u8* p = static_cast<const mfh_u8*>(packed);
-        return with_block(threads_per_block(Kern::kInt4), [&](auto block) {
+        return with_block_to_512(threads_per_block(Kern::kInt4), [&](auto block) {
             constexpr int BS = decltype(block)::value;
             const unsigned grid = grid_for(items, dev, Kern::kInt4, u, BS);
             if (u == 4) launch<4, BS>(grid, p, scales, scale_dt, out, n, group, shift, vec_ok, stream);

@@ -49,6 +49,15 @@ int with_block(int threads, F&& f)
     }
 }
 
+// with_block, plus 512-thread workgroups for the one family that runs them
+// (the Int4 dequant).
+template <typename F>
+int with_block_to_512(int threads, F&& f)
+{
+    if (threads == 512) return f(std::integral_constant<int, 512>{});
+    return with_block(threads, std::forward<F>(f));
+}
+
 int launch_status(const char* what);
 
 // Streaming 16-byte stores of a chunk: buffer stores with the non-temporal

@@ -193,15 +193,18 @@ constexpr int kMaxBlocksPerCu = 1 << 16;
 // every family runs one-shot, FP8 and Int4 with two items per thread, axpy
 // and the casts with one.  Workgroup sizes (BASELINE sizes, graph-timed
 // bench, against 256 threads): FP8 128 (+0.4%; 64 is slower), axpy 64
-// (+2.3%; 128 is slower), Int4 256 (128 and 64 lose 2-3%).  0 for the fused
+// (+2.3%; 128 is slower), Int4 512 (+0.5% in the bench's paired runs, +1.3%
+// with eager launches at 1x and 4x the BASELINE size; 128 and 64 lose 2-3%,
+// 1024 loses 3-10%).  0 for the fused
 // family means "per kernel": each generated kernel carries its shape (see
 // fusion.cpp), one-wave workgroups unless set; for the casts "per cast"
 // (cast_threads in dequant.hip).
 constexpr unsigned kSizes64To256 = (1u << 6) | (1u << 7) | (1u << 8);
-constexpr unsigned kSizes64To1024 = kSizes64To256 | (1u << 9) | (1u << 10);
+constexpr unsigned kSizes64To512 = kSizes64To256 | (1u << 9);
+constexpr unsigned kSizes64To1024 = kSizes64To512 | (1u << 10);
 LaunchCfg g_cfg[(int)Kern::kCount] = {
     {"fp8", {kMaxBlocksPerCu}, {2}, {128}, kSizes64To256},
-    {"int4", {kMaxBlocksPerCu}, {2}, {256}, kSizes64To256},
+    {"int4", {kMaxBlocksPerCu}, {2}, {512}, kSizes64To512},
     {"axpy", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
     {"axpy16", {kMaxBlocksPerCu}, {1}, {64}, kSizes64To256},
     {"convert", {kMaxBlocksPerCu}, {0}, {0}, kSizes64To256},  // 0: per cast

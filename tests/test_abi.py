@@ -276,7 +276,7 @@ def test_launch_config_set_keep_and_restore():
 
 def test_launch_threads_set_keep_restore_and_limits():
     # defaults: the measured workgroup size of each family
-    assert [M.get_launch_threads(f) for f in ("fp8", "int4", "axpy", "axpy16", "convert")] == [128, 256, 64, 64, 0]
+    assert [M.get_launch_threads(f) for f in ("fp8", "int4", "axpy", "axpy16", "convert")] == [128, 512, 64, 64, 0]
     assert M.get_launch_threads("fused") == 0  # each generated kernel's default
     k = M.FusedKernel(swiglu_nodes(), [(M.BFLOAT16, M.OPERAND_FULL, 0)] * 2, M.BFLOAT16, "threads_default")
     assert "__launch_bounds__(64)" in k.source and "gridDim.x * 64;" in k.source
@@ -300,8 +300,10 @@ def test_launch_threads_set_keep_restore_and_limits():
             assert M.get_launch_threads("fp8") == t
         with pytest.raises(M.MFHError, match="workgroups of 64, 128, 256 threads, not 512"):
             M.set_launch_threads("axpy", 512)
-        with pytest.raises(M.MFHError, match="workgroups of 64, 128, 256 threads, not 1024"):
+        with pytest.raises(M.MFHError, match="workgroups of 64, 128, 256, 512 threads, not 1024"):
             M.set_launch_threads("int4", 1024)
+        M.set_launch_threads("int4", 512)
+        assert M.get_launch_threads("int4") == 512
         M.set_launch_threads("int4", 128)
         assert M.get_launch_threads("int4") == 128
     finally:

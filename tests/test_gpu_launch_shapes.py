@@ -3,7 +3,7 @@ bits under small capped grids (one workgroup per CU, so each workgroup walks
 many chunks, with 1, 2 and 4 items per thread) as under its default one-shot
 grid, at sizes with ragged tails and on unaligned buffers, at every
 workgroup size the family runs (FP8, axpy and the casts 64, 128 and 256
-threads; generated kernels also 1024).  The default shape
+threads; Int4 also 512; generated kernels also 1024).  The default shape
 itself is pinned against the oracle here and in the per-family test files."""
 import numpy as np
 import pytest
@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 1), (1, 2), (1, 4), (3, 2), (-1, -1)]  # (workgroups per CU, items per thread); -1: default
 # workgroup sizes each ahead-of-time family runs besides its default
-THREADS = {"fp8": (64, 128, 256), "int4": (64, 128, 256), "axpy": (64, 128, 256), "axpy16": (64, 128, 256),
+THREADS = {"fp8": (64, 128, 256), "int4": (64, 128, 256, 512), "axpy": (64, 128, 256), "axpy16": (64, 128, 256),
            "convert": (64, 128, 256)}
 
 
