@@ -851,47 +851,54 @@ def graph_calls_run(torch, M):
     """--graph-calls: mfh_graph_call (runtime.Backend.CallGraph) on a graph
     of 4 independent chains of 8 unfused f32 nodes, per call, at 16 K, 256 K
     and 4 M elements, with MaxStreams 1 and 4, each plain and replayed from a
-    captured HIP graph.  Device time per call from 200 back-to-back calls
-    between a synchronize on each side; host time = until the call returns."""
+    captured HIP graph, and each on the same buffers every call or on four
+    buffer sets in turn (a replay then rebinds its graph's launches every
+    call).  Device time per call from 200 back-to-back calls between a
+    synchronize on each side; host time = until the call returns."""
     from manifesto_amd.graph import Graph, GraphNode
     from manifesto_amd import plan as P
     ops = ["math.neg", "math.abs", "math.add", "math.mul", "activation.relu", "math.sub", "math.max", "math.neg"]
     stream = torch.cuda.current_stream().cuda_stream
     for n in (16 << 10, 256 << 10, 4 << 20):
-        x = torch.randn(n, device="cuda")
-        y = torch.randn(n, device="cuda")
-        outs = {f"o{c}": torch.empty(n, device="cuda") for c in range(4)}
+        sets = []
+        for _ in range(4):
+            sets.append(({"x": torch.randn(n, device="cuda"), "y": torch.randn(n, device="cuda")},
+                         {f"o{c}": torch.empty(n, device="cuda") for c in range(4)}))
         for streams in (1, 4):
             for replay in (False, True):
-                nodes, outputs = [], {}
-                for c in range(4):
-                    prev = "x" if c % 2 == 0 else "y"
-                    for k, op in enumerate(ops):
-                        binary = op in ("math.add", "math.mul", "math.sub", "math.max")
-                        node = f"c{c}n{k}"
-                        nodes.append(GraphNode(node, op, [prev, "y" if c % 2 == 0 else "x"] if binary else [prev]))
-                        prev = node
-                    outputs[f"o{c}"] = prev
-                g = Graph(inputs=["x", "y"], outputs=outputs, execution_dtype=M.FLOAT32, nodes=nodes)
-                P.set_max_streams(g, streams)
-                g.set_replay(replay)
-                for _ in range(3):
-                    g.call({"x": x, "y": y}, outs, stream)
-                torch.cuda.synchronize()
-                reps = 200
-                host = 0.0
-                t0 = time.perf_counter()
-                for _ in range(reps):
-                    h0 = time.perf_counter()
-                    g.call({"x": x, "y": y}, outs, stream)
-                    host += time.perf_counter() - h0
-                torch.cuda.synchronize()
-                wall = (time.perf_counter() - t0) / reps
-                print(json.dumps({"elements": n, "max_streams": streams, "replay": replay,
-                                  "us_per_call": round(wall * 1e6, 1), "host_us_per_call": round(host / reps * 1e6, 1),
-                                  "replayed_calls": g.replayed_calls(), "streams_used": P.streams_used(g)}),
-                      flush=True)
-                del g
+                for buffers in ("same", "rotating"):
+                    nodes, outputs = [], {}
+                    for c in range(4):
+                        prev = "x" if c % 2 == 0 else "y"
+                        for k, op in enumerate(ops):
+                            binary = op in ("math.add", "math.mul", "math.sub", "math.max")
+                            node = f"c{c}n{k}"
+                            nodes.append(GraphNode(node, op, [prev, "y" if c % 2 == 0 else "x"] if binary else [prev]))
+                            prev = node
+                        outputs[f"o{c}"] = prev
+                    g = Graph(inputs=["x", "y"], outputs=outputs, execution_dtype=M.FLOAT32, nodes=nodes)
+                    P.set_max_streams(g, streams)
+                    g.set_replay(replay)
+                    pick = (lambda i: sets[0]) if buffers == "same" else (lambda i: sets[i % 4])
+                    for i in range(3):
+                        g.call(*pick(i), stream)
+                    torch.cuda.synchronize()
+                    reps = 200
+                    host = 0.0
+                    t0 = time.perf_counter()
+                    for i in range(reps):
+                        ins, outs = pick(i)
+                        h0 = time.perf_counter()
+                        g.call(ins, outs, stream)
+                        host += time.perf_counter() - h0
+                    torch.cuda.synchronize()
+                    wall = (time.perf_counter() - t0) / reps
+                    print(json.dumps({"elements": n, "max_streams": streams, "replay": replay, "buffers": buffers,
+                                      "us_per_call": round(wall * 1e6, 1),
+                                      "host_us_per_call": round(host / reps * 1e6, 1),
+                                      "replayed_calls": g.replayed_calls(), "streams_used": P.streams_used(g)}),
+                          flush=True)
+                    del g
 
 
 class Row(Workload):

@@ -224,14 +224,20 @@ int mfh_graph_call_noalloc(mfh_graph* graph, const mfh_value* inputs, int32_t n_
                            int32_t n_outputs, void* stream);
 
 /* Launch replay (no counterpart in the reference, whose CallGraph dispatches
- * node by node): a call identical to an earlier one (same value names,
- * pointers, dtypes and counts, same workspace and stream budget) is captured
- * as a HIP graph on its second occurrence and replayed with one
- * hipGraphLaunch from then on; the first occurrence runs as plain launches.
- * Up to 8 distinct calls are kept per graph (least recently used dropped).
- * Any change to the graph drops them.  A call made on a stream that is
- * itself being captured runs as plain launches into that capture.  Enabled
- * by default; mfh_graph_set_replay(graph, 0) turns it off.
+ * node by node): calls with the same plan (value names, dtypes, counts,
+ * which output bindings share a buffer or overlap an input, stream budget)
+ * share one HIP graph.  The plan's first call runs as plain launches, its
+ * second is captured, and every later call launches the captured graph with
+ * one hipGraphLaunch, whatever its buffers: the launches and output copies
+ * whose buffers differ from the ones the graph was last bound to get their
+ * arguments updated in place first.  Two executables per plan take turns,
+ * so that one still running is never updated (a call may wait for the call
+ * before last).  A plan that runs on several streams is not rebound: its
+ * calls replay only on buffers an executable already holds and otherwise run
+ * as plain launches.  Up to 8 plans are kept per graph (least recently used
+ * dropped); any change to the graph drops them.  A call made on a stream
+ * that is itself being captured runs as plain launches into that capture.
+ * Enabled by default; mfh_graph_set_replay(graph, 0) turns it off.
  * mfh_graph_replayed_calls counts the calls that ran as replays. */
 int mfh_graph_set_replay(mfh_graph* graph, int32_t enabled);
 int64_t mfh_graph_replayed_calls(const mfh_graph* graph);

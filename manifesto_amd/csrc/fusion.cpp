@@ -732,9 +732,20 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     return MFH_OK;
 }
 
-int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
-            hipStream_t stream, bool may_load)
+void HipLaunch::bind()
 {
+    args.clear();
+    args.reserve(ptrs.size() + 3);
+    for (const void*& p : ptrs) args.push_back(&p);
+    args.push_back(&out);
+    args.push_back(&count);
+    args.push_back(&nvec);
+}
+
+int prepare_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
+                bool may_load, HipLaunch* launch)
+{
+    launch->grid = 0;
     if (!kernel) return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: kernel is empty");
     if (n_inputs != (int)kernel->inputs.size())
         return fail(MFH_ERR_INVALID_ARGUMENT, "codegen hip: kernel \"%s\" expects %d inputs, got %d",
@@ -756,22 +767,29 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
         if (kernel->inputs[k].mode != MFH_OPERAND_SCALAR && !item_aligned(inputs[k], kernel->inputs[k].dtype))
             vec_ok = false;
     }
-    hipFunction_t fn;
-    MFH_TRY(load_function(*kernel->code, dev->ordinal, may_load, &fn));
-    int64_t nvec = vec_ok ? count / kernel->vec : 0;
+    MFH_TRY(load_function(*kernel->code, dev->ordinal, may_load, &launch->fn));
+    const int64_t nvec = vec_ok ? count / kernel->vec : 0;
     int64_t items = nvec > 0 ? (nvec + kernel->unroll - 1) / kernel->unroll : count;
     int64_t need = (items + kernel->block - 1) / kernel->block;
     int bpc = blocks_per_cu(Kern::kFused) > 0 ? blocks_per_cu(Kern::kFused) : kernel->auto_bpc;
     int64_t cap = std::min<int64_t>((int64_t)dev->compute_units * bpc, (int64_t(1) << 32) / kernel->block - 1);
-    unsigned grid = (unsigned)std::max<int64_t>(1, std::min(need, cap));
-    std::vector<const void*> ptrs(inputs, inputs + n_inputs);
-    std::vector<void*> args;
-    args.reserve(n_inputs + 3);
-    for (int k = 0; k < n_inputs; k++) args.push_back(&ptrs[k]);
-    args.push_back(&out);
-    args.push_back(&count);
-    args.push_back(&nvec);
-    return check_hip(hipModuleLaunchKernel(fn, grid, 1, 1, kernel->block, 1, 1, 0, stream, args.data(), nullptr),
+    launch->grid = (unsigned)std::max<int64_t>(1, std::min(need, cap));
+    launch->block = (unsigned)kernel->block;
+    launch->ptrs.assign(inputs, inputs + n_inputs);
+    launch->out = out;
+    launch->count = count;
+    launch->nvec = nvec;
+    return MFH_OK;
+}
+
+int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
+            hipStream_t stream, bool may_load)
+{
+    HipLaunch l;
+    MFH_TRY(prepare_hip(kernel, inputs, n_inputs, out, count, may_load, &l));
+    if (l.grid == 0) return MFH_OK;
+    l.bind();
+    return check_hip(hipModuleLaunchKernel(l.fn, l.grid, 1, 1, l.block, 1, 1, 0, stream, l.args.data(), nullptr),
                      "hipModuleLaunchKernel");
 }
 

@@ -4,6 +4,7 @@
 #define MFH_FUSION_HPP
 
 #include <cstdint>
+#include <vector>
 
 #include "common.hpp"
 
@@ -30,6 +31,25 @@ int run_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, v
 // Changes whenever a loaded kernel module is unloaded (shutdown, device
 // change); function handles taken before a change may be dangling.
 uint64_t module_generation();
+
+// The launch run_hip makes: function, grid and argument values.  grid 0 means
+// nothing to launch (count 0).
+struct HipLaunch {
+    hipFunction_t fn = nullptr;
+    unsigned grid = 0;
+    unsigned block = 0;
+    std::vector<const void*> ptrs;  // the inputs
+    void* out = nullptr;
+    int64_t count = 0;
+    int64_t nvec = 0;
+    std::vector<void*> args;  // kernel argument addresses, set by bind()
+    // Points `args` at the fields above; call it where the object stays
+    // until the launch (or node update) has read them.
+    void bind();
+};
+// run_hip's checks and launch shape for these buffers, without the launch.
+int prepare_hip(const mfh_kernel* kernel, const void* const* inputs, int n_inputs, void* out, int64_t count,
+                bool may_load, HipLaunch* launch);
 
 }  // namespace mfh
 

@@ -193,15 +193,6 @@ struct GraphNode {
     std::shared_ptr<HIPKernel> solo;     // one-node kernel of an unfused elementwise node
 };
 
-// One call seen before: its key and, once captured, its executable graph.
-struct Replay {
-    std::string key;
-    hipGraphExec_t exec = nullptr;
-    int streams = 1;
-    uint64_t tick = 0;
-};
-constexpr int kMaxReplays = 8;
-
 // A call's launches, placement and streams for one signature of bindings
 // (defined with the execution code below).
 struct PlannedCall;
@@ -229,16 +220,20 @@ struct mfh_graph {
     std::vector<hipEvent_t> events;
     std::vector<hipEvent_t> joins;  // per aux stream, back into the caller's
     hipEvent_t fork = nullptr;
-    hipEvent_t done = nullptr;  // recorded after a call's last work
+    // Recorded after a call's last work: call n records done_ring[n % 4], and
+    // `done` is the latest of them, so a call's end can still be waited for a
+    // few calls later.
+    static constexpr int kDoneRing = 4;
+    hipEvent_t done_ring[kDoneRing] = {};
+    hipEvent_t done = nullptr;
+    uint64_t call_seq = 0;  // calls recorded so far
     hipStream_t last_stream = nullptr;
     bool called = false;
-    // calls replayed as HIP graphs, keyed by everything their launches
-    // depend on; cleared by any change to the graph
+    // calls replayed as HIP graphs, one per plan (below); cleared by any
+    // change to the graph
     bool replay = true;
     bool replay_broken = false;
-    std::vector<mfh::Replay> replays;
-    uint64_t replay_clock = 0;
-    uint64_t replay_generation = 0;
+    uint64_t replay_generation = 0;  // module generation of the captured calls
     int64_t replayed = 0;
     hipStream_t capture = nullptr;
     // calls planned before, keyed by their bindings without the pointers;
@@ -882,15 +877,33 @@ int graph_streams(Graph& g, int n_streams, int n_events)
         g.events.push_back(e);
     }
     if (!g.fork) MFH_TRY(check_hip(hipEventCreateWithFlags(&g.fork, hipEventDisableTiming), "hipEventCreateWithFlags"));
-    if (!g.done) MFH_TRY(check_hip(hipEventCreateWithFlags(&g.done, hipEventDisableTiming), "hipEventCreateWithFlags"));
+    for (hipEvent_t& e : g.done_ring)
+        if (!e) MFH_TRY(check_hip(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreateWithFlags"));
     return MFH_OK;
+}
+
+// The node that the last launch on a capturing stream added to the capture
+// (nullptr if the stream is not capturing or has no single last node).
+hipGraphNode_t captured_node(hipStream_t s)
+{
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    hipGraph_t graph = nullptr;
+    const hipGraphNode_t* deps = nullptr;
+    size_t n = 0;
+    if (hipStreamGetCaptureInfo_v2(s, &status, &id, &graph, &deps, &n) != hipSuccess ||
+        status != hipStreamCaptureStatusActive || n != 1 || !deps)
+        return nullptr;
+    return deps[0];
 }
 
 // The launches of one call on `ls` and the graph's other streams: fork from
 // `ls`, every node with its waits and signals, join back into `ls`, then the
-// output copies.  With `ls` capturing, this records the call as a graph.
+// output copies.  With `ls` capturing, this records the call as a graph, and
+// `nodes` (if given) receives each step's node and then each copy's, nullptr
+// where nothing was launched or copied.
 int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipStream_t ls, void* workspace,
-               bool may_load = true)
+               bool may_load = true, std::vector<hipGraphNode_t>* nodes = nullptr)
 {
     std::vector<Slot>& slots = P.slots;
     if (n_streams > 1) {
@@ -921,6 +934,7 @@ int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipSt
         ptrs.clear();
         for (int o : st.operands) ptrs.push_back(addr(slots[o]));
         MFH_TRY(run_hip(k, ptrs.data(), (int)ptrs.size(), addr(slots[st.result]), st.count, s, may_load));
+        if (nodes) nodes->push_back(st.count > 0 ? captured_node(s) : nullptr);
         for (const mfh_sync_event& e : pn.barriers)
             if (!e.wait) MFH_TRY(check_hip(hipEventRecord(g.events[e.event_id], s), "hipEventRecord(barrier)"));
     }
@@ -934,6 +948,7 @@ int launch_all(Graph& g, Prepared& P, const Topology& topo, int n_streams, hipSt
         if (bytes)
             MFH_TRY(check_hip(hipMemcpyAsync(c.to->data, addr(s), bytes, hipMemcpyDeviceToDevice, ls),
                               "hipMemcpyAsync(graph output)"));
+        if (nodes) nodes->push_back(bytes ? captured_node(ls) : nullptr);
     }
     return MFH_OK;
 }
@@ -965,25 +980,6 @@ int64_t lay_out(Prepared& P, const Topology& topo)
     return const_bytes + arena;
 }
 
-// Everything a call's launches depend on: value names, pointers, dtypes and
-// counts, the workspace, the stream budget.
-std::string call_key(const Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_value* outputs,
-                     int32_t n_outputs)
-{
-    std::string key;
-    char buf[96];
-    auto add = [&](const mfh_value& v) {
-        key += v.name ? v.name : "";
-        snprintf(buf, sizeof buf, "|%p|%u|%lld;", v.data, (unsigned)v.dtype, (long long)v.count);
-        key += buf;
-    };
-    for (int32_t i = 0; i < n_inputs; i++) add(inputs[i]);
-    key += "->";
-    for (int32_t i = 0; i < n_outputs; i++) add(outputs[i]);
-    snprintf(buf, sizeof buf, "ws=%p/%lld;s=%d", g.ws, (long long)g.ws_bytes, (int)g.max_streams);
-    return key + buf;
-}
-
 struct PlannedCall {
     std::string key;
     Prepared P;
@@ -991,7 +987,71 @@ struct PlannedCall {
     int n_streams = 1, n_events = 0;
     int64_t need = 0;
     uint64_t tick = 0;
+    // Replay.  The plan's second call is captured as a HIP graph; later calls
+    // launch it, with the arguments of the launches whose buffers differ from
+    // those an executable was last bound to updated in place.  Two
+    // executables take turns, so that one whose last launch may still be
+    // running is never updated.
+    int calls = 0;
+    hipGraph_t graph = nullptr;
+    std::vector<hipGraphNode_t> step_node;  // per step; nullptr: nothing launched
+    std::vector<hipKernelNodeParams> step_params;
+    std::vector<hipGraphNode_t> copy_node;  // per copy; nullptr: nothing copied
+    struct Exec {
+        hipGraphExec_t exec = nullptr;
+        bool launched = false;
+        uint64_t last_call = 0;           // the graph call that launched it last
+        std::vector<const void*> bound;  // the addresses its nodes hold (call_addresses)
+    };
+    Exec execs[2];
+    int turn = 0;
+    std::vector<const void*> captured;  // the addresses the graph was captured with
+    std::vector<size_t> addr_at;        // where each step's, then each copy's, addresses start
+    std::vector<const void*> cur;       // this call's addresses
 };
+
+// Frees a plan's captured graph and executables; the caller has waited for
+// their launches.
+void release_replay(PlannedCall& p)
+{
+    for (PlannedCall::Exec& e : p.execs) {
+        if (e.exec) (void)hipGraphExecDestroy(e.exec);
+        e = PlannedCall::Exec{};
+    }
+    if (p.graph) (void)hipGraphDestroy(p.graph);
+    p.graph = nullptr;
+    p.step_node.clear();
+    p.step_params.clear();
+    p.copy_node.clear();
+    p.captured.clear();
+    p.calls = 0;
+    p.turn = 0;
+}
+
+// The addresses each launch and output copy of a planned call reads and
+// writes, into p.cur: per step its operands then its result, per copy its
+// destination and source; p.addr_at[i] is where entry i starts.
+void call_addresses(PlannedCall& p, void* workspace)
+{
+    const Prepared& P = p.P;
+    char* base = static_cast<char*>(workspace);
+    auto addr = [&](const Slot& s) -> const void* {
+        return s.kind == Slot::kInput || s.kind == Slot::kBound ? s.ptr : base + s.offset;
+    };
+    const bool first = p.addr_at.empty();
+    p.cur.clear();
+    for (const Step& st : P.steps) {
+        if (first) p.addr_at.push_back(p.cur.size());
+        for (int o : st.operands) p.cur.push_back(addr(P.slots[o]));
+        p.cur.push_back(addr(P.slots[st.result]));
+    }
+    for (const Copy& c : P.copies) {
+        if (first) p.addr_at.push_back(p.cur.size());
+        p.cur.push_back(c.to->data);
+        p.cur.push_back(addr(P.slots[c.slot]));
+    }
+    if (first) p.addr_at.push_back(p.cur.size());
+}
 
 // What a call's plan depends on besides the graph: value names, dtypes and
 // counts, which bindings have data, which output bindings share a buffer,
@@ -1072,9 +1132,14 @@ int plan_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_val
     p->need = lay_out(p->P, p->topo);
     p->key = key;
     p->tick = ++g.plan_clock;
-    if ((int)g.plans.size() >= kMaxPlans)
-        g.plans.erase(std::min_element(g.plans.begin(), g.plans.end(),
-                                       [](const auto& a, const auto& b) { return a->tick < b->tick; }));
+    if ((int)g.plans.size() >= kMaxPlans) {
+        // forget the least recently used plan, after the launches of its graph
+        auto old = std::min_element(g.plans.begin(), g.plans.end(),
+                                    [](const auto& a, const auto& b) { return a->tick < b->tick; });
+        if ((*old)->graph && g.done) (void)hipEventSynchronize(g.done);
+        release_replay(**old);
+        g.plans.erase(old);
+    }
     g.plans.push_back(std::move(p));
     *out = g.plans.back().get();
     return MFH_OK;
@@ -1084,11 +1149,134 @@ int plan_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_val
 void drop_replays(Graph& g)
 {
     bool any = false;
-    for (const Replay& r : g.replays) any = any || r.exec;
+    for (const auto& p : g.plans) any = any || p->graph;
     if (any && g.done) (void)hipEventSynchronize(g.done);
-    for (Replay& r : g.replays)
-        if (r.exec) (void)hipGraphExecDestroy(r.exec);
-    g.replays.clear();
+    for (auto& p : g.plans) release_replay(*p);
+}
+
+// Points executable `e` of plan `p` at the addresses `cur`: the launches and
+// copies whose addresses differ from those it holds get new arguments (the
+// launch shape run_hip would choose for them: the vector path depends on
+// alignment).  `e` must have no launch still running.
+int bind_exec(PlannedCall& p, PlannedCall::Exec& e)
+{
+    const std::vector<const void*>& cur = p.cur;
+    auto same = [&](size_t i) {
+        return std::equal(cur.begin() + (long)p.addr_at[i], cur.begin() + (long)p.addr_at[i + 1],
+                          e.bound.begin() + (long)p.addr_at[i]);
+    };
+    const size_t ns = p.P.steps.size();
+    for (size_t t = 0; t < ns; t++) {
+        if (!p.step_node[t] || same(t)) continue;
+        const Step& st = p.P.steps[t];
+        const void* const* a = cur.data() + p.addr_at[t];
+        const int n_in = (int)(p.addr_at[t + 1] - p.addr_at[t]) - 1;
+        HipLaunch l;
+        MFH_TRY(prepare_hip(st.resolved, a, n_in, const_cast<void*>(a[n_in]), st.count, true, &l));
+        l.bind();
+        hipKernelNodeParams kp = p.step_params[t];
+        kp.gridDim = dim3(l.grid);
+        kp.blockDim = dim3(l.block);
+        kp.kernelParams = l.args.data();
+        kp.extra = nullptr;
+        MFH_TRY(check_hip(hipGraphExecKernelNodeSetParams(e.exec, p.step_node[t], &kp),
+                          "hipGraphExecKernelNodeSetParams(graph call)"));
+    }
+    for (size_t c = 0; c < p.P.copies.size(); c++) {
+        const size_t i = ns + c;
+        if (!p.copy_node[c] || same(i)) continue;
+        const Slot& sl = p.P.slots[p.P.copies[c].slot];
+        const void* const* a = cur.data() + p.addr_at[i];
+        MFH_TRY(check_hip(hipGraphExecMemcpyNodeSetParams1D(e.exec, p.copy_node[c], const_cast<void*>(a[0]), a[1],
+                                                            (size_t)sl.count * dtype_size(sl.dtype),
+                                                            hipMemcpyDeviceToDevice),
+                          "hipGraphExecMemcpyNodeSetParams1D(graph call)"));
+    }
+    e.bound = cur;
+    return MFH_OK;
+}
+
+// Launches plan `p`'s captured graph for this call's buffers: an executable
+// already bound to them, else the next one in turn, once its last launch has
+// finished, bound to them.  A plan on several streams is not rebound (its
+// rebinding and graph launch took more host time than its plain launches:
+// 185 against 163 us for 32 nodes on four streams); such a call sets
+// `launched` false and runs as plain launches.
+int replay_call(Graph& g, PlannedCall& p, hipStream_t stream, bool* launched)
+{
+    *launched = false;
+    call_addresses(p, g.ws);
+    PlannedCall::Exec* e = nullptr;
+    for (PlannedCall::Exec& x : p.execs)
+        if (x.exec && x.bound == p.cur) e = &x;
+    if (!e && p.n_streams > 1) return MFH_OK;
+    if (!e) {
+        e = &p.execs[p.turn];
+        p.turn ^= 1;
+        if (!e->exec) {
+            MFH_TRY(check_hip(hipGraphInstantiate(&e->exec, p.graph, nullptr, nullptr, 0),
+                              "hipGraphInstantiate(graph call)"));
+            e->bound = p.captured;
+        } else if (e->launched) {
+            // its last call's event, or a later call's in the same ring slot
+            MFH_TRY(check_hip(hipEventSynchronize(g.done_ring[e->last_call % Graph::kDoneRing]),
+                              "hipEventSynchronize(graph call replay)"));
+        }
+        MFH_TRY(bind_exec(p, *e));
+    }
+    MFH_TRY(check_hip(hipGraphLaunch(e->exec, stream), "hipGraphLaunch(graph call)"));
+    e->launched = true;
+    e->last_call = g.call_seq;
+    *launched = true;
+    return MFH_OK;
+}
+
+// Captures this call's launches on the graph's capture stream as plan `p`'s
+// graph and launches it on `stream`.  Returns false (nothing launched) where
+// capture is not available or a launch's node cannot be told apart.
+bool capture_call(Graph& g, PlannedCall& p, hipStream_t stream)
+{
+    if (!g.capture && hipStreamCreateWithFlags(&g.capture, hipStreamNonBlocking) != hipSuccess) return false;
+    if (hipStreamBeginCapture(g.capture, hipStreamCaptureModeThreadLocal) != hipSuccess) return false;
+    std::vector<hipGraphNode_t> nodes;
+    const int rc = launch_all(g, p.P, p.topo, p.n_streams, g.capture, g.ws, true, &nodes);
+    hipGraph_t graph = nullptr;
+    const hipError_t end = hipStreamEndCapture(g.capture, &graph);
+    const size_t ns = p.P.steps.size();
+    bool ok = rc == MFH_OK && end == hipSuccess && graph && nodes.size() == ns + p.P.copies.size();
+    std::vector<hipKernelNodeParams> params(ns);
+    for (size_t i = 0; ok && i < nodes.size(); i++) {
+        if (i < ns) {
+            if (p.P.steps[i].count > 0)
+                ok = nodes[i] && hipGraphKernelNodeGetParams(nodes[i], &params[i]) == hipSuccess;
+        } else {
+            const Slot& sl = p.P.slots[p.P.copies[i - ns].slot];
+            if (sl.count > 0) ok = nodes[i] != nullptr;
+        }
+    }
+    // Everything that can fail comes before the launch: a call that falls
+    // back to plain launches must not have run already.
+    hipGraphExec_t exec = nullptr;
+    if (ok && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) ok = false;
+    if (ok && hipGraphLaunch(exec, stream) != hipSuccess) ok = false;
+    if (!ok) {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        (void)hipGetLastError();
+        return false;
+    }
+    p.graph = graph;
+    p.step_node.assign(nodes.begin(), nodes.begin() + (long)ns);
+    p.copy_node.assign(nodes.begin() + (long)ns, nodes.end());
+    p.step_params = std::move(params);
+    call_addresses(p, g.ws);
+    p.captured = p.cur;
+    p.execs[0].exec = exec;
+    p.execs[0].bound = p.captured;
+    p.execs[0].launched = true;
+    p.execs[0].last_call = g.call_seq;
+    p.turn = 1;
+    return true;
 }
 
 // A change to the graph: every captured call and every plan goes.
@@ -1103,42 +1291,27 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
 {
     const Device* dev;
     MFH_TRY(bind_device(&dev));
-    if (!g.replays.empty() && g.replay_generation != module_generation()) drop_replays(g);
+    if (g.replay_generation != module_generation()) {
+        // captured calls hold function handles of unloaded modules
+        drop_replays(g);
+        g.replay_generation = module_generation();
+    }
 
     // A call the caller is capturing runs as plain launches into their graph.
     hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
     MFH_TRY(check_hip(hipStreamIsCapturing(stream, &capturing), "hipStreamIsCapturing"));
-    const bool replayable = g.replay && !g.replay_broken && capturing == hipStreamCaptureStatusNone;
-    std::string key;
-    Replay* seen = nullptr;
-    if (replayable) {
-        key = call_key(g, inputs, n_inputs, outputs, n_outputs);
-        for (Replay& r : g.replays)
-            if (r.key == key) seen = &r;
-        if (seen && seen->exec) {
-            // the same call again: replay its graph
-            if (g.called && g.last_stream != stream)
-                MFH_TRY(check_hip(hipStreamWaitEvent(stream, g.done, 0), "hipStreamWaitEvent(previous call)"));
-            MFH_TRY(check_hip(hipGraphLaunch(seen->exec, stream), "hipGraphLaunch(graph call)"));
-            seen->tick = ++g.replay_clock;
-            g.replayed++;
-            g.streams_used = seen->streams;
-            MFH_TRY(check_hip(hipEventRecord(g.done, stream), "hipEventRecord(call done)"));
-            g.last_stream = stream;
-            g.called = true;
-            return MFH_OK;
-        }
-    }
+    const bool captured = capturing != hipStreamCaptureStatusNone;
+    const bool replayable = g.replay && !g.replay_broken && !captured;
 
     // Launches, streams (ScheduleStreams over the launches,
-    // ir/stream_scheduler.go:56) and placement, planned once per signature.
+    // ir/stream_scheduler.go:56) and placement, planned once per signature
+    // and rebound to this call's buffers.
     PlannedCall* plan = nullptr;
     MFH_TRY(plan_call(g, inputs, n_inputs, outputs, n_outputs, &plan));
     Prepared& P = plan->P;
     const Topology& topo = plan->topo;
     const int n_streams = plan->n_streams, n_events = plan->n_events;
     const int64_t need = plan->need;
-    const bool captured = capturing != hipStreamCaptureStatusNone;
     if (need > g.ws_bytes && captured)
         return fail(MFH_ERR_INVALID_ARGUMENT,
                     "graph call: the workspace must grow to %lld bytes while the caller's stream is being captured; "
@@ -1146,7 +1319,6 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
     if (need > g.ws_bytes) {
         // captured calls address the old workspace
         drop_replays(g);
-        seen = nullptr;
         if (g.ws) {
             // the previous workspace may still be read by queued work
             MFH_TRY(check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize"));
@@ -1157,8 +1329,6 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         MFH_TRY(check_hip(hipMalloc(&g.ws, (size_t)need), "hipMalloc(graph workspace)"));
         g.ws_bytes = need;
         g.ws_constants_valid = false;
-        // this call is remembered under the new workspace
-        if (replayable) key = call_key(g, inputs, n_inputs, outputs, n_outputs);
     }
     MFH_TRY(graph_streams(g, n_streams, n_events));
     // The workspace is shared by every call: work on a new caller stream
@@ -1177,55 +1347,27 @@ int graph_call(Graph& g, const mfh_value* inputs, int32_t n_inputs, const mfh_va
         g.ws_constants_valid = true;
     }
 
-    // The second identical call is captured once and replayed from then on;
-    // the first runs as plain launches (and loads every kernel it needs).
+    // A plan's first call runs as plain launches (and loads every kernel it
+    // needs); its second is captured as a HIP graph, and later calls launch
+    // that graph, bound to their buffers.
     bool launched = false;
-    if (replayable && seen) {
-        hipGraph_t graph = nullptr;
-        hipGraphExec_t exec = nullptr;
-        if (!g.capture) MFH_TRY(check_hip(hipStreamCreateWithFlags(&g.capture, hipStreamNonBlocking), "hipStreamCreateWithFlags"));
-        if (hipStreamBeginCapture(g.capture, hipStreamCaptureModeThreadLocal) == hipSuccess) {
-            const int rc = launch_all(g, P, topo, n_streams, g.capture, g.ws);
-            const hipError_t end = hipStreamEndCapture(g.capture, &graph);
-            if (rc == MFH_OK && end == hipSuccess && graph &&
-                hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess)
-                exec = nullptr;
-        }
-        if (graph) (void)hipGraphDestroy(graph);
-        if (exec) {
-            seen->exec = exec;
-            seen->streams = n_streams;
-            seen->tick = ++g.replay_clock;
-            MFH_TRY(check_hip(hipGraphLaunch(exec, stream), "hipGraphLaunch(graph call)"));
-            launched = true;
-        } else {
-            // capture is not available here: this call and later ones run as
-            // plain launches
-            (void)hipGetLastError();
-            g.replay_broken = true;
-        }
+    if (replayable && plan->graph) {
+        MFH_TRY(replay_call(g, *plan, stream, &launched));
+        if (launched) g.replayed++;
+    } else if (replayable && plan->calls >= 1) {
+        launched = capture_call(g, *plan, stream);
+        // capture is not available here: this call and later ones run as
+        // plain launches
+        if (!launched) g.replay_broken = true;
     }
     if (!launched) MFH_TRY(launch_all(g, P, topo, n_streams, stream, g.ws));
     g.streams_used = n_streams;
     if (captured) return MFH_OK;
-    if (replayable && !seen) {
-        if ((int)g.replays.size() >= kMaxReplays) {
-            // forget the least recently used call
-            auto old = std::min_element(g.replays.begin(), g.replays.end(),
-                                        [](const Replay& a, const Replay& b) { return a.tick < b.tick; });
-            if (old->exec) {
-                (void)hipEventSynchronize(g.done);
-                (void)hipGraphExecDestroy(old->exec);
-            }
-            g.replays.erase(old);
-        }
-        Replay r;
-        r.key = key;
-        r.tick = ++g.replay_clock;
-        g.replays.push_back(std::move(r));
-        g.replay_generation = module_generation();
-    }
-    MFH_TRY(check_hip(hipEventRecord(g.done, stream), "hipEventRecord(call done)"));
+    plan->calls++;
+    hipEvent_t done = g.done_ring[g.call_seq % Graph::kDoneRing];
+    MFH_TRY(check_hip(hipEventRecord(done, stream), "hipEventRecord(call done)"));
+    g.done = done;
+    g.call_seq++;
     g.last_stream = stream;
     g.called = true;
     return MFH_OK;
@@ -1402,8 +1544,8 @@ int mfh_graph_release(mfh_graph* graph)
 {
     if (!graph) return MFH_OK;
     int rc = MFH_OK;
-    const bool device_state = graph->ws || graph->fork || graph->done || !graph->aux.empty() || !graph->events.empty() ||
-                              graph->capture || !graph->replays.empty();
+    const bool device_state = graph->ws || graph->fork || graph->done_ring[0] || !graph->aux.empty() || !graph->events.empty() ||
+                              graph->capture || !graph->plans.empty();
     if (device_state) {
         drop_replays(*graph);
         const Device* dev;
@@ -1416,7 +1558,8 @@ int mfh_graph_release(mfh_graph* graph)
             for (hipEvent_t e : graph->joins) (void)hipEventDestroy(e);
             if (graph->capture) (void)hipStreamDestroy(graph->capture);
             if (graph->fork) (void)hipEventDestroy(graph->fork);
-            if (graph->done) (void)hipEventDestroy(graph->done);
+            for (hipEvent_t e : graph->done_ring)
+                if (e) (void)hipEventDestroy(e);
         }
     }
     delete graph;

@@ -1,5 +1,7 @@
-"""GPU tests of graph-call replay: a call identical to an earlier one is
-captured as a HIP graph on its second occurrence and replayed afterwards.
+"""GPU tests of graph-call replay: the second call of a plan (the same value
+names, dtypes, counts and output aliasing) is captured as a HIP graph, and
+later calls launch that graph, with the arguments of the launches whose
+buffers changed updated in place.
 
 Every call's outputs are checked against numpy float32 evaluations of the same
 exact ops (one IEEE f32 rounding each), with the inputs rewritten by eager
@@ -122,7 +124,8 @@ def test_replays_per_buffer_set():
         x, y = b.fill(rng)
         b.call(g)
         b.check(chain_expected(x, y), f"set {call % 2} call {call}")
-    assert g.replayed_calls() == 2  # the third call of each set
+    # call 0 launches, call 1 is captured, calls 2-5 replay bound to their set
+    assert g.replayed_calls() == 4
 
 
 def test_replay_off():
@@ -302,3 +305,119 @@ def test_outputs_bound_over_inputs():
     torch.cuda.synchronize()
     same(xc, x, "x passed through")
     same(tx, x + y, "s over x")
+
+
+def fresh_views(torch, n, pad):
+    """A new buffer of n floats, misaligned by one element when `pad`."""
+    store = torch.empty(n + 1, device="cuda")
+    return store[1:] if pad else store[:n]
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_replays_on_fresh_buffers(fuse):
+    # New buffers on every call, every third one misaligned by one element, so
+    # that launches switch between the vector and the element path: calls 2
+    # onwards replay the captured graph with the changed launches rebound.
+    torch = torch_mod()
+    rng = np.random.default_rng(29 + fuse)
+    g = chain_graph(fuse=fuse)
+    n = (1 << 16) + 3
+    for call in range(9):
+        pad = call % 3 == 2
+        x = rng.normal(0, 1, n).astype(np.float32)
+        y = rng.normal(0, 1, n).astype(np.float32)
+        tx, ty = fresh_views(torch, n, pad), fresh_views(torch, n, pad)
+        te, tc = fresh_views(torch, n, pad), fresh_views(torch, n, not pad)
+        tx.copy_(torch.from_numpy(x))
+        ty.copy_(torch.from_numpy(y))
+        te.fill_(float("nan"))
+        tc.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.call({"x": tx, "y": ty}, {"e": te, "c": tc}, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        want = chain_expected(x, y)
+        for k, t in (("e", te), ("c", tc)):
+            got = t.cpu().numpy()
+            bad = np.flatnonzero(got.view(np.uint32) != want[k].view(np.uint32))
+            assert bad.size == 0, f"call {call} (pad {pad}) output {k}: {bad.size} mismatches"
+        log(f"fresh-buffer call {call} (fused {fuse}, pad {pad}) ok")
+    assert g.replayed_calls() == 7
+
+
+def test_replays_rotate_buffer_sets_back_to_back():
+    # Three buffer sets in turn, calls queued back to back with no host
+    # synchronisation between them: the two executables take turns, each
+    # rebound only once its previous launch has finished.
+    torch = torch_mod()
+    rng = np.random.default_rng(31)
+    g = chain_graph(fuse=False)
+    sets = [Buffers((1 << 17) + 9, ["e", "c"]) for _ in range(3)]
+    inputs = [b.fill(rng) for b in sets]
+    outs = []
+    for call in range(12):
+        b = sets[call % 3]
+        out = {k: torch.empty(b.n, device="cuda") for k in ("e", "c")}
+        g.call({"x": b.x, "y": b.y}, out, torch.cuda.current_stream().cuda_stream)
+        outs.append((call % 3, out))
+    torch.cuda.synchronize()
+    for call, (k, out) in enumerate(outs):
+        want = chain_expected(*inputs[k])
+        for key, t in out.items():
+            got = t.cpu().numpy()
+            bad = np.flatnonzero(got.view(np.uint32) != want[key].view(np.uint32))
+            assert bad.size == 0, f"call {call} set {k} output {key}: {bad.size} mismatches"
+    assert g.replayed_calls() == 10
+
+
+def test_replays_rebind_output_copies():
+    # s bound one element into x's buffer is computed aside and copied out
+    # after the last launch; on fresh buffers the replayed copy follows them.
+    torch = torch_mod()
+    rng = np.random.default_rng(32)
+    k = np.float32(0.75)
+    g = Graph(inputs=["x", "y"], outputs={"s": "s"}, execution_dtype=F32, nodes=[
+        GraphNode("k", "math.constant", [], attributes={"value": 0.75}),
+        GraphNode("a", "math.mul", ["x", "k"]), GraphNode("s", "math.add", ["a", "y"])])
+    G.run(g)
+    G.attach_kernels(g)
+    n = (1 << 15) + 1
+    for call in range(6):
+        x = rng.normal(0, 1, n).astype(np.float32)
+        y = rng.normal(0, 1, n).astype(np.float32)
+        store = torch.empty(n + 1, device="cuda")
+        store[:n].copy_(torch.from_numpy(x))
+        ty = torch.from_numpy(y).cuda()
+        torch.cuda.synchronize()
+        g.call({"x": store[:n], "y": ty}, {"s": store[1:]}, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = store[1:].cpu().numpy()
+        want = x * k + y
+        bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+        assert bad.size == 0, f"call {call}: {bad.size} mismatches"
+    assert g.replayed_calls() == 4
+
+
+def test_multi_stream_replays_only_on_captured_buffers():
+    # A plan on several streams is not rebound: it replays on the buffers it
+    # was captured with and runs plain launches on any others, with the
+    # right results either way.
+    rng = np.random.default_rng(33)
+    nodes = [GraphNode("a1", "math.neg", ["x"]), GraphNode("a2", "math.abs", ["a1"]),
+             GraphNode("b1", "math.abs", ["y"]), GraphNode("b2", "math.max", ["b1", "a1"]),
+             GraphNode("c1", "math.mul", ["x", "y"]), GraphNode("d", "math.add", ["a2", "b2"]),
+             GraphNode("e", "math.sub", ["d", "c1"])]
+    g = Graph(inputs=["x", "y"], outputs={"e": "e", "b2": "b2"}, execution_dtype=F32, nodes=nodes)
+    P.set_max_streams(g, 4)
+    n = (1 << 18) + 5
+    a, b = Buffers(n, ["e", "b2"]), Buffers(n, ["e", "b2"])
+    # a: plain, b: captured, a: plain, b: replay, fresh: plain, b: replay
+    for call, buf in enumerate([a, b, a, b, Buffers(n, ["e", "b2"]), b]):
+        x, y = buf.fill(rng)
+        buf.call(g)
+        a1 = -x
+        b1 = np.abs(y)
+        b2 = np.where(b1 > a1, b1, a1)
+        buf.check({"b2": b2, "e": (np.abs(a1) + b2) - x * y}, f"call {call}")
+        log(f"multi-stream call {call} ok")
+    assert P.streams_used(g) == 3
+    assert g.replayed_calls() == 2
