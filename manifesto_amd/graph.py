@@ -294,7 +294,8 @@ class Graph:
         return _L().mfh_graph_workspace_bytes(self._h)
 
     def set_replay(self, enabled: bool) -> None:
-        """Replays of repeated identical calls as captured HIP graphs (on by
+        """Replays of calls with one plan (names, dtypes, counts, aliasing) as
+        one captured HIP graph, rebound to each call's buffers (on by
         default)."""
         check(_L().mfh_graph_set_replay(self._h, int(enabled)))
 
