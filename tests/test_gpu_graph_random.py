@@ -6,7 +6,10 @@ codegen/cpu.go:59-214, each node's output stored in its dtype).
 
 The ops are the ones whose f32 result is exact or correctly rounded (add,
 sub, mul, div, max, min, neg, abs, relu, sqrt), so every output must match
-to the bit (NaN positions included).  Inputs mix storage dtypes and operand
+to the bit (NaN positions included).  A second set of graphs adds every
+transcendental op the optimizer fuses (exp, log, sigmoid, tanh, swish, gelu,
+leaky_relu), compiled with MFH_FUSION_PRECISE (the reference's f64 forms,
+rounded once), and must match to the bit as well.  Inputs mix storage dtypes and operand
 modes (full, a repeating row, a scalar); nodes get random output types;
 outputs include intermediates read later and inputs passed through.  Each
 graph is called three times (plain launches, capture, replay) and, for half
@@ -120,6 +123,87 @@ def test_random_graph_matches_the_oracle(seed):
         t, p = empty_dev(count * SIZE[dt])
         outs[key], views[key] = t, (p, dt, count)
     for call in range(3):  # the same buffers: plain launches, capture, replay
+        for t in outs.values():
+            t.fill_(0xA5)
+        graph.call(ins, views, stream())
+        for key, value in outputs.items():
+            w, wdt = want[value]
+            dt, count = shapes[key]
+            assert (dt, count) == (wdt, w.size), f"seed {seed} output {key}: shape"
+            got = to_host(outs[key], NP[dt])
+            compare_storage(got, w.view(NP[dt]), dt, 0, f"seed {seed} call {call} output {key} ({value})")
+    assert graph.replayed_calls() == 1
+
+
+TRANSCENDENTAL = ["math.exp", "math.log", "activation.sigmoid", "activation.tanh", "activation.swish",
+                  "activation.gelu", "activation.leaky_relu"]
+
+
+def random_graph_transcendental(rng, n, d):
+    """random_graph's shapes and operand modes over every elementwise op the
+    optimizer fuses.  A gelu reads max(x, -4.5): below -4.9 the reference's
+    own gelu (1 + tanh cancelling in f64) is rounding noise that two correct
+    f64 evaluations may place a quantum apart."""
+    inputs = {}
+    for k in range(int(rng.integers(1, 4))):
+        count = [n, d, 1][int(rng.choice(3, p=[0.6, 0.25, 0.15]))]
+        inputs[f"in{k}"] = (DTYPES[int(rng.integers(3))], count)
+    names = list(inputs)
+    nodes = [GraphNode("floor", "math.constant", [], attributes={"value": -4.5})]
+    n_nodes = int(rng.integers(3, 11))
+    for i in range(n_nodes):
+        pick = lambda: names[int(rng.integers(len(names)))]  # noqa: E731
+        out_t = [0, O.FLOAT32, O.BFLOAT16, O.FLOAT16][int(rng.integers(4))]
+        r = rng.random()
+        if r < 0.45:
+            op = TRANSCENDENTAL[int(rng.integers(len(TRANSCENDENTAL)))]
+            src = pick()
+            if op == "activation.gelu":
+                nodes.append(GraphNode(f"g{i}", "math.max", [src, "floor"]))
+                src = f"g{i}"
+            nodes.append(GraphNode(f"n{i}", op, [src], output_type=out_t))
+        elif r < 0.6:
+            nodes.append(GraphNode(f"n{i}", UNARY[int(rng.integers(len(UNARY)))], [pick()], output_type=out_t))
+        else:
+            nodes.append(GraphNode(f"n{i}", BINARY[int(rng.integers(len(BINARY)))], [pick(), pick()],
+                                   output_type=out_t))
+        names.append(f"n{i}")
+    outputs = {"last": f"n{n_nodes - 1}"}
+    if rng.random() < 0.6:
+        outputs["mid"] = f"n{int(rng.integers(n_nodes))}"
+    return inputs, nodes, outputs
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_transcendental_graph_precise_matches_the_oracle(seed):
+    # MFH_FUSION_PRECISE evaluates every transcendental in the reference's f64
+    # form and rounds once, fused or not: bit-identical to the oracle's
+    # evaluation of the optimised graph, NaN where it is NaN.
+    rng = np.random.default_rng(0x5EED + 300 + seed)
+    rows, d = 101, 12
+    n = rows * d  # not a multiple of 8: every vector path has a tail
+    inputs, nodes, outputs = random_graph_transcendental(rng, n, d)
+    graph = Graph(inputs=list(inputs), outputs=outputs, execution_dtype=O.FLOAT32, nodes=nodes)
+    G.run(graph)
+    G.attach_kernels(graph, flags=M.FUSION_PRECISE)
+    log(f"transcendental graph {seed}: {[(nd.id, nd.op) for nd in graph.nodes]}")
+    data = {}
+    for name, (dt, count) in inputs.items():
+        a = rng.normal(0, 2, count).astype(np.float32)
+        a[rng.random(count) < 0.03] *= -1e30
+        data[name] = (O.encode(a, dt), dt)
+    want = oracle_values(graph, data)
+    keep, ins = [], {}
+    for name, (a, dt) in data.items():
+        t, p = to_dev(a)
+        keep.append(t)
+        ins[name] = (p, dt, a.size)
+    shapes = {key: graph.output_shape({k: (None, dt, a.size) for k, (a, dt) in data.items()}, key) for key in outputs}
+    outs, views = {}, {}
+    for key, (dt, count) in shapes.items():
+        t, p = empty_dev(count * SIZE[dt])
+        outs[key], views[key] = t, (p, dt, count)
+    for call in range(3):
         for t in outs.values():
             t.fill_(0xA5)
         graph.call(ins, views, stream())
