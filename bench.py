@@ -508,8 +508,9 @@ def time_gpu(w, steps, warmup, use_graph=None):
       launch (measured over the warm-up launches) for each timed launch.  The
       host checks that the start event had not yet fired when its last
       launch was queued; if it had, the region could hold host gaps and the
-      measurement is taken again behind a spin four times longer (at most
-      three times).
+      measurement is taken again behind a spin four times longer.  Three
+      attempts at most: the last is reported either way, and host gaps in
+      it could only understate the rate.
     - More steps (or use_graph True): the launches are captured into one HIP
       graph; the warm-up replays it and one replay is timed behind a 0.5 ms
       spin.  The replay adds its own entry and exit, about 12 us per replay
