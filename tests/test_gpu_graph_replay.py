@@ -421,3 +421,22 @@ def test_multi_stream_replays_only_on_captured_buffers():
         log(f"multi-stream call {call} ok")
     assert P.streams_used(g) == 3
     assert g.replayed_calls() == 2
+
+
+def test_replays_across_a_workspace_growth():
+    # Small calls are captured and replayed; a larger call grows the
+    # workspace, which drops every captured graph; small calls on new buffers
+    # then run plain once, are captured again and replay, all bit-exact.
+    torch = torch_mod()
+    rng = np.random.default_rng(34)
+    g = chain_graph(fuse=False)
+    sizes = [4099, 4099, 4099, 1 << 18, 4099, 4099, 4099, 4099]
+    for call, n in enumerate(sizes):
+        b = Buffers(n, ["e", "c"])
+        x, y = b.fill(rng)
+        b.call(g)
+        b.check(chain_expected(x, y), f"call {call} (n {n})")
+        log(f"growth call {call} n {n}: replayed so far {g.replayed_calls()}")
+    # small plan: plain, capture, replay; the large call grows the workspace and
+    # drops it; small again: plain, capture, replay, replay
+    assert g.replayed_calls() == 3
