@@ -43,6 +43,69 @@ def test_library_exports_every_declared_symbol():
     assert M.lib().mfh_version() == 100
 
 
+def declared_prototypes():
+    """(return type, name, parameter list) of every function the headers declare."""
+    text = ""
+    for header in sorted(os.listdir(INCLUDE)):
+        if header.endswith(".h"):
+            t = open(os.path.join(INCLUDE, header)).read()
+            t = re.sub(r"/\*.*?\*/", "", t, flags=re.S)
+            text += re.sub(r"//[^\n]*", "", t)
+    return re.findall(r"([A-Za-z_][\w \*]*?[\s\*])(mfh_\w+)\s*\(([^;{]*?)\)\s*;", text)
+
+
+# (kind, bytes) of a C type as the ABI passes it: pointers, integers, floats.
+_C_KINDS = {"int": ("i", 4), "int32_t": ("i", 4), "int64_t": ("i", 8), "uint8_t": ("i", 1),
+            "uint32_t": ("i", 4), "size_t": ("i", 8), "float": ("f", 4), "double": ("f", 8), "void": ("v", 0)}
+
+
+def c_kind(decl):
+    decl = " ".join(decl.replace("const", "").split())
+    if "*" in decl or decl == "hipStream_t":
+        return ("p", 8)
+    return _C_KINDS.get(decl, ("?", decl))
+
+
+def ctypes_kind(t):
+    import ctypes
+    if t is None:
+        return ("v", 0)
+    if t in (ctypes.c_void_p, ctypes.c_char_p) or (isinstance(t, type) and issubclass(t, ctypes._Pointer)):
+        return ("p", 8)
+    if t in (ctypes.c_float, ctypes.c_double):
+        return ("f", ctypes.sizeof(t))
+    return ("i", ctypes.sizeof(t))
+
+
+def test_ctypes_bindings_match_the_header_prototypes():
+    # Every function of include/*.h is declared to ctypes by the package, with
+    # the header's arity and, per argument and result, the same kind (pointer,
+    # integer, float) and width: a 64-bit count bound as a 32-bit one would be
+    # truncated without an error.
+    from manifesto_amd import backend, graph, plan, safetensors
+    L = M.lib()
+    for module in (backend, graph, plan, safetensors):
+        module._L()
+    protos = declared_prototypes()
+    assert len(protos) == len(declared_symbols())
+    undeclared, mismatched = [], []
+    for ret, name, params in protos:
+        fn = getattr(L, name)
+        if fn.argtypes is None:
+            undeclared.append(name)
+            continue
+        want = [c_kind(ret)]
+        for p in (p.strip() for p in params.split(",")):
+            if p and p != "void":
+                m = re.match(r"(.*?[\s\*])\w+$", p)
+                want.append(c_kind(m.group(1) if m else p))
+        got = [ctypes_kind(fn.restype)] + [ctypes_kind(a) for a in fn.argtypes]
+        if want != got:
+            mismatched.append((name, want, got))
+    assert not undeclared, undeclared
+    assert not mismatched, mismatched
+
+
 def swiglu_nodes():
     # Mul(Silu(In0), In1): what Fuse builds from swish -> mul (optimizer/fuse.go:199-265).
     return flatten((N_MUL, (N_SILU, ("in", 0)), ("in", 1)))
