@@ -200,7 +200,11 @@ typedef struct {
 
 /* Transcendental nodes evaluated in f64 exactly as codegen/cpu.go:172-200
  * writes them (bit-identical to the reference but for f64 rounding ties);
- * without it Sigmoid/Silu/Gelu use f32 algorithms within 2 ulp. */
+ * without it Sigmoid/Silu/Gelu use f32 algorithms within 2 ulp.  Sigmoid,
+ * Silu and Gelu take f64 forms about twice as cheap as the reference's, whose
+ * result is used where a test shows that it rounds to the same f32 as the
+ * reference's value; the elements the test cannot decide (about one in 2^12)
+ * are recomputed with the reference's formulas. */
 #define MFH_FUSION_PRECISE 1u
 
 /* Silu and Gelu in their f32 fast forms in every chain (the forms chains of
@@ -211,6 +215,11 @@ typedef struct {
  * For measuring the 16-bit chains' forms over f32 results; no counterpart in
  * the reference. */
 #define MFH_FUSION_SHORT_QUOTIENT 2u
+
+/* With MFH_FUSION_PRECISE: every element through the reference's formulas,
+ * without the rounding test.  The results are the same, at about twice the
+ * instructions; for checking the test.  No counterpart in the reference. */
+#define MFH_FUSION_NO_ROUNDING_TEST 4u
 
 typedef struct mfh_kernel mfh_kernel;
 

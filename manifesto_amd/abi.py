@@ -19,6 +19,7 @@ UINT64, UINT32, UINT16, UINT8 = 12, 13, 14, 15
 OPERAND_FULL, OPERAND_PERIODIC, OPERAND_SCALAR = 0, 1, 2
 FUSION_PRECISE = 1
 FUSION_SHORT_QUOTIENT = 2
+FUSION_NO_ROUNDING_TEST = 4
 
 MFH_OK = 0
 

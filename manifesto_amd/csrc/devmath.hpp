@@ -195,21 +195,44 @@ MFH_MATH float mfh_gelu_ref(float v)
 // conversion took four (f64 runs at half the f32 rate on gfx950).
 #define MFH_ROUND_INT_D 6755399441055744.0  // 1.5 * 2^52
 
+// 1 + 2^t in f64 for |t| < 2^31, by the round-to-integer reduction and the
+// degree-8 polynomial (2^-39.9).
+MFH_MATH double mfh_one_plus_2exp(double t)
+{
+    const double tk = t + MFH_ROUND_INT_D;
+    const double kd = tk - MFH_ROUND_INT_D;
+    return 1.0 + mfh_ldexp(mfh_exp2_poly_d(t - kd), mfh_low_int(tk));
+}
+
+// 1 / den: the hardware reciprocal and one Newton step.
+MFH_MATH double mfh_recip_newton(double den)
+{
+    const double r = mfh_rcp(den);
+    return mfh_fma(r, mfh_fma(-den, r, 1.0), r);
+}
+
 // sigmoid(v) = 1 / (1 + 2^t), t = -v log2(e), all in f64: for v < 0 the
 // result is ~e^v and inherits the full relative error of E, which an f32
 // exponential (0.9 ulp) plus the final rounding would push past the 1-ulp
 // Sigmoid budget on a few inputs.  In f64 (2^f to 2^-39.9, reciprocal plus one
 // Newton step) the single rounding to f32 is the only error that matters.
 // Below -708 (and -Inf, NaN) the reference's form; +Inf gives 1 by itself.
-MFH_MATH float mfh_sigmoid_fast(float v, bool& rare)
+// mfh_sigmoid_z is that f64 value (and sets den = 1 + E).
+MFH_MATH double mfh_sigmoid_z(float v, double& den)
 {
     const double x = (double)mfh_med3f(v, -708.0f, 800.0f);
     const double tk = mfh_fma(x, -MFH_LOG2E_D, MFH_ROUND_INT_D);
     const double kd = tk - MFH_ROUND_INT_D;
-    const double den = 1.0 + mfh_ldexp(mfh_exp2_poly_d(mfh_fma(x, -MFH_LOG2E_D, -kd)), mfh_low_int(tk));
-    const double r = mfh_rcp(den);
+    den = 1.0 + mfh_ldexp(mfh_exp2_poly_d(mfh_fma(x, -MFH_LOG2E_D, -kd)), mfh_low_int(tk));
+    return mfh_recip_newton(den);
+}
+
+MFH_MATH float mfh_sigmoid_fast(float v, bool& rare)
+{
+    double den;
+    const double z = mfh_sigmoid_z(v, den);
     rare |= !(v >= -708.0f);
-    return (float)mfh_fma(r, mfh_fma(-den, r, 1.0), r);
+    return (float)z;
 }
 
 // silu(v) = v / (1 + e^-v).  One clamp to [-16.5, 87] serves the
@@ -234,24 +257,24 @@ MFH_MATH float mfh_silu_fast(float v, bool& rare)
 // 2^t by the round-to-integer reduction and the degree-8 polynomial
 // (2^-39.9), the reciprocal of 1 + e^-v plus one Newton step, times v, one
 // rounding.  The f32 result is the reference's except where the exact value
-// lies within about 2^-39 of an f32 rounding boundary.  Below -708 (and
-// -Inf, NaN) the reference's form; +Inf gives +Inf by itself.  About twice
+// lies within about 2^-39 of an f32 rounding boundary.  Every v the clamp to
+// [-708, 800] changes (and NaN) takes the reference's form.  About twice
 // the instructions of mfh_silu_fast, which the 4-byte elements of such a
-// chain leave room for.
-MFH_MATH double mfh_recip_one_plus_2exp(double t)
+// chain leave room for.  mfh_silu_z is the f64 value for m = v inside the
+// clamp.
+MFH_MATH double mfh_silu_z(float m, double& den)
 {
-    const double tk = t + MFH_ROUND_INT_D;
-    const double kd = tk - MFH_ROUND_INT_D;
-    const double den = 1.0 + mfh_ldexp(mfh_exp2_poly_d(t - kd), mfh_low_int(tk));
-    const double r = mfh_rcp(den);
-    return mfh_fma(r, mfh_fma(-den, r, 1.0), r);
+    const double x = (double)m;
+    den = mfh_one_plus_2exp(x * -MFH_LOG2E_D);
+    return x * mfh_recip_newton(den);
 }
 
 MFH_MATH float mfh_silu_fast_x(float v, bool& rare)
 {
-    const double x = (double)mfh_med3f(v, -708.0f, 800.0f);
-    rare |= !(v >= -708.0f);
-    return (float)((double)v * mfh_recip_one_plus_2exp(x * -MFH_LOG2E_D));
+    const float m = mfh_med3f(v, -708.0f, 800.0f);
+    rare |= m != v;
+    double den;
+    return (float)mfh_silu_z(m, den);
 }
 
 // Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
@@ -288,13 +311,20 @@ MFH_MATH float mfh_gelu_fast(float v, bool& rare)
 
 // gelu for chains that stream f32: the same argument t = d w in f64, then
 // 2^t, the quotient and the product with v in f64 as mfh_silu_fast_x makes
-// them, one rounding.
+// them, one rounding.  mfh_gelu_z is that f64 value for c inside the clamp.
+MFH_MATH double mfh_gelu_z(float c, double& den)
+{
+    const double d = (double)c;
+    den = mfh_one_plus_2exp(mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA) * d);
+    return d * mfh_recip_newton(den);
+}
+
 MFH_MATH float mfh_gelu_fast_x(float v, bool& rare)
 {
     const float c = mfh_med3f(v, -4.9f, 1024.0f);
     rare |= c != v;
-    const double d = (double)c;
-    return (float)((double)v * mfh_recip_one_plus_2exp(mfh_fma(d * d, MFH_GELU_KB, MFH_GELU_KA) * d));
+    double den;
+    return (float)mfh_gelu_z(c, den);
 }
 
 // mfh_<name>_rare: the reference form as a real call (MFH_RARE), which the
@@ -318,6 +348,82 @@ MFH_FAST_OR_REF(mfh_silu, mfh_silu_fast, mfh_silu_rare)
 MFH_FAST_OR_REF(mfh_silu_x, mfh_silu_fast_x, mfh_silu_rare)
 MFH_FAST_OR_REF(mfh_gelu, mfh_gelu_fast, mfh_gelu_rare)
 MFH_FAST_OR_REF(mfh_gelu_x, mfh_gelu_fast_x, mfh_gelu_rare)
+
+// Rounding-tested forms (MFH_FUSION_PRECISE): mfh_<name>_cr(v, rare) returns
+// the f32 rounding of the reference's f64 value wherever it leaves `rare`
+// unset, at about half the instructions of the reference form.  It computes
+// the f64 value z as the forms above do (2^f by the degree-8 polynomial,
+// 2^-39.9; the reciprocal and one Newton step; the argument's own rounding
+// below 2^-45), within 2^-39.7 of the exact function, relative.  The
+// reference's f64 value (correctly rounded division, exp within 1 ulp) lies
+// within 2^-50 of it, and so does the reference form mfh_<name>_ref; gelu
+// adds the quantum of the reference's 1 - (1 - y) (below).  Two values that
+// close to each other round to the same f32 unless an f32 rounding midpoint
+// lies between them: z is flagged where its 29 bits below the f32 mantissa
+// lie within `margin` f64 ulps of the midpoint 2^28, with a margin of 2^15
+// f64 ulps, at least 2^-38 |z| (three times the distance allowed), so about
+// one element in 2^12 is flagged.  So are results that are not normal f32
+// numbers (the test assumes f32 keeps 23 bits above those 29) and arguments
+// outside a form's range.  Generated kernels recompute flagged elements with
+// the reference forms, so the results are the reference forms' everywhere.
+
+// True where a value within `margin` f64 ulps of z may round to another f32
+// than z does.  z must round to a normal f32 of magnitude above 2^-126.
+MFH_MATH bool mfh_near_f32_midpoint(double z, unsigned margin)
+{
+    const unsigned low = (unsigned)mfh_low_int(z) & 0x1fffffffu;
+    return low - (0x10000000u - margin) < 2u * margin;
+}
+
+// False for NaN, infinities, zeros, subnormals and 2^-126 itself, which an
+// f64 value below the normal range can round up to.  The tests here combine
+// with & and | rather than && and ||, which became one branch per element.
+MFH_MATH bool mfh_f32_normal_above_min(float r)
+{
+    const float a = mfh_absf(r);
+    return (a > 0x1p-126f) & (a <= 0x1.fffffep127f);
+}
+
+MFH_MATH float mfh_sigmoid_cr(float v, bool& rare)
+{
+    double den;
+    const double z = mfh_sigmoid_z(v, den);
+    const float r = (float)z;
+    rare |= !(v >= -708.0f) | !mfh_f32_normal_above_min(r) | mfh_near_f32_midpoint(z, 1u << 15);
+    return r;
+}
+
+MFH_MATH float mfh_silu_cr(float v, bool& rare)
+{
+    const float m = mfh_med3f(v, -708.0f, 800.0f);
+    double den;
+    const double z = mfh_silu_z(m, den);
+    const float r = (float)z;
+    rare |= (m != v) | !mfh_f32_normal_above_min(r) | mfh_near_f32_midpoint(z, 1u << 15);
+    return r;
+}
+
+// Where inner <= -0.625 the reference forms 1 + tanh as 1 - (1 - y),
+// y = 2 / (1 + E): y rounded to a multiple of 2^-53, at most 2^-54 from it,
+// which is (1 + E)/4 f64 ulps of z; and its tanh may stand up to 2^-53 off
+// there, another (1 + E)/2.  A margin of 2^15 + (1 + E) f64 ulps (at most
+// 2^15 + 2^23.4 inside the clamp) covers both, so z takes y as it is.  The
+// clamp is the fast form's, [-4.9, 1024]: every v it changes is flagged.
+MFH_MATH float mfh_gelu_cr(float v, bool& rare)
+{
+    const float c = mfh_med3f(v, -4.9f, 1024.0f);
+    double den;
+    const double z = mfh_gelu_z(c, den);
+    const float r = (float)z;
+    rare |= (c != v) | !mfh_f32_normal_above_min(r) | mfh_near_f32_midpoint(z, (1u << 15) + (unsigned)den);
+    return r;
+}
+
+// mfh_<name>_p(v): the rounding-tested form, or the reference form where it
+// sets its flag (the host accuracy sweep measures these).
+MFH_FAST_OR_REF(mfh_sigmoid_p, mfh_sigmoid_cr, mfh_sigmoid_rare)
+MFH_FAST_OR_REF(mfh_silu_p, mfh_silu_cr, mfh_silu_rare)
+MFH_FAST_OR_REF(mfh_gelu_p, mfh_gelu_cr, mfh_gelu_rare)
 #undef MFH_FAST_OR_REF
 
 MFH_MATH float mfh_exp_ref(float v) { return (float)mfh_exp_f64((double)v); }

@@ -85,7 +85,8 @@ int link(const std::vector<mfh_ast_node>& nodes, int idx, std::vector<int>& c0, 
 enum class Form {
     kFast,      // branch-free fast forms; each ORs the element's flag `qe`
     kFallback,  // the reference forms as real calls (recomputing flagged elements)
-    kPrecise,   // the reference forms inline (MFH_FUSION_PRECISE)
+    kRounded,   // the rounding-tested f64 forms; each ORs `qe` (MFH_FUSION_PRECISE)
+    kPrecise,   // the reference forms inline (MFH_FUSION_PRECISE | MFH_FUSION_NO_ROUNDING_TEST)
 };
 
 bool is_fast_activation(int type) { return type == kNodeSigmoid || type == kNodeSilu || type == kNodeGelu; }
@@ -206,6 +207,7 @@ struct Emitter {
         if (form == Form::kPrecise) return let(fn + "_ref(" + a + ")");
         if (form == Form::kFallback) return let(fn + "_rare(" + a + ")");
         flagged = true;
+        if (form == Form::kRounded) return let(fn + "_cr(" + a + ", qe)");
         const bool x = f64_forms && std::string(name) != "sigmoid";  // sigmoid's fast form is f64 already
         return let(fn + (x ? "_fast_x(" : "_fast(") + a + ", qe)");
     }
@@ -614,8 +616,12 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // MFH_FUSION_PRECISE each element runs the fast forms and the planned
     // cancellation guards, which set its flag `qe`; flagged elements are then
     // recomputed with the reference forms (real calls), so the item's main
-    // body has no branch.
-    const Form main_form = precise ? Form::kPrecise : Form::kFast;
+    // body has no branch.  With it the rounding-tested forms set the flag
+    // instead (no guards: their results are the reference's), or, with
+    // MFH_FUSION_NO_ROUNDING_TEST, every element runs the reference forms.
+    const Form main_form = !precise                                   ? Form::kFast
+                           : (flags & MFH_FUSION_NO_ROUNDING_TEST) != 0 ? Form::kPrecise
+                                                                       : Form::kRounded;
     const std::vector<Guard> guards = plan_guards(list, c0, c1, out_dtype, precise);
     std::vector<bool> packed16(n_inputs, false);
     for (int k = 0; k < n_inputs; k++)

@@ -152,9 +152,15 @@ def test_emit_hip_broadcast_operands():
     assert "8 elements per item, 1 item(s) per thread" in src
     sig = M.FusedKernel(flatten((N_SIGMOID, ("in", 0))), [(M.FLOAT16, M.OPERAND_FULL, 0)], M.FLOAT16, "sig")
     assert "8 elements per item, 2 item(s) per thread" in sig.source
+    # precise: the rounding-tested form, the reference form for the elements it
+    # flags, and no cancellation guard (its results are the reference's)
     precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)
-    assert "mfh_gelu_ref(" in precise.source and "_fast(" not in precise.source.split("EmitHIP")[1]
-    assert "qe" not in precise.source and "1 item(s) per thread" in precise.source
+    body = precise.source.split("EmitHIP")[1]
+    assert body.count("mfh_gelu_cr(t1, qe)") == 2 and body.count("mfh_gelu_rare(f1)") == 2
+    assert "_fast(" not in body and "qe |=" not in body and "1 item(s) per thread" in precise.source
+    plain = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE | M.FUSION_NO_ROUNDING_TEST)
+    body = plain.source.split("EmitHIP")[1]
+    assert "mfh_gelu_ref(t1)" in body and "_cr(" not in body and "qe" not in body
 
 
 def guard_lines(src):

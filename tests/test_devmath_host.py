@@ -10,6 +10,9 @@ is checked against the oracle's restatement of codegen/cpu.go:186-200:
 Sigmoid, Exp, Log, Tanh within 1 f32 ulp, Silu and Gelu within 2 (within 1
 in the f64 forms that chains streaming f32 use), the
 MFH_FUSION_PRECISE forms within 1, NaN exactly where the reference's is.
+The rounding-tested forms that MFH_FUSION_PRECISE kernels run (mfh_*_cr, the
+reference form where they flag an input) must give the reference forms' bit
+patterns on every swept input.
 """
 import os
 import re
@@ -36,7 +39,7 @@ def report(tmp_path_factory):
 
 
 TOL = {"sigmoid": 1, "silu": 2, "gelu": 2, "silu_x": 1, "gelu_x": 1, "exp_ref": 1, "log_ref": 1, "tanh_ref": 1,
-       "sigmoid_ref": 1, "silu_ref": 1, "gelu_ref": 1}
+       "sigmoid_ref": 1, "silu_ref": 1, "gelu_ref": 1, "sigmoid_p": 1, "silu_p": 1, "gelu_p": 1}
 
 
 @pytest.mark.parametrize("name", sorted(TOL))
@@ -47,3 +50,16 @@ def test_activation_accuracy(report, name):
     assert row["over_tol"] == 0 and row["max_ulp"] <= TOL[name], row
     # the fast forms are mostly exact; the f64 reference forms almost always
     assert row["exact"] > (0.95 if TOL[name] == 2 else 0.98), row
+
+
+@pytest.mark.parametrize("name", ["sigmoid_p", "silu_p", "gelu_p"])
+def test_rounding_tested_forms_reproduce_the_reference_forms(report, name):
+    row = report[name]
+    assert row["ref_mismatch"] == 0, row
+    # The margin of the rounding test, 2^15 f64 ulps, is at least 2^-38 of the
+    # value: the f64 value must stay well within it of the exact function
+    # (the device's reciprocal adds at most 2^-46 after its Newton step).
+    assert row["max_rel_err_log2"] < -39.5, row
+    # flagged over all bit patterns: mostly the range tests (tiny, huge and
+    # NaN inputs); on data the midpoint test flags about one element in 2^13
+    assert row["flagged"] < 0.5, row

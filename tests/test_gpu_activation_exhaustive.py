@@ -108,3 +108,32 @@ def test_precise_forms_against_the_oracle(node):
     d = np.abs(ulp_key(got[~nan_w]) - ulp_key(want[~nan_w]))
     log(f"node {node}: precise form vs oracle: max {int(d.max())} ulp, {float(np.mean(d == 0)):.7f} identical")
     assert d.max() <= 1 and np.mean(d == 0) > 0.9999, f"node {node}: max {int(d.max())} ulp"
+
+
+@pytest.mark.parametrize("node", [O.N_SIGMOID, O.N_SILU, O.N_GELU])
+def test_precise_rounding_test_reproduces_the_reference_forms(node):
+    # MFH_FUSION_PRECISE kernels run the rounding-tested f64 forms and the
+    # reference forms only where the test flags an element; with
+    # MFH_FUSION_NO_ROUNDING_TEST every element runs the reference forms.  The
+    # two must give the same bit pattern for every f32 input, NaN payloads
+    # included: that checks the test's margin against the device's own
+    # arithmetic (its f64 reciprocal among it) on every input.
+    import torch
+    M.init(0)
+    nodes = O.flatten((node, ("in", 0)))
+    ops = [(M.FLOAT32, M.OPERAND_FULL, 0)]
+    tested = M.FusedKernel(nodes, ops, M.FLOAT32, f"exh_tested_{node}", M.FUSION_PRECISE)
+    plain = M.FusedKernel(nodes, ops, M.FLOAT32, f"exh_plain_{node}", M.FUSION_PRECISE | M.FUSION_NO_ROUNDING_TEST)
+    a = torch.empty(CHUNK, dtype=torch.int32, device="cuda")
+    b = torch.empty(CHUNK, dtype=torch.int32, device="cuda")
+    for c in range((1 << 32) // CHUNK):
+        log(f"node {node} rounding test: bit patterns [{c * CHUNK:#x}, {(c + 1) * CHUNK:#x})")
+        x = (torch.arange(c * CHUNK, (c + 1) * CHUNK, dtype=torch.int64, device="cuda") - (1 << 31)).to(torch.int32)
+        tested.launch([x.data_ptr()], a.data_ptr(), CHUNK, stream())
+        plain.launch([x.data_ptr()], b.data_ptr(), CHUNK, stream())
+        idx = torch.nonzero(a != b).flatten()
+        if idx.numel():
+            i = idx[:4].cpu().tolist()
+            raise AssertionError(f"node {node}: {idx.numel()} inputs differ in chunk {c}, e.g. x bits "
+                                 f"{[int(x[j]) & 0xFFFFFFFF for j in i]}: tested {[int(a[j]) & 0xFFFFFFFF for j in i]}"
+                                 f" plain {[int(b[j]) & 0xFFFFFFFF for j in i]}")
