@@ -586,20 +586,24 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // dispatch order).  Measured on MI355X against grid-stride loops at 4-24
     // blocks per CU: +11% on the SwiGLU chain and +9% on the f16 gelu chain;
     // a no-compute 2:1 read:write stream gains 17% the same way.  One item per
-    // thread, except where the fast element math is mostly f64 (Sigmoid): two
-    // items per thread give a sigmoid chain 0-3%, while SwiGLU, Silu, add/mul
-    // chains and (since its 2^f runs on v_exp_f32) the gelu chain lose 2-6%
-    // and the precise (f64 library) forms gain nothing.  Workgroups of one
-    // wave (kFusedThreads).  mfh_set_launch_config("fused", ...) and
-    // mfh_set_launch_threads("fused", ...) override these.
+    // thread, except where the element math is mostly f64 (Sigmoid, the f64
+    // forms of chains that stream f32, the rounding-tested forms of
+    // MFH_FUSION_PRECISE): two items per thread give a sigmoid chain 0-3% and
+    // the precise SwiGLU chain 5.6% (the precise gelu chain -1%, within the
+    // noise of six alternating runs), while SwiGLU, Silu, add/mul chains and
+    // (since its 2^f runs on v_exp_f32) the gelu chain lose 2-6% and the
+    // reference forms inline (MFH_FUSION_NO_ROUNDING_TEST) gain nothing.
+    // Workgroups of one wave (kFusedThreads).  mfh_set_launch_config("fused",
+    // ...) and mfh_set_launch_threads("fused", ...) override these.
     // Chains that stream f32 take Silu and Gelu in f64 forms: their results
     // show every f32 ulp of the node, and their 4-byte elements leave room
     // for about twice the instructions (MFH_FUSION_SHORT_QUOTIENT keeps the
     // 16-bit chains' forms).
     const bool f64_forms = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
+    const bool rounded = precise && (flags & MFH_FUSION_NO_ROUNDING_TEST) == 0;
     bool f64_fast = false;
     for (const mfh_ast_node& node : list)
-        if (!precise && (node.type == kNodeSigmoid || (f64_forms && (node.type == kNodeSilu || node.type == kNodeGelu))))
+        if (is_fast_activation(node.type) && (rounded || (!precise && (node.type == kNodeSigmoid || f64_forms))))
             f64_fast = true;
     const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : f64_fast ? 2 : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
@@ -619,9 +623,7 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // body has no branch.  With it the rounding-tested forms set the flag
     // instead (no guards: their results are the reference's), or, with
     // MFH_FUSION_NO_ROUNDING_TEST, every element runs the reference forms.
-    const Form main_form = !precise                                   ? Form::kFast
-                           : (flags & MFH_FUSION_NO_ROUNDING_TEST) != 0 ? Form::kPrecise
-                                                                       : Form::kRounded;
+    const Form main_form = !precise ? Form::kFast : rounded ? Form::kRounded : Form::kPrecise;
     const std::vector<Guard> guards = plan_guards(list, c0, c1, out_dtype, precise);
     std::vector<bool> packed16(n_inputs, false);
     for (int k = 0; k < n_inputs; k++)

@@ -157,10 +157,11 @@ def test_emit_hip_broadcast_operands():
     precise = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE)
     body = precise.source.split("EmitHIP")[1]
     assert body.count("mfh_gelu_cr(t1, qe)") == 2 and body.count("mfh_gelu_rare(f1)") == 2
-    assert "_fast(" not in body and "qe |=" not in body and "1 item(s) per thread" in precise.source
+    assert "_fast(" not in body and "qe |=" not in body and "2 item(s) per thread" in precise.source
     plain = M.FusedKernel(nodes, ops, M.FLOAT16, "chain", flags=M.FUSION_PRECISE | M.FUSION_NO_ROUNDING_TEST)
     body = plain.source.split("EmitHIP")[1]
     assert "mfh_gelu_ref(t1)" in body and "_cr(" not in body and "qe" not in body
+    assert "1 item(s) per thread" in plain.source
 
 
 def guard_lines(src):
