@@ -7,7 +7,8 @@
 // Reference semantics (codegen/cpu.go:186-200): Sigmoid, Silu and Gelu are
 // evaluated in f64 and rounded once to f32.  The fast forms below compute in
 // f32 with error-free corrections and stay within 2 f32 ulps of that; the
-// MFH_FUSION_PRECISE forms (mfh_*_ref) restate the f64 formulas.
+// reference forms (mfh_*_ref) restate the f64 formulas, and the
+// rounding-tested forms (mfh_*_cr) give their results at lower cost.
 //
 //   e^a:          a log2(e) = k + f, |f| <= 1/2, with k from the
 //                 round-to-integer constant 1.5 * 2^23 and f formed with
