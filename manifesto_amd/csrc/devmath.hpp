@@ -328,31 +328,10 @@ MFH_MATH float mfh_gelu_fast_x(float v, bool& rare)
     return (float)mfh_gelu_z(c, den);
 }
 
-// mfh_<name>_rare: the reference form as a real call (MFH_RARE), which the
-// generated kernels use to recompute flagged elements.  mfh_<name>(v): the
-// fast form, or the reference form where the fast one sets its flag (the
-// host accuracy sweep measures these).
-#define MFH_FAST_OR_REF(name, fast, ref)                                \
-    MFH_MATH float name(float v)                                        \
-    {                                                                   \
-        bool rare = false;                                              \
-        float s = fast(v, rare);                                        \
-        MFH_KEEP(s);                                                    \
-        if (rare) s = ref(v);                                           \
-        return s;                                                       \
-    }
-MFH_RARE float mfh_sigmoid_rare(float v) { return mfh_sigmoid_ref(v); }
-MFH_RARE float mfh_silu_rare(float v) { return mfh_silu_ref(v); }
-MFH_RARE float mfh_gelu_rare(float v) { return mfh_gelu_ref(v); }
-MFH_FAST_OR_REF(mfh_sigmoid, mfh_sigmoid_fast, mfh_sigmoid_rare)
-MFH_FAST_OR_REF(mfh_silu, mfh_silu_fast, mfh_silu_rare)
-MFH_FAST_OR_REF(mfh_silu_x, mfh_silu_fast_x, mfh_silu_rare)
-MFH_FAST_OR_REF(mfh_gelu, mfh_gelu_fast, mfh_gelu_rare)
-MFH_FAST_OR_REF(mfh_gelu_x, mfh_gelu_fast_x, mfh_gelu_rare)
-
-// Rounding-tested forms (MFH_FUSION_PRECISE): mfh_<name>_cr(v, rare) returns
-// the f32 rounding of the reference's f64 value wherever it leaves `rare`
-// unset, at about half the instructions of the reference form.  It computes
+// Rounding-tested forms (MFH_FUSION_PRECISE kernels, and the recomputation
+// of flagged elements below): mfh_<name>_cr(v, rare) returns the f32 rounding
+// of the reference's f64 value wherever it leaves `rare` unset, at about two
+// thirds of the instructions of the reference form.  It computes
 // the f64 value z as the forms above do (2^f by the degree-8 polynomial,
 // 2^-39.9; the reciprocal and one Newton step; the argument's own rounding
 // below 2^-45), within 2^-39.7 of the exact function, relative.  The
@@ -420,11 +399,47 @@ MFH_MATH float mfh_gelu_cr(float v, bool& rare)
     return r;
 }
 
+// mfh_<name>_rare: the reference's result as a real call (MFH_RARE), which
+// the generated kernels use to recompute flagged elements: the
+// rounding-tested form above, and the reference form where that one flags the
+// input too (a guard's recomputation in the f16 gelu chain: 49 VALU
+// instructions where the test decides, 18 of them moves of the polynomial's
+// constants, against 67 for the reference form).  mfh_<name>(v): the fast
+// form, or that result where the fast one sets its flag (the host accuracy
+// sweep measures these).
+#define MFH_FAST_OR_REF(name, fast, ref)                                \
+    MFH_MATH float name(float v)                                        \
+    {                                                                   \
+        bool rare = false;                                              \
+        float s = fast(v, rare);                                        \
+        MFH_KEEP(s);                                                    \
+        if (rare) s = ref(v);                                           \
+        return s;                                                       \
+    }
+#define MFH_RARE_FORM(name)                                             \
+    MFH_RARE float mfh_##name##_rare(float v)                           \
+    {                                                                   \
+        bool rare = false;                                              \
+        float s = mfh_##name##_cr(v, rare);                             \
+        MFH_KEEP(s);                                                    \
+        if (rare) s = mfh_##name##_ref(v);                              \
+        return s;                                                       \
+    }
+MFH_RARE_FORM(sigmoid)
+MFH_RARE_FORM(silu)
+MFH_RARE_FORM(gelu)
+#undef MFH_RARE_FORM
+MFH_FAST_OR_REF(mfh_sigmoid, mfh_sigmoid_fast, mfh_sigmoid_rare)
+MFH_FAST_OR_REF(mfh_silu, mfh_silu_fast, mfh_silu_rare)
+MFH_FAST_OR_REF(mfh_silu_x, mfh_silu_fast_x, mfh_silu_rare)
+MFH_FAST_OR_REF(mfh_gelu, mfh_gelu_fast, mfh_gelu_rare)
+MFH_FAST_OR_REF(mfh_gelu_x, mfh_gelu_fast_x, mfh_gelu_rare)
+
 // mfh_<name>_p(v): the rounding-tested form, or the reference form where it
 // sets its flag (the host accuracy sweep measures these).
-MFH_FAST_OR_REF(mfh_sigmoid_p, mfh_sigmoid_cr, mfh_sigmoid_rare)
-MFH_FAST_OR_REF(mfh_silu_p, mfh_silu_cr, mfh_silu_rare)
-MFH_FAST_OR_REF(mfh_gelu_p, mfh_gelu_cr, mfh_gelu_rare)
+MFH_FAST_OR_REF(mfh_sigmoid_p, mfh_sigmoid_cr, mfh_sigmoid_ref)
+MFH_FAST_OR_REF(mfh_silu_p, mfh_silu_cr, mfh_silu_ref)
+MFH_FAST_OR_REF(mfh_gelu_p, mfh_gelu_cr, mfh_gelu_ref)
 #undef MFH_FAST_OR_REF
 
 MFH_MATH float mfh_exp_ref(float v) { return (float)mfh_exp_f64((double)v); }
