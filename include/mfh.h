@@ -207,13 +207,14 @@ typedef struct {
  * are recomputed with the reference's formulas. */
 #define MFH_FUSION_PRECISE 1u
 
-/* Silu and Gelu in their f32 fast forms in every chain (the forms chains of
- * 16-bit operands always use: the rounding of 1 + E left in the quotient,
- * within the 2-ulp node budget).  Without it a chain that streams f32 (an f32
- * output or a full or periodic f32 operand) evaluates them in f64, about
- * twice the instructions, since its results show every f32 ulp of the node.
- * For measuring the 16-bit chains' forms over f32 results; no counterpart in
- * the reference. */
+/* Sigmoid, Silu and Gelu in the fast forms of chains of 16-bit operands in
+ * every chain (Silu and Gelu in f32 with the rounding of 1 + E left in the
+ * quotient, within the 2-ulp node budget; Sigmoid in f64 within 1 ulp).
+ * Without it a chain that streams f32 (an f32 output or a full or periodic
+ * f32 operand), whose results show every f32 ulp of the node, evaluates them
+ * as MFH_FUSION_PRECISE does, the reference's values at about twice the
+ * instructions.  For measuring the 16-bit chains' forms over f32 results; no
+ * counterpart in the reference. */
 #define MFH_FUSION_SHORT_QUOTIENT 2u
 
 /* With MFH_FUSION_PRECISE: every element through the reference's formulas,

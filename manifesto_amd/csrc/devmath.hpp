@@ -253,29 +253,17 @@ MFH_MATH float mfh_silu_fast(float v, bool& rare)
     return mfh_div_one_plus(v, mfh_exp_neg(m));
 }
 
-// silu for chains that stream f32 (their results show every f32 ulp of the
-// node): the whole computation in f64, as the fast sigmoid makes it, e^-v =
-// 2^t by the round-to-integer reduction and the degree-8 polynomial
-// (2^-39.9), the reciprocal of 1 + e^-v plus one Newton step, times v, one
-// rounding.  The f32 result is the reference's except where the exact value
-// lies within about 2^-39 of an f32 rounding boundary.  Every v the clamp to
-// [-708, 800] changes (and NaN) takes the reference's form.  About twice
-// the instructions of mfh_silu_fast, which the 4-byte elements of such a
-// chain leave room for.  mfh_silu_z is the f64 value for m = v inside the
-// clamp.
+// silu in f64 for the rounding-tested form below (chains that stream f32,
+// whose results show every f32 ulp of the node, and MFH_FUSION_PRECISE), as
+// the fast sigmoid makes it: e^-v = 2^t by the round-to-integer reduction and
+// the degree-8 polynomial (2^-39.9), the reciprocal of 1 + e^-v plus one
+// Newton step, times v.  mfh_silu_z is that f64 value for m = v inside the
+// clamp [-708, 800], and sets den = 1 + e^-v.
 MFH_MATH double mfh_silu_z(float m, double& den)
 {
     const double x = (double)m;
     den = mfh_one_plus_2exp(x * -MFH_LOG2E_D);
     return x * mfh_recip_newton(den);
-}
-
-MFH_MATH float mfh_silu_fast_x(float v, bool& rare)
-{
-    const float m = mfh_med3f(v, -708.0f, 800.0f);
-    rare |= m != v;
-    double den;
-    return (float)mfh_silu_z(m, den);
 }
 
 // Fast gelu = v / (1 + E), E = e^(-2 inner) = 2^t with
@@ -310,9 +298,10 @@ MFH_MATH float mfh_gelu_fast(float v, bool& rare)
     return mfh_div_one_plus(v, mfh_gelu_e(c));
 }
 
-// gelu for chains that stream f32: the same argument t = d w in f64, then
-// 2^t, the quotient and the product with v in f64 as mfh_silu_fast_x makes
-// them, one rounding.  mfh_gelu_z is that f64 value for c inside the clamp.
+// gelu in f64 for the rounding-tested form below: the same argument t = d w
+// in f64, then 2^t, the quotient and the product with v in f64 as
+// mfh_silu_z makes them.  mfh_gelu_z is that f64 value for c inside the fast
+// form's clamp, and sets den = 1 + E.
 MFH_MATH double mfh_gelu_z(float c, double& den)
 {
     const double d = (double)c;
@@ -320,16 +309,9 @@ MFH_MATH double mfh_gelu_z(float c, double& den)
     return d * mfh_recip_newton(den);
 }
 
-MFH_MATH float mfh_gelu_fast_x(float v, bool& rare)
-{
-    const float c = mfh_med3f(v, -4.9f, 1024.0f);
-    rare |= c != v;
-    double den;
-    return (float)mfh_gelu_z(c, den);
-}
-
-// Rounding-tested forms (MFH_FUSION_PRECISE kernels, and the recomputation
-// of flagged elements below): mfh_<name>_cr(v, rare) returns the f32 rounding
+// Rounding-tested forms (chains that stream f32, MFH_FUSION_PRECISE kernels,
+// and the recomputation of flagged elements below): mfh_<name>_cr(v, rare)
+// returns the f32 rounding
 // of the reference's f64 value wherever it leaves `rare` unset, at about two
 // thirds of the instructions of the reference form.  It computes
 // the f64 value z as the forms above do (2^f by the degree-8 polynomial,
@@ -431,9 +413,7 @@ MFH_RARE_FORM(gelu)
 #undef MFH_RARE_FORM
 MFH_FAST_OR_REF(mfh_sigmoid, mfh_sigmoid_fast, mfh_sigmoid_rare)
 MFH_FAST_OR_REF(mfh_silu, mfh_silu_fast, mfh_silu_rare)
-MFH_FAST_OR_REF(mfh_silu_x, mfh_silu_fast_x, mfh_silu_rare)
 MFH_FAST_OR_REF(mfh_gelu, mfh_gelu_fast, mfh_gelu_rare)
-MFH_FAST_OR_REF(mfh_gelu_x, mfh_gelu_fast_x, mfh_gelu_rare)
 
 // mfh_<name>_p(v): the rounding-tested form, or the reference form where it
 // sets its flag (the host accuracy sweep measures these).

@@ -85,7 +85,7 @@ int link(const std::vector<mfh_ast_node>& nodes, int idx, std::vector<int>& c0, 
 enum class Form {
     kFast,      // branch-free fast forms; each ORs the element's flag `qe`
     kFallback,  // the reference forms as real calls (recomputing flagged elements)
-    kRounded,   // the rounding-tested f64 forms; each ORs `qe` (MFH_FUSION_PRECISE)
+    kRounded,   // the rounding-tested f64 forms; each ORs `qe` (chains that stream f32, MFH_FUSION_PRECISE)
     kPrecise,   // the reference forms inline (MFH_FUSION_PRECISE | MFH_FUSION_NO_ROUNDING_TEST)
 };
 
@@ -114,19 +114,21 @@ bool is_transcendental(int type)
 // difference is under 2^-25).  The guarantee is made where the activation
 // reaches the output through exactly one Add/Sub and no other transcendental
 // node (the BASELINE chains); other paths keep the node-envelope contract.
-// f32 outputs carry every f32 ulp of the node, so they take no guard.
+// f32 outputs carry every f32 ulp of the node, so they take no guard; nor do
+// chains whose activations take the reference's values (`exact`: the
+// rounding-tested and reference forms).
 struct Guard {
     int factor = 0;  // flag when |s| factor < M; 0 = no guard
     bool lhs = false, rhs = false;  // which operands carry an activation's error (M = the max of those)
 };
 
 std::vector<Guard> plan_guards(const std::vector<mfh_ast_node>& nodes, const std::vector<int>& c0,
-                               const std::vector<int>& c1, uint8_t out_dtype, bool precise)
+                               const std::vector<int>& c1, uint8_t out_dtype, bool exact)
 {
     const int n = (int)nodes.size();
     std::vector<Guard> guards(n);
     const int mantissa = out_dtype == kFloat16 ? 10 : out_dtype == kBFloat16 ? 7 : 0;
-    if (precise || mantissa == 0) return guards;
+    if (exact || mantissa == 0) return guards;
     std::vector<int> parent(n, -1);
     for (int i = 0; i < n; i++) {
         if (c0[i] >= 0) parent[c0[i]] = i;
@@ -179,8 +181,6 @@ struct Emitter {
     const std::vector<int>& c0;
     const std::vector<int>& c1;
     Form form;
-    // Silu and Gelu in their f64 forms (mfh_*_fast_x): chains that stream f32.
-    bool f64_forms = false;
     const std::vector<Guard>* guards = nullptr;  // kFast only
     std::string prefix = "t";
     // Vector loop only: inputs held as packed f16 words w<k>[u][j >> 1]
@@ -207,9 +207,7 @@ struct Emitter {
         if (form == Form::kPrecise) return let(fn + "_ref(" + a + ")");
         if (form == Form::kFallback) return let(fn + "_rare(" + a + ")");
         flagged = true;
-        if (form == Form::kRounded) return let(fn + "_cr(" + a + ", qe)");
-        const bool x = f64_forms && std::string(name) != "sigmoid";  // sigmoid's fast form is f64 already
-        return let(fn + (x ? "_fast_x(" : "_fast(") + a + ", qe)");
+        return let(fn + (form == Form::kRounded ? "_cr(" : "_fast(") + a + ", qe)");
     }
 
     // s = a + b (or a - b): the cancellation guard of node idx, if planned.
@@ -595,15 +593,18 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // reference forms inline (MFH_FUSION_NO_ROUNDING_TEST) gain nothing.
     // Workgroups of one wave (kFusedThreads).  mfh_set_launch_config("fused",
     // ...) and mfh_set_launch_threads("fused", ...) override these.
-    // Chains that stream f32 take Silu and Gelu in f64 forms: their results
-    // show every f32 ulp of the node, and their 4-byte elements leave room
-    // for about twice the instructions (MFH_FUSION_SHORT_QUOTIENT keeps the
-    // 16-bit chains' forms).
-    const bool f64_forms = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
-    const bool rounded = precise && (flags & MFH_FUSION_NO_ROUNDING_TEST) == 0;
+    // Chains that stream f32 (an f32 output or a full or periodic f32
+    // operand) show every f32 ulp of their activations: they take the
+    // rounding-tested forms, whose results are the reference's, at about
+    // twice the instructions of the f32 forms, which their 4-byte elements
+    // leave room for (MFH_FUSION_SHORT_QUOTIENT keeps the 16-bit chains'
+    // forms).  So do MFH_FUSION_PRECISE kernels unless
+    // MFH_FUSION_NO_ROUNDING_TEST asks for the reference forms inline.
+    const bool streams_f32 = vec == 4 && (flags & MFH_FUSION_SHORT_QUOTIENT) == 0;
+    const bool rounded = precise ? (flags & MFH_FUSION_NO_ROUNDING_TEST) == 0 : streams_f32;
     bool f64_fast = false;
     for (const mfh_ast_node& node : list)
-        if (is_fast_activation(node.type) && (rounded || (!precise && (node.type == kNodeSigmoid || f64_forms))))
+        if (is_fast_activation(node.type) && (rounded || (!precise && node.type == kNodeSigmoid)))
             f64_fast = true;
     const int unroll = items_per_thread(Kern::kFused) > 0 ? items_per_thread(Kern::kFused) : f64_fast ? 2 : 1;
     const int auto_bpc = kOneShotBlocksPerCu;
@@ -620,21 +621,21 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // MFH_FUSION_PRECISE each element runs the fast forms and the planned
     // cancellation guards, which set its flag `qe`; flagged elements are then
     // recomputed with the reference forms (real calls), so the item's main
-    // body has no branch.  With it the rounding-tested forms set the flag
-    // instead (no guards: their results are the reference's), or, with
-    // MFH_FUSION_NO_ROUNDING_TEST, every element runs the reference forms.
-    const Form main_form = !precise ? Form::kFast : rounded ? Form::kRounded : Form::kPrecise;
-    const std::vector<Guard> guards = plan_guards(list, c0, c1, out_dtype, precise);
+    // body has no branch.  The rounding-tested forms set the flag instead (no
+    // guards: their results are the reference's); with
+    // MFH_FUSION_NO_ROUNDING_TEST every element runs the reference forms.
+    const Form main_form = rounded ? Form::kRounded : precise ? Form::kPrecise : Form::kFast;
+    const std::vector<Guard> guards = plan_guards(list, c0, c1, out_dtype, main_form != Form::kFast);
     std::vector<bool> packed16(n_inputs, false);
     for (int k = 0; k < n_inputs; k++)
         packed16[k] = inputs[k].mode != MFH_OPERAND_SCALAR && inputs[k].dtype == kFloat16;
-    Emitter em{list, c0, c1, main_form, f64_forms, &guards};
+    Emitter em{list, c0, c1, main_form, &guards};
     const std::string result = em.emit(0);
-    Emitter emf{list, c0, c1, Form::kFallback, f64_forms, nullptr, "f"};
+    Emitter emf{list, c0, c1, Form::kFallback, nullptr, "f"};
     const std::string fresult = em.flagged ? emf.emit(0) : "";
-    Emitter emv{list, c0, c1, main_form, f64_forms, &guards, "t", packed16};
+    Emitter emv{list, c0, c1, main_form, &guards, "t", packed16};
     const std::string vresult = emv.emit(0);
-    Emitter emvf{list, c0, c1, Form::kFallback, f64_forms, nullptr, "f", packed16};
+    Emitter emvf{list, c0, c1, Form::kFallback, nullptr, "f", packed16};
     const std::string vfresult = emv.flagged ? emvf.emit(0) : "";
 
     std::string identifier = output_port && *output_port ? output_port : "anon";

@@ -79,7 +79,6 @@ int main(int argc, char** argv)
     const int threads = argc > 2 ? std::atoi(argv[2]) : 4;
     const Fn fns[] = {
         {"sigmoid", 15, mfh_sigmoid, 1}, {"silu", 17, mfh_silu, 2}, {"gelu", 18, mfh_gelu, 2},
-        {"silu_x", 17, mfh_silu_x, 2}, {"gelu_x", 18, mfh_gelu_x, 2},
         {"exp_ref", 12, mfh_exp_ref, 1}, {"log_ref", 13, mfh_log_ref, 1}, {"tanh_ref", 16, mfh_tanh_ref, 1},
         {"sigmoid_ref", 15, mfh_sigmoid_ref, 1}, {"silu_ref", 17, mfh_silu_ref, 1}, {"gelu_ref", 18, mfh_gelu_ref, 1},
         {"sigmoid_p", 15, mfh_sigmoid_p, 1, mfh_sigmoid_cr, mfh_sigmoid_ref, sigmoid_z, sigmoid_exact},

@@ -204,24 +204,31 @@ def test_cancellation_guard_counts_the_error_on_its_operands():
     assert guard_lines(k.source) == []
 
 
-def test_chains_that_stream_f32_take_the_f64_forms():
+def test_chains_that_stream_f32_take_the_rounding_tested_forms():
+    # An f32 output or a full or periodic f32 operand: every activation ulp
+    # shows, so Sigmoid, Silu and Gelu take the rounding-tested forms (the
+    # reference's values), with no cancellation guard and two items per thread.
     silu = flatten((N_MUL, (N_SILU, ("in", 0)), ("in", 1)))
     gelu = flatten((N_GELU, ("in", 0)))
     bf, f32 = (M.BFLOAT16, M.OPERAND_FULL, 0), (M.FLOAT32, M.OPERAND_FULL, 0)
     assert "mfh_silu_fast(x0, qe)" in M.FusedKernel(silu, [bf, bf], M.BFLOAT16, "s16").source
-    assert "mfh_silu_fast_x(x0, qe)" in M.FusedKernel(silu, [bf, bf], M.FLOAT32, "s32").source
-    assert "mfh_silu_fast_x(x0, qe)" in M.FusedKernel(silu, [f32, bf], M.BFLOAT16, "s32i").source
+    assert "mfh_silu_cr(x0, qe)" in M.FusedKernel(silu, [bf, bf], M.FLOAT32, "s32").source
+    assert "mfh_silu_cr(x0, qe)" in M.FusedKernel(silu, [f32, bf], M.BFLOAT16, "s32i").source
     # a scalar f32 operand does not make the chain stream f32
     assert "mfh_silu_fast(x0, qe)" in M.FusedKernel(silu, [bf, (M.FLOAT32, M.OPERAND_SCALAR, 0)],
                                                     M.BFLOAT16, "ss").source
-    assert "mfh_gelu_fast_x(x0, qe)" in M.FusedKernel(gelu, [f32], M.FLOAT32, "g32").source
+    assert "mfh_gelu_cr(x0, qe)" in M.FusedKernel(gelu, [f32], M.FLOAT32, "g32").source
     short = M.FusedKernel(gelu, [f32], M.FLOAT32, "g32s", flags=M.FUSION_SHORT_QUOTIENT)
     assert "mfh_gelu_fast(x0, qe)" in short.source
-    # sigmoid's fast form is f64 either way; f64 forms take two items per thread
     sig = M.FusedKernel(flatten((N_SIGMOID, ("in", 0))), [f32], M.FLOAT32, "sg")
-    assert "mfh_sigmoid_fast(x0, qe)" in sig.source and "2 item(s) per thread" in sig.source
+    assert "mfh_sigmoid_cr(x0, qe)" in sig.source and "2 item(s) per thread" in sig.source
     assert "2 item(s) per thread" in M.FusedKernel(gelu, [f32], M.FLOAT32, "g32u").source
     assert "1 item(s) per thread" in short.source
+    # f32 operand, bf16 output: exact activations need no guard; the 16-bit
+    # chain's fast form does
+    add = flatten((N_ADD, (N_GELU, ("in", 0)), ("in", 1)))
+    assert guard_lines(M.FusedKernel(add, [f32, bf], M.BFLOAT16, "ga32").source) == []
+    assert guard_lines(M.FusedKernel(add, [bf, bf], M.BFLOAT16, "ga16").source) != []
 
 
 def test_emit_hip_item_width_follows_the_widest_operand():

@@ -1,18 +1,20 @@
-"""Every f32 input through the device's fast Sigmoid, Silu and Gelu nodes.
+"""Every f32 input through the device's Sigmoid, Silu and Gelu nodes.
 
-The fast forms run on the GPU over all 2^32 f32 bit patterns (in chunks)
-beside the MFH_FUSION_PRECISE forms.  An f32 chain evaluates Silu and Gelu
-in f64; the f32 forms 16-bit chains use (the rounding of 1 + E left in the
-quotient) run here through MFH_FUSION_SHORT_QUOTIENT, so both are measured
-over every f32 input.  The precise forms, which restate the
-reference's f64 formulas (codegen/cpu.go:186-200) and round once, are within
-one f32 ulp of the oracle (they differ only where an f64 result sits at an f32
-rounding tie that two f64 libraries round differently).  NaN positions must
-match.  Every input where the fast form is `tol` or more ulps from the
-precise form is then checked against the CPU oracle itself, which it must be
-within `tol` of; every other input is within tol - 1 of the precise form and
-so within tol of the oracle.  This covers the device math the host sweep
-(test_devmath_host.py) cannot model: the hardware reciprocal, and gelu's
+The fused kernels run on the GPU over all 2^32 f32 bit patterns (in chunks)
+beside the MFH_FUSION_PRECISE kernels.  A chain that streams f32 evaluates
+the three activations in their rounding-tested forms, which must give the
+precise kernel's bit pattern on every input.  The forms 16-bit chains use
+(f32 Silu and Gelu with the rounding of 1 + E left in the quotient, the f64
+Sigmoid without a rounding test) run here through MFH_FUSION_SHORT_QUOTIENT.
+The precise kernels, which give the reference's f64 formulas
+(codegen/cpu.go:186-200) rounded once, are within one f32 ulp of the oracle
+(they differ only where an f64 result sits at an f32 rounding tie that two
+f64 libraries round differently).  NaN positions must match.  Every input
+where a 16-bit chain's form is `tol` or more ulps from the precise kernel is
+then checked against the CPU oracle itself, which it must be within `tol`
+of; every other input is within tol - 1 of the precise kernel and so within
+tol of the oracle.  This covers the device math the host sweep
+(test_devmath_host.py) cannot model: the hardware reciprocals, and gelu's
 hardware v_exp_f32.
 """
 import numpy as np
@@ -39,8 +41,8 @@ def ulp_key(bits):
     return torch.where(b < 0, -(b & 0x7FFFFFFF), b)
 
 
-CASES = [(O.N_SIGMOID, 0), (O.N_SILU, 0), (O.N_SILU, M.FUSION_SHORT_QUOTIENT), (O.N_GELU, 0),
-         (O.N_GELU, M.FUSION_SHORT_QUOTIENT)]
+CASES = [(O.N_SIGMOID, 0), (O.N_SIGMOID, M.FUSION_SHORT_QUOTIENT), (O.N_SILU, 0), (O.N_SILU, M.FUSION_SHORT_QUOTIENT),
+         (O.N_GELU, 0), (O.N_GELU, M.FUSION_SHORT_QUOTIENT)]
 
 
 @pytest.mark.parametrize("node, flags", CASES)
@@ -74,6 +76,8 @@ def test_fast_activation_every_f32_input(node, flags):
     h = hist.tolist()
     log(f"node {node} flags {flags}: ulps from the precise form {h} (last bin: {tol + 2} or more)")
     assert sum(h) == 1 << 32
+    if not flags:  # a chain that streams f32: the rounding-tested forms
+        assert h[0] == 1 << 32, f"node {node}: {(1 << 32) - h[0]} inputs differ from the precise kernel"
     assert h[0] / (1 << 32) > 0.95, f"node {node}: only {h[0] / (1 << 32):.4f} identical to the precise form"
     if not candidates:
         return

@@ -4,7 +4,7 @@ evaluator (CPUKernel.Run, codegen/cpu.go:59-214).
 Each seed draws a random FusionAST over every node type, 1-3 inputs in
 f32/bf16/f16 storage as full, periodic (a repeating row) or scalar operands,
 an element count that exercises the vector loop, its scalar tail or the
-element loop alone, and buffers that may be misaligned by one element.  Two
+element loop alone, and buffers that may be misaligned by one element.  Three
 classes of chain, each with a property that holds for every element:
 
 1. Default flags (the fast Sigmoid/Silu/Gelu forms and the cancellation
@@ -20,6 +20,9 @@ classes of chain, each with a property that holds for every element:
    The device's f64 exp/log/tanh and the oracle's libm may round the last
    f64 bit differently; that changes the f32 result in about 2^-29 of
    evaluations, so up to 1e-4 of a chain's elements may differ.
+3. Default flags, f32 output (a chain that streams f32), any chain: the
+   activations take their rounding-tested forms, the reference's values, so
+   the same property as class 2 holds.
 
 Exp/Log/Tanh run the reference's f64 form in every mode.  Gelu's input goes
 through Max(., -4.5): below -4.9 the reference's 1 + tanh(inner) cancels in
@@ -172,8 +175,20 @@ def test_fast_forms_within_one_storage_ulp(gpu, seed):
 @pytest.mark.parametrize("seed", range(200, 232))
 def test_precise_forms_match_the_reference(gpu, seed):
     case = random_case(seed, -1, DTYPES)
-    out_dt = case[-1]
     got, want = run_case(*case, M.FUSION_PRECISE, seed)
+    assert_reference_bits(got, want, case[-1], seed)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(300, 332))
+def test_chains_that_stream_f32_match_the_reference(gpu, seed):
+    case = random_case(seed, -1, [O.FLOAT32])
+    got, want = run_case(*case, 0, seed)
+    assert_reference_bits(got, want, case[-1], seed)
+
+
+def assert_reference_bits(got, want, out_dt, seed):
+    """Bit-identical but for f64 last-bit differences of exp/log/tanh."""
     bits = np.uint32 if out_dt == O.FLOAT32 else np.uint16
     gb, wb = got.view(bits), want.view(bits)
     gn, wn = nan_mask(gb, out_dt), nan_mask(wb, out_dt)
