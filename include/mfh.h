@@ -203,7 +203,7 @@ typedef struct {
  * without it Sigmoid/Silu/Gelu use f32 algorithms within 2 ulp.  Sigmoid,
  * Silu and Gelu take f64 forms about twice as cheap as the reference's, whose
  * result is used where a test shows that it rounds to the same f32 as the
- * reference's value; the elements the test cannot decide (about one in 2^12)
+ * reference's value; the elements the test cannot decide (about one in 2^13)
  * are recomputed with the reference's formulas. */
 #define MFH_FUSION_PRECISE 1u
 

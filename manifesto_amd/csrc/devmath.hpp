@@ -311,23 +311,23 @@ MFH_MATH double mfh_gelu_z(float c, double& den)
 
 // Rounding-tested forms (chains that stream f32, MFH_FUSION_PRECISE kernels,
 // and the recomputation of flagged elements below): mfh_<name>_cr(v, rare)
-// returns the f32 rounding
-// of the reference's f64 value wherever it leaves `rare` unset, at about two
-// thirds of the instructions of the reference form.  It computes
-// the f64 value z as the forms above do (2^f by the degree-8 polynomial,
-// 2^-39.9; the reciprocal and one Newton step; the argument's own rounding
-// below 2^-45), within 2^-39.7 of the exact function, relative.  The
-// reference's f64 value (correctly rounded division, exp within 1 ulp) lies
-// within 2^-50 of it, and so does the reference form mfh_<name>_ref; gelu
-// adds the quantum of the reference's 1 - (1 - y) (below).  Two values that
-// close to each other round to the same f32 unless an f32 rounding midpoint
-// lies between them: z is flagged where its 29 bits below the f32 mantissa
-// lie within `margin` f64 ulps of the midpoint 2^28, with a margin of 2^15
-// f64 ulps, at least 2^-38 |z| (three times the distance allowed), so about
-// one element in 2^12 is flagged.  So are results that are not normal f32
-// numbers (the test assumes f32 keeps 23 bits above those 29) and arguments
-// outside a form's range.  Generated kernels recompute flagged elements with
-// the reference forms, so the results are the reference forms' everywhere.
+// returns the f32 rounding of the reference's f64 value wherever it leaves
+// `rare` unset, at about two thirds of the instructions of the reference
+// form.  It computes the f64 value z as the forms above do (2^f by the
+// degree-8 polynomial, 2^-39.9; the reciprocal and one Newton step; the
+// argument's own rounding below 2^-45), within 2^-39.7 of the exact
+// function, relative.  The reference's f64 value (correctly rounded
+// division, exp within 1 ulp) lies within 2^-50 of it, and so does the
+// reference form mfh_<name>_ref; gelu adds the quantum of the reference's
+// 1 - (1 - y) (below).  Two values that close to each other round to the
+// same f32 unless an f32 rounding midpoint lies between them: z is flagged
+// where its 29 bits below the f32 mantissa lie within `margin` f64 ulps of
+// the midpoint 2^28, with a margin of 2^15 f64 ulps, at least 2^-38 |z|
+// (three times the distance allowed), so about one element in 2^13 is
+// flagged.  So are results that are not normal f32 numbers (the test
+// assumes f32 keeps 23 bits above those 29) and arguments outside a form's
+// range.  Generated kernels recompute flagged elements through
+// mfh_<name>_rare, so the results are the reference forms' everywhere.
 
 // True where a value within `margin` f64 ulps of z may round to another f32
 // than z does.  z must round to a normal f32 of magnitude above 2^-126.
