@@ -199,12 +199,14 @@ typedef struct {
 } mfh_operand;
 
 /* Transcendental nodes evaluated in f64 exactly as codegen/cpu.go:172-200
- * writes them (bit-identical to the reference but for f64 rounding ties);
- * without it Sigmoid/Silu/Gelu use f32 algorithms within 2 ulp.  Sigmoid,
- * Silu and Gelu take f64 forms about twice as cheap as the reference's, whose
- * result is used where a test shows that it rounds to the same f32 as the
- * reference's value; the elements the test cannot decide (about one in 2^13)
- * are recomputed with the reference's formulas. */
+ * writes them (bit-identical to the reference but for f64 rounding ties).
+ * Sigmoid, Silu and Gelu take f64 forms with about two thirds of the
+ * reference's instructions, whose result is used where a test shows that it
+ * rounds to the same f32 as the reference's value; the elements the test
+ * cannot decide (about one in 2^13) are recomputed with the reference's
+ * formulas.  Without it, chains that stream f32 take the same forms, and
+ * chains of 16-bit operands f32 Silu and Gelu within 2 ulp and an f64
+ * Sigmoid within 1. */
 #define MFH_FUSION_PRECISE 1u
 
 /* Sigmoid, Silu and Gelu in the fast forms of chains of 16-bit operands in
