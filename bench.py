@@ -203,7 +203,8 @@ class SwiGLU(Workload):
 
     def compile(self, flags=0):
         """The chain's kernel: fast transcendentals, or with
-        MFH_FUSION_PRECISE the reference's f64 forms."""
+        MFH_FUSION_PRECISE the reference's f64 results (rounding-tested
+        f64 forms, the reference's formulas where the test cannot decide)."""
         self.k = self.M.FusedKernel(self.nodes, [(self.M.BFLOAT16, 0, 0)] * 2, self.M.BFLOAT16,
                                     "swiglu_precise" if flags else "swiglu", flags)
 
