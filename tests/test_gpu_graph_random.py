@@ -8,8 +8,10 @@ The ops are the ones whose f32 result is exact or correctly rounded (add,
 sub, mul, div, max, min, neg, abs, relu, sqrt), so every output must match
 to the bit (NaN positions included).  A second set of graphs adds every
 transcendental op the optimizer fuses (exp, log, sigmoid, tanh, swish, gelu,
-leaky_relu), compiled with MFH_FUSION_PRECISE (the reference's f64 forms,
-rounded once), and must match to the bit as well.  Inputs mix storage dtypes and operand
+leaky_relu), compiled with MFH_FUSION_PRECISE (the reference's f64 results,
+rounded once), and must match to the bit as well; so must the same graphs
+over f32 inputs and outputs at default flags, whose kernels all stream f32
+and take the rounding-tested activations.  Inputs mix storage dtypes and operand
 modes (full, a repeating row, a scalar); nodes get random output types;
 outputs include intermediates read later and inputs passed through.  Each
 graph is called three times (plain launches, capture, replay) and, for half
@@ -139,21 +141,22 @@ TRANSCENDENTAL = ["math.exp", "math.log", "activation.sigmoid", "activation.tanh
                   "activation.gelu", "activation.leaky_relu"]
 
 
-def random_graph_transcendental(rng, n, d):
+def random_graph_transcendental(rng, n, d, dtypes=DTYPES, out_types=(0, O.FLOAT32, O.BFLOAT16, O.FLOAT16)):
     """random_graph's shapes and operand modes over every elementwise op the
-    optimizer fuses.  A gelu reads max(x, -4.5): below -4.9 the reference's
+    optimizer fuses, inputs in `dtypes`, node outputs in `out_types` (0: the
+    execution dtype).  A gelu reads max(x, -4.5): below -4.9 the reference's
     own gelu (1 + tanh cancelling in f64) is rounding noise that two correct
     f64 evaluations may place a quantum apart."""
     inputs = {}
     for k in range(int(rng.integers(1, 4))):
         count = [n, d, 1][int(rng.choice(3, p=[0.6, 0.25, 0.15]))]
-        inputs[f"in{k}"] = (DTYPES[int(rng.integers(3))], count)
+        inputs[f"in{k}"] = (dtypes[int(rng.integers(len(dtypes)))], count)
     names = list(inputs)
     nodes = [GraphNode("floor", "math.constant", [], attributes={"value": -4.5})]
     n_nodes = int(rng.integers(3, 11))
     for i in range(n_nodes):
         pick = lambda: names[int(rng.integers(len(names)))]  # noqa: E731
-        out_t = [0, O.FLOAT32, O.BFLOAT16, O.FLOAT16][int(rng.integers(4))]
+        out_t = out_types[int(rng.integers(len(out_types)))]
         r = rng.random()
         if r < 0.45:
             op = TRANSCENDENTAL[int(rng.integers(len(TRANSCENDENTAL)))]
@@ -176,17 +179,31 @@ def random_graph_transcendental(rng, n, d):
 
 @pytest.mark.parametrize("seed", range(12))
 def test_random_transcendental_graph_precise_matches_the_oracle(seed):
-    # MFH_FUSION_PRECISE evaluates every transcendental in the reference's f64
-    # form and rounds once, fused or not: bit-identical to the oracle's
-    # evaluation of the optimised graph, NaN where it is NaN.
-    rng = np.random.default_rng(0x5EED + 300 + seed)
+    # MFH_FUSION_PRECISE gives every transcendental the reference's f64 value
+    # rounded once, fused or not: bit-identical to the oracle's evaluation of
+    # the optimised graph, NaN where it is NaN.
+    check_transcendental_graph(seed, 0x5EED + 300 + seed, M.FUSION_PRECISE, DTYPES,
+                               (0, O.FLOAT32, O.BFLOAT16, O.FLOAT16))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_f32_transcendental_graph_matches_the_oracle_at_default_flags(seed):
+    # f32 inputs and node outputs: every kernel streams f32, so its Sigmoid,
+    # Silu and Gelu take the rounding-tested forms at default flags, and the
+    # graph is bit-identical to the oracle's evaluation as under
+    # MFH_FUSION_PRECISE.
+    check_transcendental_graph(seed, 0x5EED + 400 + seed, 0, [O.FLOAT32], (0, O.FLOAT32))
+
+
+def check_transcendental_graph(seed, rng_seed, flags, dtypes, out_types):
+    rng = np.random.default_rng(rng_seed)
     rows, d = 101, 12
     n = rows * d  # not a multiple of 8: every vector path has a tail
-    inputs, nodes, outputs = random_graph_transcendental(rng, n, d)
+    inputs, nodes, outputs = random_graph_transcendental(rng, n, d, dtypes, out_types)
     graph = Graph(inputs=list(inputs), outputs=outputs, execution_dtype=O.FLOAT32, nodes=nodes)
     G.run(graph)
-    G.attach_kernels(graph, flags=M.FUSION_PRECISE)
-    log(f"transcendental graph {seed}: {[(nd.id, nd.op) for nd in graph.nodes]}")
+    G.attach_kernels(graph, flags=flags)
+    log(f"transcendental graph {seed} (flags {flags}): {[(nd.id, nd.op) for nd in graph.nodes]}")
     data = {}
     for name, (dt, count) in inputs.items():
         a = rng.normal(0, 2, count).astype(np.float32)
