@@ -584,8 +584,8 @@ int emit_hip(const mfh_ast_node* nodes, int n_nodes, const mfh_operand* inputs, 
     // dispatch order).  Measured on MI355X against grid-stride loops at 4-24
     // blocks per CU: +11% on the SwiGLU chain and +9% on the f16 gelu chain;
     // a no-compute 2:1 read:write stream gains 17% the same way.  One item per
-    // thread, except where the element math is mostly f64 (Sigmoid, the f64
-    // forms of chains that stream f32, the rounding-tested forms of
+    // thread, except where the element math is mostly f64 (Sigmoid, and the
+    // rounding-tested forms of chains that stream f32 and of
     // MFH_FUSION_PRECISE): two items per thread give a sigmoid chain 0-3% and
     // the precise SwiGLU chain 5.6% (the precise gelu chain -1%, within the
     // noise of six alternating runs), while SwiGLU, Silu, add/mul chains and
