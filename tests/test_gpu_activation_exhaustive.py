@@ -6,7 +6,7 @@ the three activations in their rounding-tested forms, which must give the
 precise kernel's bit pattern on every input.  The forms 16-bit chains use
 (f32 Silu and Gelu with the rounding of 1 + E left in the quotient, the f64
 Sigmoid without a rounding test) run here through MFH_FUSION_SHORT_QUOTIENT.
-The precise kernels, which give the reference's f64 formulas
+The precise kernels, which give the values of the reference's f64 formulas
 (codegen/cpu.go:186-200) rounded once, are within one f32 ulp of the oracle
 (they differ only where an f64 result sits at an f32 rounding tie that two
 f64 libraries round differently).  NaN positions must match.  Every input
